@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized matmul hot path on one MI355X.
+
+Headline workload: one LFM2-1.2B-shaped decode step run as weight-only INT8 GEMVs -- 16 layers typed
+C C A C C A C C A C A C A C A C (6 attention, 10 short-conv), per attention layer qkv [3072x2048] and o [2048x2048]
+(+residual), per conv layer in_proj [6144x2048] and out_proj [2048x2048] (+residual), per layer w1|w3 [16384x2048]
+(+SwiGLU) and w2 [2048x8192] (+residual), then lm_head [65536x2048]. Every layer has its own weights (1.17 GB of
+INT8 per step, so the 256 MB MALL cannot hold them). The 113 launches of one step are captured into a HIP graph;
+a "step" is one replay. value = algorithmic bytes of the step / step time (GB/s), at batch 1; batches 4 and 16 are
+reported alongside. Synthetic data: int8 weights uniform over [-127, 127], scales |N(0,1)| 0.01 + 1e-3, bf16
+activations N(0, 1), seeded.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "lfm2.5-vl-optimization_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import torch  # noqa: E402
+import torch.nn.functional as F  # noqa: E402
+
+METRIC = "W8 GEMV HBM GB/s (% of peak) + W8A8 GEMM int8 TOPS (% MFMA) at LFM2 shapes"
+HBM_PEAK_GBS = 8000.0
+LAYER_TYPES = "CCACCACCACACACAC"  # LFM2-1.2B layer order (A = attention, C = gated short conv)
+H, FFN, VOCAB, QKV, CONV_IN = 2048, 8192, 65536, 3072, 6144
+
+
+def gemv_bytes(N, K, B, residual=False):
+    """Algorithmic bytes of one weight-only INT8 GEMV: W, scale, x and y once each (+ the residual read)."""
+    return N * K + 4 * N + 2 * B * K + 2 * B * N + (2 * B * N if residual else 0)
+
+
+def swiglu_bytes(S, K, B):
+    return 2 * S * K + 4 * 2 * S + 2 * B * K + 2 * B * S
+
+
+class DecodeStep:
+    """All GEMVs of one decode step with distinct weights per layer, as a list of zero-argument launches."""
+
+    def __init__(self, B, device, seed=0):
+        from lfm2opt.kernels import ext
+
+        E = ext()
+        g = torch.Generator(device=device).manual_seed(seed)
+        bf = torch.bfloat16
+
+        def w8(N, K):
+            W = torch.randint(-127, 128, (N, K), device=device, dtype=torch.int8, generator=g)
+            s = torch.rand(N, device=device, generator=g) * 0.01 + 1e-3
+            return W, s
+
+        self.x = torch.randn(B, H, device=device, generator=g).to(bf)       # normed residual stream
+        self.mix = torch.randn(B, H, device=device, generator=g).to(bf)     # attention / conv output
+        self.h = torch.randn(B, H, device=device, generator=g).to(bf)       # residual stream (updated in place)
+        self.qkv = torch.empty(B, QKV, device=device, dtype=bf)
+        self.bcx = torch.empty(B, CONV_IN, device=device, dtype=bf)
+        self.act = torch.empty(B, FFN, device=device, dtype=bf)
+        self.logits = torch.empty(B, VOCAB, device=device, dtype=bf)
+        self.ops = []      # (kind, fn, bytes)
+        self.weights = []  # keep alive
+        for t in LAYER_TYPES:
+            if t == "A":
+                Wq, sq = w8(QKV, H)
+                Wo, so = w8(H, H)
+                self.ops.append(("qkv", lambda W=Wq, s=sq: E.gemv(W, s, self.x, self.qkv), gemv_bytes(QKV, H, B)))
+                self.ops.append(("o+res", lambda W=Wo, s=so: E.gemv_residual(W, s, self.mix, self.h),
+                                 gemv_bytes(H, H, B, True)))
+                self.weights += [Wq, sq, Wo, so]
+            else:
+                Wi, si = w8(CONV_IN, H)
+                Wc, sc = w8(H, H)
+                self.ops.append(("in", lambda W=Wi, s=si: E.gemv(W, s, self.x, self.bcx), gemv_bytes(CONV_IN, H, B)))
+                self.ops.append(("out+res", lambda W=Wc, s=sc: E.gemv_residual(W, s, self.mix, self.h),
+                                 gemv_bytes(H, H, B, True)))
+                self.weights += [Wi, si, Wc, sc]
+            W13, s13 = w8(2 * FFN, H)
+            W2, s2 = w8(H, FFN)
+            self.ops.append(("w1|w3+swiglu", lambda W=W13, s=s13: E.gemv_epi(0, W, s, self.x, self.act),
+                             swiglu_bytes(FFN, H, B)))
+            self.ops.append(("w2+res", lambda W=W2, s=s2: E.gemv_residual(W, s, self.act, self.h),
+                             gemv_bytes(H, FFN, B, True)))
+            self.weights += [W13, s13, W2, s2]
+        Wh, sh = w8(VOCAB, H)
+        self.ops.append(("lm_head", lambda: E.gemv(Wh, sh, self.x, self.logits), gemv_bytes(VOCAB, H, B)))
+        self.weights += [Wh, sh]
+        self.bytes = sum(b for _, _, b in self.ops)
+        self.weight_bytes = sum(w.numel() * w.element_size() for w in self.weights if w.dtype == torch.int8)
+
+    def run(self, kinds=None):
+        for kind, fn, _ in self.ops:
+            if kinds is None or kind in kinds:
+                fn()
+
+
+def capture(fn):
+    """Capture fn's launches (all on torch's current stream) into a HIP graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # eager warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, reps, warmup):
+    """ms per replay over `reps` back-to-back replays, bracketed by synchronizations (HIP events on the stream)."""
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    t0.record()
+    for _ in range(reps):
+        graph.replay()
+    t1.record()
+    t1.synchronize()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - w0) * 1e3 / reps
+    return t0.elapsed_time(t1) / reps, wall
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(budget_s=10.0):
+    """The reference's PyTorch dequant-matmul (tests/test_kernels.py:137, restated in oracle/cpu_baseline.py) over
+    one decode step's worth of distinct GEMV shapes at batch 1, repeated until ~budget_s of CPU work."""
+    from oracle.cpu_baseline import gemv_w8_dequant_matmul
+
+    torch.set_num_threads(torch.get_num_threads())
+    g = torch.Generator().manual_seed(0)
+    shapes = [(QKV, H), (H, H), (CONV_IN, H), (2 * FFN, H), (H, FFN), (VOCAB, H)]
+    mats = []
+    for N, K in shapes:
+        W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+        s = torch.rand(N, generator=g) * 0.01 + 1e-3
+        x = torch.randn(1, K, generator=g).to(torch.bfloat16)
+        mats.append((W, s, x))
+    nbytes = sum(gemv_bytes(N, K, 1) for N, K in shapes)
+    for W, s, x in mats:  # warm-up
+        gemv_w8_dequant_matmul(W, s, x)
+    times, t_start = [], time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        for W, s, x in mats:
+            gemv_w8_dequant_matmul(W, s, x)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"one each of the 6 decode GEMV shapes (qkv, o/out, in, w1|w3, w2, lm_head), batch 1, "
+                      f"{nbytes / 1e6:.1f} MB per pass, median of {len(times)} passes; "
+                      f"F.linear(x.float(), Wq.float() * scale[:, None]).to(bf16) with the dequant inside the "
+                      f"timed region; os.cpu_count()={os.cpu_count()}, cpu='{cpu_model()}'"}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_results(B, steps, warmup):
+    log(f"decode step, batch {B}: allocating weights")
+    step = DecodeStep(B, "cuda")
+    graph = capture(step.run)
+    ms, wall = time_graph(graph, steps, warmup)
+    res = {"batch": B, "ms_per_step": ms, "wall_ms_per_step": wall, "bytes_per_step": step.bytes,
+           "gbs": step.bytes / ms / 1e6, "hbm_frac": step.bytes / ms / 1e6 / HBM_PEAK_GBS, "launches": len(step.ops)}
+    # per-kind breakdown: each kind's launches alone, graph-captured, back to back
+    kinds = {}
+    for kind in dict.fromkeys(k for k, _, _ in step.ops):
+        g = capture(lambda kind=kind: step.run({kind}))
+        n = sum(1 for k, _, _ in step.ops if k == kind)
+        kb = sum(b for k, _, b in step.ops if k == kind)
+        kms, _ = time_graph(g, max(5, steps // 4), 3)
+        kinds[kind] = {"launches": n, "us_per_launch": round(kms * 1e3 / n, 2), "gbs": round(kb / kms / 1e6, 1),
+                       "bytes_per_launch": kb // n}
+        del g
+    res["kinds"] = kinds
+    log(f"decode step, batch {B}: {ms * 1e3:.1f} us/step, {res['gbs']:.0f} GB/s")
+    del graph, step
+    torch.cuda.empty_cache()
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    res1 = decode_results(1, args.steps, args.warmup)
+    extra = {B: decode_results(B, max(20, args.steps // 2), args.warmup) for B in (4, 16)}
+    dom = res1["kinds"]["w1|w3+swiglu"]
+    out = {
+        "metric": METRIC,
+        "value": round(res1["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "LFM2-1.2B decode step as weight-only INT8 GEMVs: 16 layers (6 attention, 10 "
+                               "short-conv) + lm_head, 113 launches in one HIP graph, batch 1",
+                   "batch": 1, "hidden": H, "ffn": FFN, "vocab": VOCAB, "bytes_per_step": res1["bytes_per_step"],
+                   "compute": "int8 weights x bf16 activations, fp32 accumulation, bf16 out",
+                   "parallelism": "single GPU"},
+        "hbm_frac": round(res1["hbm_frac"], 4),
+        "roofline": {"bound": "hbm", "kernel": "gemv_b1_kernel<int8,1,2,SWIGLU> (w1|w3 16384x2048 + SwiGLU)",
+                     "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "us_per_launch": dom["us_per_launch"], "bytes_per_launch": dom["bytes_per_launch"]},
+        "decode": {str(B): r for B, r in [(1, res1)] + list(extra.items())},
+    }
+    if not args.no_cpu:
+        log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,82 @@
+/* liblfm2q: the quantized matrix-multiply hot path of the LFM2.5-VL inference stack, as hand-written gfx950
+ * (MI355X) kernels behind a C ABI.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensors are row-major and contiguous, in device memory; the caller owns every buffer. No entry point
+ *     allocates, synchronizes or reads device memory on the host.
+ *   - bf16 tensors are passed as their raw 16-bit patterns (lfm2q_bf16 = uint16_t).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and runs asynchronously.
+ *   - The return value is a status: LFM2Q_OK (0) or one of the error codes below, in which case nothing was
+ *     launched and lfm2q_last_error() returns a message for the calling thread. Argument errors are detected
+ *     before any launch; LFM2Q_ERR_LAUNCH reports a failed kernel launch (hipGetLastError).
+ *
+ * Reference interfaces: the raw-pointer launchers of kernels/lfm2_decode.cu and kernels/int8_gemm.cu and the
+ * pybind11 functions of kernels/lfm2_decode.cpp and kernels/int8_gemm.cpp (paths relative to the reference
+ * repository). Each declaration cites the one it replaces.
+ */
+#ifndef LFM2Q_H
+#define LFM2Q_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t lfm2q_bf16;
+typedef void *lfm2q_stream_t; /* hipStream_t */
+
+enum {
+    LFM2Q_OK = 0,
+    LFM2Q_ERR_ARG = 1,     /* null pointer, bad enum value */
+    LFM2Q_ERR_SHAPE = 2,   /* sizes out of range or not multiples of what the kernel needs */
+    LFM2Q_ERR_ALIGN = 3,   /* a pointer is not aligned to 16 bytes */
+    LFM2Q_ERR_LAUNCH = 4,  /* the kernel launch failed */
+    LFM2Q_ERR_DEVICE = 5   /* no usable device / device query failed */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *lfm2q_last_error(void);
+/* Library version string. */
+const char *lfm2q_version(void);
+
+/* ------------------------------------------------------------------------------------------ decode GEMVs */
+
+/* Weight-only INT8 GEMV: y[b, n] = bf16( (sum_k W[n, k] * x[b, k]) * scale[n] ).
+ * W int8 [N, K], scale fp32 [N], x bf16 [B, K], y bf16 [B, N]; B >= 1, K % 64 == 0.
+ * rows: output rows per wavefront for B == 1 (1, 2 or 4; 0 = automatic), ignored otherwise.
+ * Replaces launch_gemv(W, int8 = true, ...) kernels/lfm2_decode.cu:708-714 (bound as gemv(),
+ * kernels/lfm2_decode.cpp:74-85). */
+int lfm2q_gemv_w8(const int8_t *W, const float *scale, const lfm2q_bf16 *x, lfm2q_bf16 *y, int B, int N, int K,
+                  int rows, lfm2q_stream_t stream);
+
+/* BF16-weight GEMV: y[b, n] = bf16( (sum_k W[n, k] * x[b, k]) * (scale ? scale[n] : 1) ).
+ * W bf16 [N, K]; same shapes and rules as lfm2q_gemv_w8.
+ * Replaces launch_gemv(W, int8 = false, ...) kernels/lfm2_decode.cu:708-714. */
+int lfm2q_gemv_bf16(const lfm2q_bf16 *W, const float *scale, const lfm2q_bf16 *x, lfm2q_bf16 *y, int B, int N,
+                    int K, int rows, lfm2q_stream_t stream);
+
+/* GEMV over the stacked w1|w3 weight W [2S, K] with the SwiGLU epilogue fused:
+ *   g = bf16(acc[b, n] * s[n]), u = bf16(acc[b, S + n] * s[S + n]), y[b, n] = bf16( bf16(silu(g)) * u ).
+ * wtype 0: W int8 (scale required); wtype 1: W bf16 (scale optional). y bf16 [B, S]; any B >= 1.
+ * Bit-identical to the plain GEMV followed by lfm2q_silu_mul on the same inputs.
+ * Replaces gemv_epi(0, ...) kernels/lfm2_decode.cpp:130-150 / gemv_epi_kernel<WT, 2, 0>
+ * kernels/lfm2_decode.cu:724-805 (which is batch 1 only). */
+int lfm2q_gemv_swiglu(int wtype, const void *W, const float *scale, const lfm2q_bf16 *x, lfm2q_bf16 *y, int B,
+                      int S, int K, lfm2q_stream_t stream);
+
+/* GEMV with the residual add fused: h[b, n] = bf16( h[b, n] + bf16(acc[b, n] * s[n]) ), h bf16 [B, N] in place.
+ * Bit-identical to the plain GEMV followed by the residual add of add_rmsnorm (kernels/lfm2_decode.cu:108-113).
+ * No counterpart kernel in the reference (there it is the separate add_rmsnorm launch). */
+int lfm2q_gemv_residual(int wtype, const void *W, const float *scale, const lfm2q_bf16 *x, lfm2q_bf16 *h, int B,
+                        int N, int K, lfm2q_stream_t stream);
+
+/* y[b, i] = bf16( bf16(silu(g[b, i])) * g[b, I + i] ), g bf16 [B, 2I], y bf16 [B, I].
+ * Replaces launch_silu_mul kernels/lfm2_decode.cu:954-969 (bound as silu_mul(), kernels/lfm2_decode.cpp:100-103). */
+int lfm2q_silu_mul(const lfm2q_bf16 *g, lfm2q_bf16 *y, int B, int I, lfm2q_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LFM2Q_H */

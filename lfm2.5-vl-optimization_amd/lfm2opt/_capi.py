@@ -1,0 +1,61 @@
+"""ctypes binding of liblfm2q.so (the C ABI declared in include/lfm2q.h).
+
+torch is imported before the library is opened: the shared object links against libamdhip64.so.7 by SONAME, and
+loading it after torch makes it use the HIP runtime torch already loaded, so the hipStream_t handles torch hands out
+are valid in the library. There is no fallback: if the library is missing, every op raises.
+"""
+
+import ctypes
+import pathlib
+
+import torch  # noqa: F401  (must precede the dlopen below, see module docstring)
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent.parent / "lib" / "liblfm2q.so"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+
+# name -> argument types (every entry point returns an int status)
+SIGNATURES = {
+    "lfm2q_gemv_w8": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "lfm2q_gemv_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "lfm2q_gemv_swiglu": [_I, _P, _P, _P, _P, _I, _I, _I, _P],
+    "lfm2q_gemv_residual": [_I, _P, _P, _P, _P, _I, _I, _I, _P],
+    "lfm2q_silu_mul": [_P, _P, _I, _I, _P],
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"liblfm2q.so is not built ({LIB_PATH}); build it with "
+                               f"`make -C lfm2.5-vl-optimization_amd/csrc` or __graft_entry__.build()")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.lfm2q_last_error.restype = ctypes.c_char_p
+        L.lfm2q_last_error.argtypes = []
+        L.lfm2q_version.restype = ctypes.c_char_p
+        L.lfm2q_version.argtypes = []
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes, fn.restype = args, ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def call(name, *args):
+    """Call entry point `name`; a non-zero status becomes RuntimeError with the library's message."""
+    st = getattr(lib(), name)(*args)
+    if st != 0:
+        raise RuntimeError(lib().lfm2q_last_error().decode())
+
+
+def stream(t):
+    """Raw hipStream_t of torch's current stream on t's device (the reference launches on the same stream)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,143 @@
+"""Extension entry points with the reference's Python surface, backed by the gfx950 library liblfm2q.so.
+
+`ext()` stands in for the JIT-built decode extension and `int8_ext()` for the INT8 GEMM extension of
+src/lfm2opt/kernels.py:16-32,66-68. The ops keep their names, argument order and meaning, destination-passing
+style (every output is preallocated by the caller, ops return None) and launch on torch's current stream. Argument
+errors raise RuntimeError with the reference's TORCH_CHECK wording (kernels/lfm2_decode.cpp:28-150) before any
+launch. Ops outside the quantized-matmul path (attention, norms, convolutions) are not provided.
+"""
+
+import os
+
+import torch
+
+from . import _capi
+
+_EXT = None
+
+
+def _check_bf16(t, name):
+    if not (t.is_cuda and t.dtype == torch.bfloat16 and t.is_contiguous()):
+        raise RuntimeError(f"{name} must be contiguous CUDA bf16")
+
+
+def _check_t(t, dtype, name):
+    if not (t.is_cuda and t.dtype == dtype and t.is_contiguous()):
+        raise RuntimeError(f"{name} must be contiguous CUDA {dtype}")
+
+
+def _same_device(*ts):
+    dev = ts[0].device
+    for t in ts[1:]:
+        if t is not None and t.device != dev:
+            raise RuntimeError("all tensors must be on the same device")
+
+
+class DecodeOps:
+    """Decode-path ops (reference: kernels/lfm2_decode.cpp)."""
+
+    def __init__(self):
+        _capi.lib()
+        self.pdl = True
+        self.gemv_impl = 1
+
+    # ---- reference ops ------------------------------------------------------------------------------------
+    def gemv(self, W, scale, x, y, rows=0):
+        """y [B, N] = x [B, K] @ W^T, W [N, K] bf16 or int8 (then scale [N] fp32 is required); any B >= 1.
+        Reference: gemv(), kernels/lfm2_decode.cpp:74-85. rows: output rows per wavefront for B == 1."""
+        _check_bf16(x, "x")
+        _check_bf16(y, "y")
+        if not (W.is_cuda and W.is_contiguous() and W.dim() == 2):
+            raise RuntimeError("W must be a contiguous CUDA matrix")
+        int8 = W.dtype == torch.int8
+        if not (int8 or W.dtype == torch.bfloat16):
+            raise RuntimeError("W must be bf16 or int8")
+        if int8 and (scale is None or scale.dtype != torch.float32):
+            raise RuntimeError("int8 W needs fp32 scale")
+        N, K = W.shape
+        B = x.numel() // K if K else 0
+        if not (B >= 1 and x.numel() == B * K and y.numel() == B * N):
+            raise RuntimeError("x [B, K], y [B, N]")
+        if scale is not None:
+            _check_t(scale, torch.float32, "scale")
+            if scale.numel() != N:
+                raise RuntimeError("scale must have N elements")
+        _same_device(W, x, y, scale)
+        fn = "lfm2q_gemv_w8" if int8 else "lfm2q_gemv_bf16"
+        _capi.call(fn, W.data_ptr(), _capi.ptr(scale), x.data_ptr(), y.data_ptr(), B, N, K, int(rows),
+                   _capi.stream(x))
+
+    def gemv_epi(self, epi, W, scale, x, y, state=None, cw=None, cbias=None):
+        """epi 0: W = w1|w3 [2S, K] -> y [B, S] = silu(w1 x) * (w3 x), fused into the GEMV.
+        Reference: gemv_epi(), kernels/lfm2_decode.cpp:130-150 (batch 1 there; any B >= 1 here). epi 1 (the LFM2
+        short-conv step) is not a matmul epilogue and is not provided by this library."""
+        if epi != 0:
+            if epi == 1:
+                raise RuntimeError("gemv_epi: epi 1 (short-conv step) is outside the quantized-matmul library")
+            raise RuntimeError("epi 0 (swiglu) or 1 (shortconv)")
+        W, scale, B, S, K, wtype = self._epi_args(W, scale, x, y, rows_per_out=2)
+        _capi.call("lfm2q_gemv_swiglu", wtype, W.data_ptr(), _capi.ptr(scale), x.data_ptr(), y.data_ptr(), B, S, K,
+                   _capi.stream(x))
+
+    def silu_mul(self, g, y):
+        """y = silu(a) * b on g = [a | b]; reference: silu_mul(), kernels/lfm2_decode.cpp:100-103."""
+        _check_bf16(g, "g")
+        _check_bf16(y, "y")
+        I2 = g.size(-1)
+        B = g.numel() // I2
+        if I2 % 2 or y.numel() != B * (I2 // 2):
+            raise RuntimeError("g [B, 2I], y [B, I]")
+        _same_device(g, y)
+        _capi.call("lfm2q_silu_mul", g.data_ptr(), y.data_ptr(), B, I2 // 2, _capi.stream(g))
+
+    def set_pdl(self, on):
+        """Accepted for compatibility (kernels/lfm2_decode.cpp:165); HIP has no programmatic dependent launch,
+        back-to-back kernels on one stream are ordered by the stream and captured into HIP graphs instead."""
+        self.pdl = bool(on)
+
+    def set_gemv_impl(self, impl):
+        """Accepted for compatibility (kernels/lfm2_decode.cpp:166): there is one GEMV implementation per batch
+        size class here, so the choice between shared-memory and direct activation loads has no effect."""
+        if impl not in (0, 1):
+            raise RuntimeError("GEMV implementation: 0 = x staged in shared memory, 1 = direct x loads")
+        self.gemv_impl = int(impl)
+
+    # ---- additions ----------------------------------------------------------------------------------------
+    def gemv_residual(self, W, scale, x, h):
+        """h [B, N] += bf16(x @ W^T * scale) in place, rounded as the reference's residual add
+        (kernels/lfm2_decode.cu:108-113): h = bf16(h + bf16(acc * s))."""
+        W, scale, B, N, K, wtype = self._epi_args(W, scale, x, h, rows_per_out=1)
+        _capi.call("lfm2q_gemv_residual", wtype, W.data_ptr(), _capi.ptr(scale), x.data_ptr(), h.data_ptr(), B, N,
+                   K, _capi.stream(x))
+
+    def _epi_args(self, W, scale, x, y, rows_per_out):
+        _check_bf16(x, "x")
+        _check_bf16(y, "y")
+        if not (W.is_cuda and W.is_contiguous() and W.dim() == 2):
+            raise RuntimeError("W must be a contiguous CUDA matrix")
+        int8 = W.dtype == torch.int8
+        if not (int8 or W.dtype == torch.bfloat16):
+            raise RuntimeError("W must be bf16 or int8")
+        if int8 and (scale is None or scale.dtype != torch.float32):
+            raise RuntimeError("int8 W needs fp32 scale")
+        Nw, K = W.shape
+        Nout = Nw // rows_per_out
+        B = x.numel() // K if K else 0
+        if not (Nw == rows_per_out * Nout and B >= 1 and x.numel() == B * K and y.numel() == B * Nout):
+            raise RuntimeError("x [B, K], y [B, N]" if rows_per_out == 1 else "x [B, K], W [2S, K], y [B, S]")
+        if scale is not None:
+            _check_t(scale, torch.float32, "scale")
+            if scale.numel() != Nw:
+                raise RuntimeError("scale must have one element per row of W")
+        _same_device(W, x, y, scale)
+        return W, scale, B, Nout, K, 0 if int8 else 1
+
+
+def ext():
+    """The decode-op extension (reference: src/lfm2opt/kernels.py:16-32). LFM2_PDL is read like the reference
+    does; it has no effect on HIP."""
+    global _EXT
+    if _EXT is None:
+        _EXT = DecodeOps()
+        _EXT.set_pdl(os.environ.get("LFM2_PDL", "1") != "0")
+    return _EXT

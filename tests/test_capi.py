@@ -1,0 +1,77 @@
+"""The C ABI without a GPU: liblfm2q.so loads, exports every function include/lfm2q.h declares, the ctypes table
+matches the header, and argument errors come back as status codes (no kernel is launched for them)."""
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "lfm2q.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(lfm2q_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from lfm2opt import _capi
+
+    return _capi.lib()
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "lfm2q_gemv_w8" in names and "lfm2q_last_error" in names
+
+
+def test_library_exports_every_declared_symbol(L):
+    missing = [n for n in declared() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_ctypes_table_matches_header():
+    from lfm2opt import _capi
+
+    assert sorted(_capi.SIGNATURES) == sorted(set(declared()) - {"lfm2q_last_error", "lfm2q_version"})
+
+
+def test_version(L):
+    assert L.lfm2q_version().decode().startswith("lfm2q")
+
+
+def test_status_codes_without_launch(L):
+    """Shape and pointer checks run on the host and return before any HIP call that launches work."""
+    from lfm2opt import _capi
+
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails its argument check first
+    assert _capi.lib().lfm2q_gemv_w8(None, None, None, None, 1, 64, 512, 0, None) == 1  # null pointers
+    assert "null pointer" in L.lfm2q_last_error().decode()
+    assert L.lfm2q_gemv_w8(fake, None, fake, fake, 1, 64, 512, 0, None) == 1  # int8 without scale
+    assert L.lfm2q_gemv_w8(fake, fake, fake, fake, 1, 64, 96, 0, None) == 2  # K % 64
+    assert "multiple of 64" in L.lfm2q_last_error().decode()
+    assert L.lfm2q_gemv_w8(fake, fake, fake, fake, 0, 64, 512, 0, None) == 2  # B = 0
+    assert L.lfm2q_gemv_w8(ctypes.c_void_p(0x1001), fake, fake, fake, 1, 64, 512, 0, None) == 3  # misaligned
+    assert L.lfm2q_gemv_swiglu(2, fake, fake, fake, fake, 1, 64, 512, None) == 1  # bad wtype
+    assert L.lfm2q_silu_mul(None, fake, 1, 8, None) == 1
+
+
+def test_python_checks_match_reference_wording():
+    """The torch-facing layer raises RuntimeError with the reference's TORCH_CHECK text before reaching the C ABI
+    (kernels/lfm2_decode.cpp:28-85); CPU tensors are rejected as non-CUDA."""
+    import torch
+    from lfm2opt.kernels import ext
+
+    E = ext()
+    W = torch.zeros(64, 512, dtype=torch.int8)
+    x = torch.zeros(1, 512, dtype=torch.bfloat16)
+    y = torch.zeros(1, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="must be contiguous CUDA bf16"):
+        E.gemv(W, torch.ones(64), x, y)
+    with pytest.raises(RuntimeError, match="GEMV implementation"):
+        E.set_gemv_impl(3)
+    E.set_pdl(False)
+    E.set_gemv_impl(0)
