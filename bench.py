@@ -5,7 +5,7 @@ Headline workload: one LFM2-1.2B-shaped decode step run as weight-only INT8 GEMV
 C C A C C A C C A C A C A C A C (6 attention, 10 short-conv), per attention layer qkv [3072x2048] and o [2048x2048]
 (+residual), per conv layer in_proj [6144x2048] and out_proj [2048x2048] (+residual), per layer w1|w3 [16384x2048]
 (+SwiGLU) and w2 [2048x8192] (+residual), then lm_head [65536x2048]. Every layer has its own weights (1.17 GB of
-INT8 per step, so the 256 MB MALL cannot hold them). The 113 launches of one step are captured into a HIP graph;
+INT8 per step, so the 256 MB MALL cannot hold them). The 65 launches of one step are captured into a HIP graph;
 a "step" is one replay. value = algorithmic bytes of the step / step time (GB/s), at batch 1; batches 4 and 16 are
 reported alongside. Synthetic data: int8 weights uniform over [-127, 127], scales |N(0,1)| 0.01 + 1e-3, bf16
 activations N(0, 1), seeded.
@@ -210,14 +210,16 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--batches", default="1,4,16", help="decode batch sizes to run (the first one is `value`)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
 
-    res1 = decode_results(1, args.steps, args.warmup)
-    extra = {B: decode_results(B, max(20, args.steps // 2), args.warmup) for B in (4, 16)}
+    batches = [int(b) for b in args.batches.split(",")]
+    res1 = decode_results(batches[0], args.steps, args.warmup)
+    extra = {B: decode_results(B, max(20, args.steps // 2), args.warmup) for B in batches[1:]}
     dom = res1["kinds"]["w1|w3+swiglu"]
     out = {
         "metric": METRIC,
@@ -233,7 +235,7 @@ def main():
         "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "LFM2-1.2B decode step as weight-only INT8 GEMVs: 16 layers (6 attention, 10 "
-                               "short-conv) + lm_head, 113 launches in one HIP graph, batch 1",
+                               "short-conv) + lm_head, 65 launches in one HIP graph, batch 1",
                    "batch": 1, "hidden": H, "ffn": FFN, "vocab": VOCAB, "bytes_per_step": res1["bytes_per_step"],
                    "compute": "int8 weights x bf16 activations, fp32 accumulation, bf16 out",
                    "parallelism": "single GPU"},
@@ -242,7 +244,7 @@ def main():
                      "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
                      "us_per_launch": dom["us_per_launch"], "bytes_per_launch": dom["bytes_per_launch"]},
-        "decode": {str(B): r for B, r in [(1, res1)] + list(extra.items())},
+        "decode": {str(B): r for B, r in [(batches[0], res1)] + list(extra.items())},
     }
     if not args.no_cpu:
         log("cpu baseline")

@@ -28,23 +28,57 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }  // round to bf16 and back
 
-// Sum over the 64 lanes of a wave; every lane receives the total. The butterfly order is fixed, so the result is
-// a deterministic function of the 64 inputs (kernels that must agree bit for bit share this routine).
+// DPP lane permutations within a 16-lane row (no LDS traffic, unlike ds_bpermute).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int DPP_XOR1 = 0xb1;         // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4e;         // quad_perm [2, 3, 0, 1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <- lane 7 - i within each 8 lanes
+constexpr int DPP_MIRROR = 0x140;       // lane i <- lane 15 - i within each 16 lanes
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total. The order is fixed (row sums by DPP, then the
+// four row sums added as (r0 + r1) + (r2 + r3)), so the result is a deterministic function of the 64 inputs:
+// kernels that must agree bit for bit share this routine.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
+    v += dpp<DPP_XOR1>(v);
+    v += dpp<DPP_XOR2>(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    v += dpp<DPP_MIRROR>(v);
+    return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
+    v = fmaxf(v, dpp<DPP_XOR1>(v));
+    v = fmaxf(v, dpp<DPP_XOR2>(v));
+    v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp<DPP_MIRROR>(v));
+    return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
 }
 
 // 16-byte streaming load that does not keep the line in the caches (weights are read exactly once per call).
 __device__ __forceinline__ v4i ld_nt16(const void *p) { return __builtin_nontemporal_load((const v4i *)p); }
 // 16-byte cached load (activations: small and shared by every wave).
 __device__ __forceinline__ v4i ld16(const void *p) { return *(const v4i *)p; }
+
+// Buffer resources (gfx9 descriptor word 3 = 0x00020000): a wavefront-uniform base and byte range held in four
+// SGPRs. Loads through them take a per-lane byte offset, so the address arithmetic of a uniform row base stays
+// scalar, and offsets at or beyond `bytes` read zero.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr int AUX_NT = 2;  // non-temporal (streamed once)
+__device__ __forceinline__ v4i buf_ld16(rsrc_t r, uint32_t voff, int soff = 0) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, soff, 0));
+}
+__device__ __forceinline__ v4i buf_ld16_nt(rsrc_t r, uint32_t voff, int soff = 0) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, soff, AUX_NT));
+}
 
 // SiLU exactly as the decode path rounds it: silu(g) = g / (1 + exp(-g)) in fp32.
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.f + expf(-g)); }

@@ -14,6 +14,12 @@ int launch_status(const char *what);
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Compute units of the current device (queried once per device, then cached; 256 on MI355X).
+int device_cus();
+
+// Integer tuning knob from the environment (read once per name by the caller), or `dflt` when unset.
+int env_int(const char *name, int dflt);
+
 }  // namespace lfm2q
 
 #define LFM2Q_REQUIRE(cond, code, ...)                      \
