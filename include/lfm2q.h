@@ -75,6 +75,27 @@ int lfm2q_gemv_residual(int wtype, const void *W, const float *scale, const lfm2
  * Replaces launch_silu_mul kernels/lfm2_decode.cu:954-969 (bound as silu_mul(), kernels/lfm2_decode.cpp:100-103). */
 int lfm2q_silu_mul(const lfm2q_bf16 *g, lfm2q_bf16 *y, int B, int I, lfm2q_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------ W8A8 GEMM */
+
+/* Per-token activation quantization: s[r] = max(max_k |x[r, k]|, 1e-8) / 127 (IEEE division),
+ * q[r, k] = clamp(rint(x[r, k] / s[r]), -127, 127) with round-half-even. x bf16 [rows, K], q int8 [rows, K],
+ * s fp32 [rows]; K % 8 == 0 (the reference accepts K % 128 == 0 and K <= 2048 only).
+ * Replaces launch_quant_rows kernels/int8_gemm.cu:822-825 (bound as quant_rows(), kernels/int8_gemm.cpp:83-96). */
+int lfm2q_quant_rows(const lfm2q_bf16 *x, int8_t *q, float *s, int rows, int K, lfm2q_stream_t stream);
+
+/* W8A8 GEMM with the dequant epilogue: Y[m, n] = bf16( g( ((float)acc[m, n] * sa[m]) * sb[n] + bias[n] ) ),
+ * acc[m, n] = sum_k A[m, k] B[n, k] exact in int32, the three fp32 operations separately rounded (no FMA),
+ * g = GELU (tanh approximation) if gelu != 0, else identity. A int8 [M, K], sa fp32 [M], B int8 [N, K],
+ * sb fp32 [N], bias bf16 [N] or NULL, Y bf16 [M, N]; K % 16 == 0, any M, N >= 1.
+ * Replaces launch_gemm_i8(..., grouped = false, ...) kernels/int8_gemm.cu:741-748 (bound as gemm_i8(),
+ * kernels/int8_gemm.cpp:39-50, which also requires N % 8 == 0). */
+int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
+                  lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream);
+
+/* The exact int32 accumulators of the W8A8 GEMM: C[m, n] = sum_k A[m, k] B[n, k], C int32 [M, N]. No counterpart
+ * entry point in the reference (whose tests use torch._int_mm for this, tests/test_int8_gemm.py:236). */
+int lfm2q_gemm_i8_i32(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, lfm2q_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -133,6 +133,94 @@ class DecodeOps:
         return W, scale, B, Nout, K, 0 if int8 else 1
 
 
+class Int8Ops:
+    """INT8 prefill / vision ops (reference: kernels/int8_gemm.cpp). Grouped-64 activation scales (2-D sx) and the
+    fused producers are not provided by this build: asking for them raises RuntimeError."""
+
+    def __init__(self):
+        _capi.lib()
+
+    def gemm_i8(self, xq, sx, w, sw, bias, y, gelu):
+        """W8A8: y [M, N] = bf16(gelu?((xq . w^T) * sx[m] * sw[n] + bias[n])), exact int32 accumulation.
+        Reference: gemm_i8(), kernels/int8_gemm.cpp:39-50."""
+        _check_t(xq, torch.int8, "xq")
+        _check_t(sx, torch.float32, "sx")
+        K = xq.size(-1)
+        M = xq.numel() // K if K else 0
+        if sx.dim() == 2:
+            raise RuntimeError("gemm_i8: grouped activation scales (sx [K/64, M]) are not provided by this build")
+        if sx.numel() != M:
+            raise RuntimeError("sx shape")
+        N = self._check_common(w, sw, bias, y, M, K)
+        _same_device(xq, sx, w, sw, bias, y)
+        _capi.call("lfm2q_gemm_i8", xq.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias),
+                   y.data_ptr(), M, N, K, int(bool(gelu)), _capi.stream(xq))
+
+    def gemm_i8_i32(self, xq, w, c):
+        """The exact int32 accumulators c [M, N] = xq [M, K] . w [N, K]^T (the torch._int_mm analogue)."""
+        _check_t(xq, torch.int8, "xq")
+        _check_t(w, torch.int8, "w")
+        _check_t(c, torch.int32, "c")
+        K = xq.size(-1)
+        M = xq.numel() // K if K else 0
+        if not (w.dim() == 2 and w.size(1) == K):
+            raise RuntimeError("w must be [N, K]")
+        N = w.size(0)
+        if c.numel() != M * N:
+            raise RuntimeError("c shape")
+        if K % 16:
+            raise RuntimeError("need K % 16 == 0")
+        _same_device(xq, w, c)
+        _capi.call("lfm2q_gemm_i8_i32", xq.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, _capi.stream(xq))
+
+    def quant_rows(self, x, q, s):
+        """Per-row symmetric quantization: s = max|x| / 127, q = round(x / s). Reference: quant_rows(),
+        kernels/int8_gemm.cpp:83-96 (a 2-D s asks for grouped scales, not provided by this build)."""
+        _check_bf16(x, "x")
+        _check_t(q, torch.int8, "q")
+        _check_t(s, torch.float32, "s")
+        K = x.size(-1)
+        rows = x.numel() // K if K else 0
+        if s.dim() == 2:
+            raise RuntimeError("quant_rows: grouped scales (s [K/64, rows]) are not provided by this build")
+        if K % 8 or K == 0:
+            raise RuntimeError("K must be a multiple of 8")
+        if q.numel() != x.numel() or s.numel() != rows:
+            raise RuntimeError("q / s shape")
+        _same_device(x, q, s)
+        _capi.call("lfm2q_quant_rows", x.data_ptr(), q.data_ptr(), s.data_ptr(), rows, K, _capi.stream(x))
+
+    @staticmethod
+    def _check_common(w, sw, bias, y, M, K):
+        """kernels/int8_gemm.cpp:22-36 (N % 8 is not required here)."""
+        _check_t(w, torch.int8, "w")
+        _check_t(sw, torch.float32, "sw")
+        _check_bf16(y, "y")
+        if not (w.dim() == 2 and w.size(1) == K):
+            raise RuntimeError("w must be [N, K]")
+        N = w.size(0)
+        if K % 16:
+            raise RuntimeError("need K % 16 == 0")
+        if not (sw.numel() == N and y.numel() == M * N):
+            raise RuntimeError("sw / y shape")
+        if bias is not None:
+            _check_bf16(bias, "bias")
+            if bias.numel() != N:
+                raise RuntimeError("bias shape")
+        return N
+
+
+_INT8 = None
+
+
+def int8_ext():
+    """INT8 GEMM ops for prefill and the vision encoder (reference: src/lfm2opt/kernels.py:66-68)."""
+    global _INT8
+    if _INT8 is None:
+        _INT8 = Int8Ops()
+    return _INT8
+
+
 def ext():
     """The decode-op extension (reference: src/lfm2opt/kernels.py:16-32). LFM2_PDL is read like the reference
     does; it has no effect on HIP."""

@@ -61,6 +61,55 @@ def case_silu_mul(seed, B, I):
     return dict(g=g, y=oracle.silu_mul(g))
 
 
+def division_trap_rows(seed, n_rows=12):
+    """Rows of 64 bf16 values holding (amax, x, -x) where x * fl(1 / s) and the correctly rounded x / s round to
+    different integers (s = amax / 127): a quantizer that multiplies by the reciprocal fails them."""
+    r = np.random.default_rng(seed)
+    allx = np.arange(0, 0x7F80, dtype=np.uint16)
+    fx = oracle.bf2f(allx)
+    rows = []
+    for a in np.unique(bf16(np.abs(r.standard_normal(600)) * 4 + 0.1)):
+        af = oracle.bf2f(np.array([a]))[0]
+        sc = np.float32(af) / np.float32(127)
+        cand = fx[fx <= af]
+        bad = np.nonzero(np.rint(cand / sc) != np.rint(cand * (np.float32(1) / sc)))[0]
+        if bad.size:
+            row = np.zeros(64, np.uint16)
+            pick = allx[bad[np.linspace(0, bad.size - 1, min(bad.size, 20)).astype(int)]]
+            row[0] = a
+            row[1:1 + pick.size] = pick
+            row[32:32 + pick.size] = pick | 0x8000
+            rows.append(row)
+        if len(rows) == n_rows:
+            break
+    return np.stack(rows)
+
+
+def case_quant_rows(seed, M, K):
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((M, K)) * r.uniform(0.01, 4, (M, 1))
+    x[0, 3] = 37.0
+    if M > 2:
+        x[2] = 0.0  # an all-zero row: s = 1e-8 / 127
+    xb = bf16(x)
+    if K == 64:
+        xb[: min(M, 12)] = division_trap_rows(seed)[: min(M, 12)]
+    q, sc = oracle.quant_rows(xb)
+    return dict(x=xb, q=q, s=sc)
+
+
+def case_gemm_i8(seed, M, K, N, bias, gelu):
+    r = np.random.default_rng(seed)
+    xq, sx = oracle.quant_rows(bf16(r.standard_normal((M, K))))
+    wq, sw = oracle.quant_rows(bf16(r.standard_normal((N, K)) * 0.02))
+    d = dict(xq=xq, sx=sx, wq=wq, sw=sw, acc=oracle.gemm_i8_i32(xq, wq))
+    b = bf16(r.standard_normal(N)) if bias else None
+    if b is not None:
+        d["bias"] = b
+    d["y"] = oracle.gemm_i8_epilogue(d["acc"], sx, sw, b, gelu)
+    return d
+
+
 CASES = {
     "gemv_w8_b1_n80_k1024": (case_gemv_w8, (1, 1, 80, 1024)),
     "gemv_w8_b3_n80_k1024": (case_gemv_w8, (2, 3, 80, 1024)),
@@ -73,6 +122,14 @@ CASES = {
     "residual_w8_b1_n64_k2048": (case_residual_w8, (9, 1, 64, 2048)),
     "residual_w8_b16_n64_k1024": (case_residual_w8, (10, 16, 64, 1024)),
     "silu_mul_b3_i300": (case_silu_mul, (11, 3, 300)),
+    "quant_rows_traps_k64": (case_quant_rows, (12, 12, 64)),
+    "quant_rows_m37_k1152": (case_quant_rows, (13, 37, 1152)),
+    "quant_rows_m5_k4304": (case_quant_rows, (14, 5, 4304)),
+    "quant_rows_m3_k8192": (case_quant_rows, (15, 3, 8192)),
+    "gemm_i8_m37_k320_n24_bias": (case_gemm_i8, (16, 37, 320, 24, True, False)),
+    "gemm_i8_m70_k1152_n100": (case_gemm_i8, (17, 70, 1152, 100, False, False)),
+    "gemm_i8_m33_k576_n40_bias_gelu": (case_gemm_i8, (18, 33, 576, 40, True, True)),
+    "gemm_i8_m129_k4304_n72_bias": (case_gemm_i8, (19, 129, 4304, 72, True, False)),
 }
 
 

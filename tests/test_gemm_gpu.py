@@ -1,0 +1,182 @@
+"""W8A8 GEMM and per-token activation quantization on the GPU (through the C ABI via lfm2opt.kernels.int8_ext())
+against the CPU oracle and, at the full prefill / vision shapes, against exact fp64 products on the GPU.
+
+Parity bar (tests/test_int8_gemm.py:158-175, :55-78): quantization bit-exact (q and s), int32 accumulators
+bit-exact, bf16 epilogue 0 ulp without GELU and <= 1 bf16 ulp with GELU.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import GOLDEN
+from gpu_util import dev, dev_bf16, host_bits, ulp_dist
+
+pytestmark = pytest.mark.gpu
+
+PREFILL = [(M, K, N) for M in (512, 2048, 4096) for K, N in ((2048, 3072), (2048, 16384), (8192, 2048))]
+VISION = [(10240, 1152, 3456, False), (10240, 1152, 1152, False), (10240, 1152, 4304, True), (10240, 4304, 1152, False)]
+
+
+@pytest.fixture(scope="module")
+def E(cuda):
+    from lfm2opt.kernels import int8_ext
+
+    return int8_ext()
+
+
+def load(name):
+    return dict(np.load(GOLDEN / f"{name}.npz"))
+
+
+# ------------------------------------------------------------------------------------------------ quant_rows
+@pytest.mark.parametrize("name", ["quant_rows_traps_k64", "quant_rows_m37_k1152", "quant_rows_m5_k4304",
+                                  "quant_rows_m3_k8192"])
+def test_quant_rows_fixture(E, name):
+    f = load(name)
+    rows, K = f["x"].shape
+    q = torch.empty(rows, K, device="cuda", dtype=torch.int8)
+    s = torch.empty(rows, device="cuda", dtype=torch.float32)
+    E.quant_rows(dev_bf16(f["x"]), q, s)
+    assert np.array_equal(s.cpu().numpy(), f["s"]), "scales differ"
+    qq = q.cpu().numpy()
+    assert np.array_equal(qq, f["q"]), f"{int((qq != f['q']).sum())} q mismatches"
+
+
+@pytest.mark.parametrize("M,K", [(4096, 8192), (10240, 1152), (2048, 2048), (777, 4304), (1, 2048), (9, 96)])
+def test_quant_rows_vs_oracle(E, M, K):
+    """Activations ~N(0,1) with 0.1% outliers at 20 sigma (the prefill workload), every K path of the kernel."""
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g)
+    out = torch.rand(M, K, generator=g) < 1e-3
+    x[out] = 20.0 * torch.sign(torch.randn(int(out.sum()), generator=g))
+    xb = x.to(torch.bfloat16)
+    q = torch.empty(M, K, device="cuda", dtype=torch.int8)
+    s = torch.empty(M, device="cuda", dtype=torch.float32)
+    E.quant_rows(xb.cuda(), q, s)
+    rq, rs = oracle.quant_rows(xb.view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(q.cpu().numpy(), rq)
+
+
+# ------------------------------------------------------------------------------------------------ fixtures
+@pytest.mark.parametrize("name", ["gemm_i8_m37_k320_n24_bias", "gemm_i8_m70_k1152_n100",
+                                  "gemm_i8_m33_k576_n40_bias_gelu", "gemm_i8_m129_k4304_n72_bias"])
+def test_gemm_fixture(E, name):
+    f = load(name)
+    M, N = f["y"].shape
+    xq, wq = dev(f["xq"]), dev(f["wq"])
+    c = torch.empty(M, N, device="cuda", dtype=torch.int32)
+    E.gemm_i8_i32(xq, wq, c)
+    assert np.array_equal(c.cpu().numpy(), f["acc"]), "int32 accumulators differ"
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    gelu = "gelu" in name
+    E.gemm_i8(xq, dev(f["sx"]), wq, dev(f["sw"]), dev_bf16(f["bias"]) if "bias" in f else None, y, gelu)
+    u = int(ulp_dist(host_bits(y), f["y"]).max())
+    assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
+
+
+# ------------------------------------------------------------------------------------------------ seeded parity
+def _operands(seed, M, K, N, bias):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    xq, sx = oracle.quant_rows(x.view(torch.int16).numpy().view(np.uint16))
+    wq, sw = oracle.quant_rows(w.view(torch.int16).numpy().view(np.uint16))
+    b = (torch.randn(N, generator=g).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)) if bias else None
+    return xq, sx, wq, sw, b
+
+
+@pytest.mark.parametrize("M,K,N,bias,gelu", [(272, 2048, 3072, False, False), (17, 2048, 2048, False, False),
+                                             (1, 1152, 1152, True, False), (300, 1152, 1152, True, True),
+                                             (257, 4304, 1152, True, False), (64, 1152, 4304, True, True)])
+def test_gemm_vs_oracle(E, M, K, N, bias, gelu):
+    """The reference test's shapes (tests/test_int8_gemm.py:256-259, scaled to oracle-friendly M) plus the vision
+    fc2 K = 4304 and fc1 N = 4304 tails."""
+    xq, sx, wq, sw, b = _operands(M * 7 + N, M, K, N, bias)
+    acc = oracle.gemm_i8_i32(xq, wq)
+    ref = oracle.gemm_i8_epilogue(acc, sx, sw, b, gelu)
+    c = torch.empty(M, N, device="cuda", dtype=torch.int32)
+    E.gemm_i8_i32(dev(xq), dev(wq), c)
+    assert np.array_equal(c.cpu().numpy(), acc)
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), None if b is None else dev_bf16(b), y, gelu)
+    u = int(ulp_dist(host_bits(y), ref).max())
+    assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
+
+
+def _full_check(E, M, K, N, bias, gelu, seed):
+    """Full-size GEMM: int32 against an exact fp64 product on the GPU, bf16 output of 256 sampled rows against the
+    reference test's fp32 epilogue expression (tests/test_int8_gemm.py:166-172) evaluated by torch on the GPU."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    xq = torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8, generator=g)
+    wq = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+    sx = torch.rand(M, device="cuda", generator=g) * 0.05 + 1e-3
+    sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+    c = torch.empty(M, N, device="cuda", dtype=torch.int32)
+    E.gemm_i8_i32(xq, wq, c)
+    exact = (xq.double() @ wq.double().t())
+    assert torch.equal(c.double(), exact), "int32 accumulators differ from the exact product"
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(xq, sx, wq, sw, b, y, gelu)
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(seed))[:256].cuda()
+    r = exact[rows].float() * sx[rows, None]
+    r = r * sw[None, :]
+    if b is not None:
+        r = r + b.float()
+    if gelu:
+        r = torch.nn.functional.gelu(r, approximate="tanh")
+    u = int(ulp_dist(host_bits(y[rows]), host_bits(r.to(torch.bfloat16))).max())
+    assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
+
+
+@pytest.mark.parametrize("M,K,N", PREFILL)
+def test_gemm_prefill_shapes(E, M, K, N):
+    _full_check(E, M, K, N, False, False, M + K + N)
+
+
+@pytest.mark.parametrize("M,K,N,gelu", VISION)
+def test_gemm_vision_shapes(E, M, K, N, gelu):
+    _full_check(E, M, K, N, True, gelu, K + N)
+
+
+# ------------------------------------------------------------------------------------------------ errors
+def test_gemm_argument_errors(E):
+    xq = torch.zeros(4, 64, device="cuda", dtype=torch.int8)
+    w = torch.zeros(8, 64, device="cuda", dtype=torch.int8)
+    sx, sw = torch.ones(4, device="cuda"), torch.ones(8, device="cuda")
+    y = torch.empty(4, 8, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="sx shape"):
+        E.gemm_i8(xq, torch.ones(3, device="cuda"), w, sw, None, y, False)
+    with pytest.raises(RuntimeError, match=r"w must be \[N, K\]"):
+        E.gemm_i8(xq, sx, torch.zeros(8, 32, device="cuda", dtype=torch.int8), sw, None, y, False)
+    with pytest.raises(RuntimeError, match="K % 16"):
+        E.gemm_i8(torch.zeros(4, 40, device="cuda", dtype=torch.int8), sx,
+                  torch.zeros(8, 40, device="cuda", dtype=torch.int8), sw, None, y, False)
+    with pytest.raises(RuntimeError, match="grouped"):
+        E.gemm_i8(xq, torch.ones(1, 4, device="cuda"), w, sw, None, y, False)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        E.quant_rows(torch.zeros(2, 12, device="cuda", dtype=torch.bfloat16), torch.empty(2, 12, device="cuda",
+                     dtype=torch.int8), torch.empty(2, device="cuda"))
+    torch.cuda.synchronize()
+
+
+def test_int8_linear_per_token(cuda, monkeypatch):
+    """Int8Linear (src/lfm2opt/int8.py:54-91) with per-token scales equals quantize_rows + gemm_i8 by hand."""
+    monkeypatch.setenv("LFM2_INT8_GROUP", "0")
+    from lfm2opt.int8 import Int8Linear, quantize_rows
+    from lfm2opt.kernels import int8_ext
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    w = (torch.randn(96, 1152, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(96, device="cuda", generator=g).to(torch.bfloat16)
+    x = torch.randn(2, 5, 1152, device="cuda", generator=g).to(torch.bfloat16)
+    lin = Int8Linear(w, b, kind="qkv")
+    y = lin(x, gelu=True)
+    assert y.shape == (2, 5, 96)
+    xq, sx = quantize_rows(x.reshape(-1, 1152))
+    ref = torch.empty(10, 96, device="cuda", dtype=torch.bfloat16)
+    int8_ext().gemm_i8(xq, sx, lin.q, lin.s, b, ref, True)
+    assert torch.equal(y.reshape(10, 96), ref)
