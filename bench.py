@@ -32,6 +32,12 @@ import torch.nn.functional as F  # noqa: E402
 
 METRIC = "W8 GEMV HBM GB/s (% of peak) + W8A8 GEMM int8 TOPS (% MFMA) at LFM2 shapes"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+# W8A8 shapes (M, K, N, bias, gelu, name): LFM2 prefill at 512 / 2048 / 4096 tokens, SigLIP2 vision at 10 tiles
+W8A8_SHAPES = ([(M, K, N, False, False, f"prefill M={M} {n}") for M in (512, 2048, 4096)
+                for K, N, n in ((2048, 3072, "qkv"), (2048, 16384, "w1|w3"), (8192, 2048, "w2"))]
+               + [(10240, 1152, 3456, True, False, "vision qkv"), (10240, 1152, 1152, True, False, "vision out"),
+                  (10240, 1152, 4304, True, True, "vision fc1+gelu"), (10240, 4304, 1152, True, False, "vision fc2")])
 LAYER_TYPES = "CCACCACCACACACAC"  # LFM2-1.2B layer order (A = attention, C = gated short conv)
 H, FFN, VOCAB, QKV, CONV_IN = 2048, 8192, 65536, 3072, 6144
 
@@ -204,6 +210,51 @@ def decode_results(B, steps, warmup):
     return res
 
 
+def w8a8_results(reps):
+    """Per shape: per-token quantization of the bf16 activations + W8A8 GEMM (bf16 out, bias / GELU where the
+    layer has them), each call on its own weights (>= 512 MB of distinct weights rotated). Activations ~N(0,1)
+    with 0.1% outliers at 20 sigma."""
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    out = []
+    for M, K, N, bias, gelu, name in W8A8_SHAPES:
+        log(f"w8a8 {name} {M}x{K}x{N}")
+        g = torch.Generator(device="cuda").manual_seed(M + K + N)
+        ncopy = max(2, -(-512 * 2 ** 20 // (N * K)))
+        Ws = [torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g) for _ in range(ncopy)]
+        sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+        b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+        x = torch.randn(M, K, device="cuda", generator=g)
+        x = torch.where(torch.rand(M, K, device="cuda", generator=g) < 1e-3, 20.0 * torch.sign(x), x)
+        x = x.to(torch.bfloat16)
+        xq = torch.empty(M, K, device="cuda", dtype=torch.int8)
+        sx = torch.empty(M, device="cuda")
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+
+        def full():
+            for W in Ws:
+                E.quant_rows(x, xq, sx)
+                E.gemm_i8(xq, sx, W, sw, b, y, gelu)
+
+        def gemm_only():
+            for W in Ws:
+                E.gemm_i8(xq, sx, W, sw, b, y, gelu)
+
+        g_full, g_gemm = capture(full), capture(gemm_only)
+        t_full, _ = time_graph(g_full, reps, 2)
+        t_gemm, _ = time_graph(g_gemm, reps, 2)
+        us_full, us_gemm = t_full * 1e3 / ncopy, t_gemm * 1e3 / ncopy
+        ops = 2.0 * M * N * K
+        out.append({"name": name, "M": M, "K": K, "N": N, "bias": bias, "gelu": gelu,
+                    "us_gemm": round(us_gemm, 2), "us_quant_gemm": round(us_full, 2),
+                    "tops_gemm": round(ops / us_gemm / 1e6, 1), "tops_quant_gemm": round(ops / us_full / 1e6, 1),
+                    "mfma_frac_gemm": round(ops / us_gemm / 1e6 / INT8_PEAK_TOPS, 4)})
+        del g_full, g_gemm, Ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,12 +262,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--batches", default="1,4,16", help="decode batch sizes to run (the first one is `value`)")
+    ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 GEMM shapes")
+    ap.add_argument("--only-w8a8", action="store_true", help="W8A8 shapes only (no decode step, no CPU baseline)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
 
+    if args.only_w8a8:
+        print(json.dumps({"w8a8_shapes": w8a8_results(max(5, args.steps // 10))}))
+        return
     batches = [int(b) for b in args.batches.split(",")]
     res1 = decode_results(batches[0], args.steps, args.warmup)
     extra = {B: decode_results(B, max(20, args.steps // 2), args.warmup) for B in batches[1:]}
@@ -246,6 +302,19 @@ def main():
                      "us_per_launch": dom["us_per_launch"], "bytes_per_launch": dom["bytes_per_launch"]},
         "decode": {str(B): r for B, r in [(batches[0], res1)] + list(extra.items())},
     }
+    if not args.no_w8a8:
+        shapes = w8a8_results(max(5, args.steps // 10))
+        ops = sum(2.0 * r["M"] * r["N"] * r["K"] for r in shapes)
+        t_gemm = sum(r["us_gemm"] for r in shapes)
+        t_full = sum(r["us_quant_gemm"] for r in shapes)
+        vis = [r for r in shapes if r["name"].startswith("vision")]
+        vops = sum(2.0 * r["M"] * r["N"] * r["K"] for r in vis)
+        out["w8a8"] = {"unit": "TOPS", "peak": INT8_PEAK_TOPS,
+                       "all_shapes_tops_gemm": round(ops / t_gemm / 1e6, 1),
+                       "all_shapes_tops_quant_gemm": round(ops / t_full / 1e6, 1),
+                       "vision_layer_tops_gemm": round(vops / sum(r["us_gemm"] for r in vis) / 1e6, 1),
+                       "vision_layer_tops_quant_gemm": round(vops / sum(r["us_quant_gemm"] for r in vis) / 1e6, 1),
+                       "shapes": shapes}
     if not args.no_cpu:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline()

@@ -25,11 +25,12 @@ namespace {
 constexpr int GT = 256;  // threads per GEMM workgroup
 constexpr int BK = 64;   // bytes of K per stage
 
-__device__ __forceinline__ int swz(int r, int c) { return (r * 4 + (c ^ ((r >> 1) & 3))) * 16; }
+// LDS byte offset of 16-byte chunk c of 64-byte row r: chunk c is stored at slot c ^ ((r >> sh) & 3)
+__device__ __forceinline__ int swz(int r, int c, int sh) { return (r * 4 + (c ^ ((r >> sh) & 3))) * 16; }
 
 enum GemmOut { OUT_BF16 = 0, OUT_BF16_GELU = 1, OUT_I32 = 2 };
 
-// ((float)acc * sx) * sw + b, each op rounded separately (no FMA contraction), then optional GELU
+// ((float)acc * sx) * sw + b, each op rounded separately (no FMA contraction)
 __device__ __forceinline__ float dequant(int acc, float sx, float sw, float b) {
 #pragma clang fp contract(off)
     float v = (float)acc * sx;
@@ -37,107 +38,317 @@ __device__ __forceinline__ float dequant(int acc, float sx, float sw, float b) {
     return v + b;
 }
 
-template <int BM, int BN, int OUT>
-__global__ __launch_bounds__(GT) void gemm_i8_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
-                                                     const float *__restrict__ sx, const float *__restrict__ sw,
-                                                     const uint16_t *__restrict__ bias, void *__restrict__ Y, int M,
-                                                     int N, int K) {
-    constexpr int WM = BM / 2, WN = BN / 2;     // wavefront block
-    constexpr int TM = WM / 32, TN = WN / 32;   // 32 x 32 MFMA tiles per wavefront
-    constexpr int LA = BM * 4 / GT, LB = BN * 4 / GT;  // 16-byte global loads per thread per stage
-    static_assert(LA >= 1 && LB >= 1 && TM >= 1 && TN >= 1, "tile too small");
-    __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * BK];
-    __shared__ __attribute__((aligned(16))) uint8_t sB[2][BN * BK];
+typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {  // round to nearest even (v_cvt_pk_bf16_f32)
+    v2bf_t r;
+    r[0] = (__bf16)lo;
+    r[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, r);
+}
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int KT = (K + BK - 1) / BK;
+// Workgroup -> output tile. Workgroups are dealt to the 8 XCDs round-robin (workgroup w runs on XCD w % 8), so the
+// tile sequence is split into 8 contiguous bands and band x is given to the workgroups of XCD x; inside the band
+// tiles go in groups of 8 M-tiles that sweep N, so concurrently resident workgroups of one XCD share operand panels
+// in that XCD's L2.
+__device__ __forceinline__ void tile_of(int w, int tm_n, int tn_n, int &tm, int &tn) {
+    const int T = tm_n * tn_n;
+    int t = w;
+    if (T % 8 == 0) t = (w % 8) * (T / 8) + w / 8;
+    constexpr int GM = 8;
+    const int per_group = GM * tn_n;
+    const int g = t / per_group, r = t % per_group;
+    const int gm = min(GM, tm_n - g * GM);
+    tm = g * GM + r % gm;
+    tn = r / gm;
+}
 
-    // global -> register staging: thread t moves chunk (row = t / 4 + 64 j, c = t % 4) of each operand tile
-    v4i ra[LA], rb[LB];
-    auto gload = [&](int kt) {
-        const int k = kt * BK + (tid & 3) * 16;
-#pragma unroll
-        for (int j = 0; j < LA; ++j) {
-            const int r = (tid >> 2) + 64 * j, gm = m0 + r;
-            ra[j] = (gm < M && k < K) ? ld16(A + (size_t)gm * K + k) : v4i{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int j = 0; j < LB; ++j) {
-            const int r = (tid >> 2) + 64 * j, gn = n0 + r;
-            rb[j] = (gn < N && k < K) ? ld16(B + (size_t)gn * K + k) : v4i{0, 0, 0, 0};
-        }
-    };
-    auto swrite = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < LA; ++j)
-            *reinterpret_cast<v4i *>(sA[buf] + swz((tid >> 2) + 64 * j, tid & 3)) = ra[j];
-#pragma unroll
-        for (int j = 0; j < LB; ++j)
-            *reinterpret_cast<v4i *>(sB[buf] + swz((tid >> 2) + 64 * j, tid & 3)) = rb[j];
-    };
+constexpr int STAGES = 3;  // LDS ring depth: stage s computes while s + 1 and s + 2 are loading
 
-    v16i acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+// Raw buffer descriptor in four SGPRs: base, stride 0, num_records = bytes, gfx9 word 3.
+__device__ __forceinline__ v4i make_desc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
+}
+// 16 bytes per lane from buffer offset `voff` straight into LDS at lds_base + 16 * lane (M0 holds lds_base). Written
+// as inline asm so the compiler, which cannot see which LDS bytes the load writes, does not drain every
+// outstanding load before each LDS read or barrier; the kernel orders it with explicit s_waitcnt + barrier.
+__device__ __forceinline__ void lds_dma16(v4i desc, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(desc),
+                 "s"(lds_base)
+                 : "memory", "m0");
+}
+// LDS address of p as a wavefront-uniform (SGPR) value for M0
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(p));
+}
 
-    gload(0);
-    swrite(0);
-    __syncthreads();
-    const int lr = lane & 31, lh = lane >> 5;  // MFMA operand row / k-half of this lane
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        const bool next = kt + 1 < KT;
-        if (next) gload(kt + 1);
-        const uint8_t *a_s = sA[buf], *b_s = sB[buf];
+// Epilogue of one wavefront block: tokens mb .. mb + 32 TM - 1 x weight rows nb .. nb + 32 TN - 1. Per tile (i, j)
+// and run q the lane holds 4 consecutive output columns n .. n + 3 of token row m.
+template <int TM, int TN, int OUT>
+__device__ __forceinline__ void store_tile(const v16i (&acc)[TN][TM], const float *__restrict__ sx,
+                                           const float *__restrict__ sw, const uint16_t *__restrict__ bias,
+                                           void *__restrict__ Y, int M, int N, int mb, int nb, int lr, int lh) {
+    // 4-wide vector path: rows of 4k elements and aligned Y (16 B), sw (16 B) and bias (8 B)
+    const bool vec = (N & 3) == 0 && (((uintptr_t)Y | (uintptr_t)sw) & 15) == 0 && ((uintptr_t)bias & 7) == 0;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {  // two 32-byte k steps per stage
-            const int c = 2 * kk + lh;
-            v4i af[TM], bf[TN];
+    for (int j = 0; j < TM; ++j) {
+        const int m = mb + 32 * j + lr;
+        if (m >= M) continue;
+        const float s_m = OUT == OUT_I32 ? 0.f : sx[m];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const v4i *>(a_s + swz(wm * WM + 32 * i + lr, c));
+        for (int i = 0; i < TN; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const v4i *>(b_s + swz(wn * WN + 32 * j + lr, c));
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (next) swrite(buf ^ 1);
-        __syncthreads();
-    }
-
-    // epilogue. 32x32 MFMA output: lane l, element e -> row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn * WN + 32 * j + lr;
-        if (n >= N) continue;
-        float w = 0.f, b = 0.f;
-        if (OUT != OUT_I32) {
-            w = sw[n];
-            b = bias ? bf2f(bias[n]) : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int m = m0 + wm * WM + 32 * i + 8 * (e >> 2) + 4 * lh + (e & 3);
-                if (m >= M) continue;
+            for (int q = 0; q < 4; ++q) {
+                const int n = nb + 32 * i + 8 * q + 4 * lh;
+                if (n >= N) continue;
+                const size_t o = (size_t)m * N + n;
                 if (OUT == OUT_I32) {
-                    reinterpret_cast<int32_t *>(Y)[(size_t)m * N + n] = acc[i][j][e];
+                    if (vec) {
+                        *reinterpret_cast<v4i *>(reinterpret_cast<int32_t *>(Y) + o) =
+                            v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < N) reinterpret_cast<int32_t *>(Y)[o + e] = acc[i][j][4 * q + e];
+                    }
                 } else {
-                    float v = dequant(acc[i][j][e], sx[m], w, b);
-                    if (OUT == OUT_BF16_GELU) v = gelu_tanh_f32(v);
-                    reinterpret_cast<uint16_t *>(Y)[(size_t)m * N + n] = (uint16_t)f2bf(v);
+                    float v[4];
+                    if (vec) {
+                        const v4f w4 = *reinterpret_cast<const v4f *>(sw + n);
+                        uint32_t b01 = 0, b23 = 0;
+                        if (bias) {
+                            const uint2 bb = *reinterpret_cast<const uint2 *>(bias + n);
+                            b01 = bb.x;
+                            b23 = bb.y;
+                        }
+                        v[0] = dequant(acc[i][j][4 * q], s_m, w4[0], bf2f_lo(b01));
+                        v[1] = dequant(acc[i][j][4 * q + 1], s_m, w4[1], bf2f_hi(b01));
+                        v[2] = dequant(acc[i][j][4 * q + 2], s_m, w4[2], bf2f_lo(b23));
+                        v[3] = dequant(acc[i][j][4 * q + 3], s_m, w4[3], bf2f_hi(b23));
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int ne = min(n + e, N - 1);
+                            v[e] = dequant(acc[i][j][4 * q + e], s_m, sw[ne], bias ? bf2f(bias[ne]) : 0.f);
+                        }
+                    }
+                    if (OUT == OUT_BF16_GELU)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f32(v[e]);
+                    uint16_t *yo = reinterpret_cast<uint16_t *>(Y) + o;
+                    if (vec) {
+                        *reinterpret_cast<uint2 *>(yo) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < N) yo[e] = (uint16_t)f2bf(v[e]);
+                    }
                 }
             }
     }
+}
+
+// BM: token rows (M) per workgroup, BN: weight rows (N). Wavefront (wm, wn) of the 2 x 2 grid owns BM/2 tokens x
+// BN/2 weight rows as TN x TM tiles of 32 x 32, with the weights as the MFMA A operand and the tokens as B, so a
+// lane's accumulator holds, per tile, 4 runs of 4 consecutive output columns of one token row: D[n][m], lane l ->
+// m = l % 32, element e -> n = 8 (e / 4) + 4 (l / 32) + e % 4.
+//
+// Operand tiles go global -> LDS directly (buffer_load_dwordx4 ... lds): one wavefront instruction fills 1 KiB of
+// LDS in lane order, i.e. 16 rows of 64 bytes, so lane i fetches the logical chunk c = (i % 4) ^ key(row) that the
+// swizzled layout keeps in that slot. Rows past M and chunks past K read zeros (buffer range check). The loads of
+// stage s + 2 are issued before the MFMAs of stage s; one s_waitcnt + barrier per stage makes stage s visible.
+template <int BM, int BN, int OUT>
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_kernel(
+    const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
+    const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
+    int sh) {
+    constexpr int WMt = BM / 2, WNt = BN / 2;   // wavefront block: tokens x weight rows
+    constexpr int TM = WMt / 32, TN = WNt / 32;  // 32 x 32 MFMA tiles per wavefront
+    constexpr int IX = BM / 64, IW = BN / 64;    // direct-load instructions per wavefront per stage (16 rows each)
+    static_assert(IX >= 1 && IW >= 1 && TM >= 1 && TN >= 1, "tile too small");
+    __shared__ __attribute__((aligned(1024))) uint8_t sX[STAGES][BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint8_t sW[STAGES][BN * BK];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = (K + BK - 1) / BK;
+
+    // this lane's share of the direct loads: instruction j of wavefront w covers tile rows 16 (4 j + w) + lane / 4
+    const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
+    const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
+    uint32_t ox[IX], ow[IW];
+    int cx[IX], cw[IW];  // byte offset of the fetched chunk within the 64-byte row slice of a stage
+#pragma unroll
+    for (int j = 0; j < IX; ++j) {
+        const int row = 16 * (4 * j + wave) + (lane >> 2);
+        cx[j] = 16 * ((lane & 3) ^ ((row >> sh) & 3));
+        ox[j] = (uint32_t)row * K + cx[j];
+    }
+#pragma unroll
+    for (int j = 0; j < IW; ++j) {
+        const int row = 16 * (4 * j + wave) + (lane >> 2);
+        cw[j] = 16 * ((lane & 3) ^ ((row >> sh) & 3));
+        ow[j] = (uint32_t)row * K + cw[j];
+    }
+    auto issue = [&](int kt) {
+        const int buf = kt % STAGES, k0 = kt * BK;
+#pragma unroll
+        for (int j = 0; j < IX; ++j) {
+            const uint32_t vo = k0 + cx[j] < K ? ox[j] + k0 : 0xfffffff0u;
+            lds_dma16(rx, vo, lds_addr(sX[buf] + 1024 * (4 * j + wave)));
+        }
+#pragma unroll
+        for (int j = 0; j < IW; ++j) {
+            const uint32_t vo = k0 + cw[j] < K ? ow[j] + k0 : 0xfffffff0u;
+            lds_dma16(rw, vo, lds_addr(sW[buf] + 1024 * (4 * j + wave)));
+        }
+    };
+
+    v16i acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+    const int lr = lane & 31, lh = lane >> 5;  // MFMA operand row / k-half of this lane
+    int fw[2][TN], fx[2][TM];                    // fragment byte offsets within a stage buffer
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i) fw[kk][i] = swz(wn * WNt + 32 * i + lr, 2 * kk + lh, sh);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) fx[kk][j] = swz(wm * WMt + 32 * j + lr, 2 * kk + lh, sh);
+    }
+
+    issue(0);
+    if (KT > 1) issue(1);
+    for (int kt = 0; kt < KT; ++kt) {
+        // stage kt has landed once at most the loads of stage kt + 1 are outstanding
+        if (kt + 1 < KT)
+            __builtin_amdgcn_s_waitcnt(0x3f70 | (IX + IW));  // vmcnt(IX + IW), expcnt / lgkmcnt unchanged (max)
+        else
+            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+        // stage kt visible to all; everyone is done with stage kt - 1, whose buffer refills next. A bare s_barrier:
+        // __syncthreads()' fences would make the compiler drain every outstanding load here, the prefetches included
+        // (LDS needs no cache maintenance between the wavefronts of a workgroup).
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + 2 < KT) issue(kt + 2);
+        const uint8_t *x_s = sX[kt % STAGES], *w_s = sW[kt % STAGES];
+        // both k steps' fragments are read up front, the second set while the first set's MFMAs run
+        v4i wf[2][TN], xf[2][TM];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int i = 0; i < TN; ++i) wf[kk][i] = *reinterpret_cast<const v4i *>(w_s + fw[kk][i]);
+#pragma unroll
+            for (int j = 0; j < TM; ++j) xf[kk][j] = *reinterpret_cast<const v4i *>(x_s + fx[kk][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk][i], xf[kk][j], acc[i][j], 0, 0, 0);
+    }
+
+    store_tile<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lr, lh);
+}
+
+// ------------------------------------------------------------------------------------------------ big tiles
+// 256 x 256 tiles for the large GEMMs: 512 threads (8 wavefronts as 4 token blocks x 2 weight blocks, each 64 tokens x
+// 128 weight rows = 2 x 4 MFMA tiles, two wavefronts per SIMD), 128-byte K stages (full 128-byte lines of both
+// operands per row), two LDS stages of 64 KiB filled by direct loads. Per MAC this moves 2/3 of the operand bytes
+// of the 128 x 256 kernel, in whole cache lines. LDS rows are 128 bytes: chunk c of row r sits at slot
+// c ^ ((r >> 1) & 7), so the 16 rows a 16-lane phase of ds_read_b128 reads at one logical chunk hit 16 distinct
+// 16-byte bank groups of the 64-bank LDS.
+constexpr int BKB = 128;
+__device__ __forceinline__ int swz128(int r, int c) { return (r * 8 + (c ^ ((r >> 1) & 7))) * 16; }
+
+template <int OUT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_big_kernel(
+    const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
+    const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K) {
+    constexpr int BM = 256, BN = 256, WMt = 64, WNt = 128, TM = 2, TN = 4;
+    constexpr int IL = BM * BKB / 1024 / 8;  // direct-load instructions per wavefront per operand per stage (= 4)
+    __shared__ __attribute__((aligned(1024))) uint8_t sX[2][BM * BKB];
+    __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BN * BKB];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = (K + BKB - 1) / BKB;
+
+    const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
+    const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
+    // instruction j of wavefront w fills LDS rows 8 (8 j + w) .. + 7; lane i -> row + i / 8, slot i % 8
+    uint32_t off[IL];
+    int cb[IL];
+#pragma unroll
+    for (int j = 0; j < IL; ++j) {
+        const int row = 8 * (8 * j + wave) + (lane >> 3);
+        cb[j] = 16 * ((lane & 7) ^ ((row >> 1) & 7));
+        off[j] = (uint32_t)row * K + cb[j];
+    }
+    auto issue = [&](int kt) {
+        const int buf = kt & 1, k0 = kt * BKB;
+#pragma unroll
+        for (int j = 0; j < IL; ++j) {
+            const bool in = k0 + cb[j] < K;
+            lds_dma16(rx, in ? off[j] + k0 : 0xfffffff0u, lds_addr(sX[buf] + 1024 * (8 * j + wave)));
+            lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, lds_addr(sW[buf] + 1024 * (8 * j + wave)));
+        }
+    };
+
+    v16i acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+    const int lr = lane & 31, lh = lane >> 5;
+    issue(0);
+    for (int kt = 0; kt < KT; ++kt) {
+        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wavefront's loads of stage kt have landed
+        asm volatile("s_barrier" ::: "memory");  // everyone's have; everyone is done with stage kt - 1
+        if (kt + 1 < KT) issue(kt + 1);
+        const uint8_t *x_s = sX[kt & 1], *w_s = sW[kt & 1];
+        // four 32-byte k steps per stage; the fragments of step kk + 1 are read (into the other register set)
+        // before the MFMAs of step kk are issued, so LDS latency hides behind matrix-core work
+        v4i wf[2][TN], xf[2][TM];
+        auto rd = [&](int set, int kk) {
+            const int c = 2 * kk + lh;
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+                wf[set][i] = *reinterpret_cast<const v4i *>(w_s + swz128(wn * WNt + 32 * i + lr, c));
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+                xf[set][j] = *reinterpret_cast<const v4i *>(x_s + swz128(wm * WMt + 32 * j + lr, c));
+        };
+        rd(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            if (kk + 1 < 4) rd((kk + 1) & 1, kk + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk & 1][i], xf[kk & 1][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    store_tile<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lr, lh);
 }
 
 // ------------------------------------------------------------------------------------------------ quant_rows
@@ -211,30 +422,31 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restr
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
-// Tile choice: the largest of 256x256, 256x128, 128x256, 128x128, 128x64, 64x64 (BM x BN) whose tile count fills the
-// chip at least ~1.5 times over, else the one with the best balance of rounds x tile work.
+// Tile choice by a small cost model: time ~ rounds x (K stages + 2) x stage time, rounds = tiles / (CUs x resident
+// workgroups per CU), stage time = tile MACs / relative MFMA efficiency of the configuration (measured on MI355X:
+// the 256 x 256 kernel runs its MFMAs the most densely, 64 x 64 the least). LFM2Q_GEMM_BM / _BN force a tile.
 struct TileCfg {
-    int bm, bn;
+    int bm, bn, wgs_per_cu;
+    double eff;
 };
 
 inline TileCfg pick_tile(int M, int N, int K) {
-    static const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
-    const TileCfg opts[] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {128, 64}, {64, 64}};
+    const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
+    const TileCfg opts[] = {{256, 256, 1, 1.0}, {128, 256, 2, 0.75}, {256, 128, 2, 0.75}, {128, 128, 3, 0.6},
+                            {128, 64, 4, 0.45}, {64, 128, 4, 0.45}, {64, 64, 6, 0.3}};
     if (force_bm && force_bn)
         for (const TileCfg &o : opts)
             if (o.bm == force_bm && o.bn == force_bn) return o;
     const int cus = device_cus();
-    // estimated time ~ rounds * (tile MACs / per-CU rate + per-tile overhead), per-tile overhead ~ 4 stages of K
     double best = 1e30;
     TileCfg bestc = opts[0];
     for (const TileCfg &o : opts) {
         const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
-        const long rounds = (tiles + cus - 1) / cus;
-        const double kst = (double)(K + BK - 1) / BK;
-        // a 64x64 tile runs its MFMAs at about half the efficiency of 256x256 (LDS reads per MAC double as tiles
-        // halve); model it as cost per stage ~ bm * bn * (1 + 64 / bm + 64 / bn) / 256^2
-        const double stage = (double)o.bm * o.bn * (1.0 + 64.0 / o.bm + 64.0 / o.bn) / 65536.0;
-        const double t = rounds * (kst + 4.0) * stage;
+        const long slots = (long)cus * o.wgs_per_cu;
+        const double rounds = (double)((tiles + slots - 1) / slots) * o.wgs_per_cu;  // a CU runs its residents together
+        const double bk = o.bm == 256 && o.bn == 256 ? 128.0 : 64.0;
+        const double stage = (double)o.bm * o.bn * bk / o.eff;
+        const double t = rounds * ((double)(K + bk - 1) / bk + 2.0) * stage;
         if (t < best * 0.999) {
             best = t;
             bestc = o;
@@ -247,17 +459,22 @@ template <int OUT>
 void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float *sw, const uint16_t *bias, void *Y,
                  int M, int N, int K, hipStream_t st) {
     const TileCfg t = pick_tile(M, N, K);
-    const dim3 grid((N + t.bn - 1) / t.bn, (M + t.bm - 1) / t.bm);
+    static const int sh = env_int("LFM2Q_GEMM_SWZ", 2);
+    const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
+    if (t.bm == 256 && t.bn == 256) {
+        gemm_i8_big_kernel<OUT><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+        return;
+    }
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
-        gemm_i8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);                         \
+        gemm_i8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K, sh);                     \
         return;                                                                                                      \
     }
-    LFM2Q_GEMM(256, 256)
-    LFM2Q_GEMM(256, 128)
     LFM2Q_GEMM(128, 256)
+    LFM2Q_GEMM(256, 128)
     LFM2Q_GEMM(128, 128)
     LFM2Q_GEMM(128, 64)
+    LFM2Q_GEMM(64, 128)
     LFM2Q_GEMM(64, 64)
 #undef LFM2Q_GEMM
 }
@@ -267,7 +484,9 @@ int check_gemm(const char *name, const int8_t *A, const int8_t *B, const void *Y
     LFM2Q_REQUIRE(M >= 1 && N >= 1 && K >= 16, LFM2Q_ERR_SHAPE, "%s: need M, N >= 1 and K >= 16 (M=%d N=%d K=%d)",
                   name, M, N, K);
     LFM2Q_REQUIRE(K % 16 == 0, LFM2Q_ERR_SHAPE, "%s: need K %% 16 == 0 (K=%d)", name, K);
-    LFM2Q_REQUIRE(M <= 65535 * 64, LFM2Q_ERR_SHAPE, "%s: M too large (%d)", name, M);
+    LFM2Q_REQUIRE((long)M * K < (1L << 31) && (long)N * K < (1L << 31), LFM2Q_ERR_SHAPE,
+                  "%s: each operand must be smaller than 2 GiB (buffer offsets are 32-bit)", name);
+    LFM2Q_REQUIRE((long)((M + 63) / 64) * ((N + 63) / 64) < (1L << 31), LFM2Q_ERR_SHAPE, "%s: too many tiles", name);
     LFM2Q_REQUIRE(aligned16(A) && aligned16(B), LFM2Q_ERR_ALIGN, "%s: A and B must be 16-byte aligned", name);
     return LFM2Q_OK;
 }

@@ -142,6 +142,25 @@ def test_gemm_vision_shapes(E, M, K, N, gelu):
     _full_check(E, M, K, N, True, gelu, K + N)
 
 
+TILES = [(256, 256), (128, 256), (256, 128), (128, 128), (128, 64), (64, 128), (64, 64)]
+
+
+@pytest.mark.parametrize("bm,bn", TILES)
+def test_gemm_every_tile_config(E, bm, bn, monkeypatch):
+    """Each kernel configuration (forced through LFM2Q_GEMM_BM / _BN) on a shape with M, N and K tails."""
+    monkeypatch.setenv("LFM2Q_GEMM_BM", str(bm))
+    monkeypatch.setenv("LFM2Q_GEMM_BN", str(bn))
+    M, K, N = 300, 4304, 520
+    xq, sx, wq, sw, b = _operands(bm * 7 + bn, M, K, N, True)
+    acc = oracle.gemm_i8_i32(xq, wq)
+    c = torch.empty(M, N, device="cuda", dtype=torch.int32)
+    E.gemm_i8_i32(dev(xq), dev(wq), c)
+    assert np.array_equal(c.cpu().numpy(), acc)
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), dev_bf16(b), y, False)
+    assert int(ulp_dist(host_bits(y), oracle.gemm_i8_epilogue(acc, sx, sw, b)).max()) == 0
+
+
 # ------------------------------------------------------------------------------------------------ errors
 def test_gemm_argument_errors(E):
     xq = torch.zeros(4, 64, device="cuda", dtype=torch.int8)
