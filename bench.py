@@ -255,6 +255,34 @@ def w8a8_results(reps):
     return out
 
 
+def eager_kind(kind, B, reps):
+    """Counter-collection mode: the launches of one decode kind (or a plain 256 MiB device copy, kind "copy", the
+    calibration of the HBM byte counters) run eagerly, one kernel per dispatch, `reps` times over."""
+    if kind == "copy":
+        src = torch.randint(-127, 128, (256 << 20,), device="cuda", dtype=torch.int8)
+        dst = torch.empty_like(src)
+        fns, nbytes = [lambda: dst.copy_(src)], 2 * src.numel()
+    else:
+        step = DecodeStep(B, "cuda")
+        sel = [(fn, b) for k, fn, b in step.ops if k == kind]
+        if not sel:
+            raise SystemExit(f"unknown kind {kind!r}: one of {sorted(set(k for k, _, _ in step.ops))} or copy")
+        fns, nbytes = [fn for fn, _ in sel], sel[0][1]
+    for fn in fns:
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        for fn in fns:
+            fn()
+    t1.record()
+    t1.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / (reps * len(fns))
+    print(json.dumps({"kind": kind, "batch": B, "launches": reps * len(fns), "us_per_launch_eager": round(us, 2),
+                      "bytes_per_launch": nbytes}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -264,12 +292,17 @@ def main():
     ap.add_argument("--batches", default="1,4,16", help="decode batch sizes to run (the first one is `value`)")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 GEMM shapes")
     ap.add_argument("--only-w8a8", action="store_true", help="W8A8 shapes only (no decode step, no CPU baseline)")
+    ap.add_argument("--eager-kind", default=None,
+                    help="run one decode kind (e.g. 'w1|w3+swiglu') or 'copy' eagerly, for counter collection")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
 
+    if args.eager_kind:
+        eager_kind(args.eager_kind, int(args.batches.split(",")[0]), args.steps)
+        return
     if args.only_w8a8:
         print(json.dumps({"w8a8_shapes": w8a8_results(max(5, args.steps // 10))}))
         return

@@ -148,6 +148,79 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[TN][TM], const floa
     }
 }
 
+// Staged epilogue for bf16 output, used when N % 8 == 0 and Y / sw are 16-byte (bias 8-byte) aligned. The MFMA
+// layout leaves each lane with 16-byte pieces of 32 different token rows, which as direct stores become partial-line
+// writes spread over rows N * 2 bytes apart. Instead each wavefront dequantizes one 32-token slice of its block at a
+// time into its own LDS region (row pitch 2 WN + 8 bytes: conflict-free 8-byte writes of 32 rows), then reads it
+// back row-major (two 8-byte reads per lane and row) and writes whole contiguous row runs, 16 bytes per lane. LDS ops of one wavefront execute in order,
+// so the slice needs no barrier between its writes and the reads of other lanes, nor before the next slice.
+template <int TN>
+constexpr int stage_bytes() { return 32 * (64 * TN + 8); }
+
+template <int TM, int TN, int OUT>
+__device__ __forceinline__ void store_tile_staged(const v16i (&acc)[TN][TM], const float *__restrict__ sx,
+                                                  const float *__restrict__ sw, const uint16_t *__restrict__ bias,
+                                                  uint16_t *__restrict__ Y, int M, int N, int mb, int nb, int lane,
+                                                  uint8_t *stage) {
+    constexpr int WN = 32 * TN;      // output columns of the block
+    constexpr int P = 2 * WN + 8;    // LDS row pitch (bytes)
+    constexpr int CPRo = WN / 8;     // 16-byte chunks per output row
+    constexpr int RPI = 64 / CPRo;   // rows per store instruction
+    const int lr = lane & 31, lh = lane >> 5;
+    const int c = lane % CPRo, r0 = lane / CPRo;
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int m = mb + 32 * j + lr;
+        const float s_m = sx[min(m, M - 1)];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = min(nb + 32 * i + 8 * q + 4 * lh, N - 4);  // N % 8 == 0: clamped runs are whole
+                const v4f w4 = *reinterpret_cast<const v4f *>(sw + n);
+                uint32_t b01 = 0, b23 = 0;
+                if (bias) {
+                    const uint2 bb = *reinterpret_cast<const uint2 *>(bias + n);
+                    b01 = bb.x;
+                    b23 = bb.y;
+                }
+                float v[4];
+                v[0] = dequant(acc[i][j][4 * q], s_m, w4[0], bf2f_lo(b01));
+                v[1] = dequant(acc[i][j][4 * q + 1], s_m, w4[1], bf2f_hi(b01));
+                v[2] = dequant(acc[i][j][4 * q + 2], s_m, w4[2], bf2f_lo(b23));
+                v[3] = dequant(acc[i][j][4 * q + 3], s_m, w4[3], bf2f_hi(b23));
+                if (OUT == OUT_BF16_GELU)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f32(v[e]);
+                *reinterpret_cast<uint2 *>(stage + lr * P + 2 * (32 * i + 8 * q + 4 * lh)) =
+                    make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int rr = 0; rr < 32; rr += RPI) {
+            const int r = rr + r0;
+            // two 8-byte reads: odd rows are only 8-byte aligned at this pitch
+            const uint2 v0 = *reinterpret_cast<const uint2 *>(stage + r * P + 16 * c);
+            const uint2 v1 = *reinterpret_cast<const uint2 *>(stage + r * P + 16 * c + 8);
+            const int mo = mb + 32 * j + r, no = nb + 8 * c;
+            if (mo < M && no < N) *reinterpret_cast<uint4 *>(Y + (size_t)mo * N + no) = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+template <int TM, int TN, int OUT>
+__device__ __forceinline__ void epilogue(const v16i (&acc)[TN][TM], const float *__restrict__ sx,
+                                         const float *__restrict__ sw, const uint16_t *__restrict__ bias,
+                                         void *__restrict__ Y, int M, int N, int mb, int nb, int lane,
+                                         uint8_t *stage) {
+    const int lr = lane & 31, lh = lane >> 5;
+    if (OUT != OUT_I32 && (N & 7) == 0 && (((uintptr_t)Y | (uintptr_t)sw) & 15) == 0 && ((uintptr_t)bias & 7) == 0)
+        store_tile_staged<TM, TN, OUT>(acc, sx, sw, bias, reinterpret_cast<uint16_t *>(Y), M, N, mb, nb, lane, stage);
+    else
+        store_tile<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, mb, nb, lr, lh);
+}
+
 // BM: token rows (M) per workgroup, BN: weight rows (N). Wavefront (wm, wn) of the 2 x 2 grid owns BM/2 tokens x
 // BN/2 weight rows as TN x TM tiles of 32 x 32, with the weights as the MFMA A operand and the tokens as B, so a
 // lane's accumulator holds, per tile, 4 runs of 4 consecutive output columns of one token row: D[n][m], lane l ->
@@ -166,8 +239,10 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     constexpr int TM = WMt / 32, TN = WNt / 32;  // 32 x 32 MFMA tiles per wavefront
     constexpr int IX = BM / 64, IW = BN / 64;    // direct-load instructions per wavefront per stage (16 rows each)
     static_assert(IX >= 1 && IW >= 1 && TM >= 1 && TN >= 1, "tile too small");
-    __shared__ __attribute__((aligned(1024))) uint8_t sX[STAGES][BM * BK];
-    __shared__ __attribute__((aligned(1024))) uint8_t sW[STAGES][BN * BK];
+    static_assert(4 * stage_bytes<TN>() <= STAGES * (BM + BN) * BK, "epilogue staging exceeds the LDS ring");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * (BM + BN) * BK];
+    uint8_t(*sX)[BM * BK] = reinterpret_cast<uint8_t(*)[BM * BK]>(smem);
+    uint8_t(*sW)[BN * BK] = reinterpret_cast<uint8_t(*)[BN * BK]>(smem + STAGES * BM * BK);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
@@ -258,48 +333,60 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk][i], xf[kk][j], acc[i][j], 0, 0, 0);
     }
 
-    store_tile<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lr, lh);
+    __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
+    epilogue<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
+                          smem + wave * stage_bytes<TN>());
 }
 
 // ------------------------------------------------------------------------------------------------ big tiles
 // 256 x 256 tiles for the large GEMMs: 512 threads (8 wavefronts as 4 token blocks x 2 weight blocks, each 64 tokens x
-// 128 weight rows = 2 x 4 MFMA tiles, two wavefronts per SIMD), 128-byte K stages (full 128-byte lines of both
-// operands per row), two LDS stages of 64 KiB filled by direct loads. Per MAC this moves 2/3 of the operand bytes
-// of the 128 x 256 kernel, in whole cache lines. LDS rows are 128 bytes: chunk c of row r sits at slot
-// c ^ ((r >> 1) & 7), so the 16 rows a 16-lane phase of ds_read_b128 reads at one logical chunk hit 16 distinct
-// 16-byte bank groups of the 64-bank LDS.
-constexpr int BKB = 128;
-__device__ __forceinline__ int swz128(int r, int c) { return (r * 8 + (c ^ ((r >> 1) & 7))) * 16; }
+// 128 weight rows = 2 x 4 MFMA tiles, two wavefronts per SIMD). Per MAC this moves 2/3 of the L2 -> LDS operand
+// bytes of the 128 x 256 kernel, which is what bounds the large shapes (the L2 runs near saturation there). K
+// advances in BKT-byte stages through an NST-deep LDS ring filled by direct loads (NST - 1 stages in flight).
+// LDS rows are BKT bytes = CPR 16-byte chunks; chunk c of row r sits at slot c ^ ((r / (8 / CPR * 2)) % CPR), so
+// the 16 rows a 16-lane phase of ds_read_b128 reads at one logical chunk hit 16 distinct 16-byte bank groups of the
+// 64-bank LDS.
+template <int CPR>
+__device__ __forceinline__ int swzb(int r, int c) {
+    constexpr int SH = CPR == 8 ? 1 : 2;
+    return (r * CPR + (c ^ ((r >> SH) & (CPR - 1)))) * 16;
+}
 
-template <int OUT>
+template <int OUT, int BKT, int NST>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_big_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K) {
     constexpr int BM = 256, BN = 256, WMt = 64, WNt = 128, TM = 2, TN = 4;
-    constexpr int IL = BM * BKB / 1024 / 8;  // direct-load instructions per wavefront per operand per stage (= 4)
-    __shared__ __attribute__((aligned(1024))) uint8_t sX[2][BM * BKB];
-    __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BN * BKB];
+    constexpr int CPR = BKT / 16;        // 16-byte chunks per LDS row
+    constexpr int RPI = 64 / CPR;        // rows one direct-load instruction fills (1 KiB)
+    constexpr int IL = BM / RPI / 8;     // direct-load instructions per wavefront per operand per stage
+    constexpr int KS = BKT / 32;         // 32-byte MFMA k steps per stage
+    static_assert(2 * NST * BM * BKT <= 160 * 1024, "LDS ring too large");
+    static_assert(8 * stage_bytes<TN>() <= 2 * NST * BM * BKT, "epilogue staging exceeds the LDS ring");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * BM * BKT];
+    uint8_t(*sX)[BM * BKT] = reinterpret_cast<uint8_t(*)[BM * BKT]>(smem);
+    uint8_t(*sW)[BN * BKT] = reinterpret_cast<uint8_t(*)[BN * BKT]>(smem + NST * BM * BKT);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     int tm, tn;
     tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int KT = (K + BKB - 1) / BKB;
+    const int KT = (K + BKT - 1) / BKT;
 
     const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
     const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
-    // instruction j of wavefront w fills LDS rows 8 (8 j + w) .. + 7; lane i -> row + i / 8, slot i % 8
+    // instruction j of wavefront w fills LDS rows RPI (8 j + w) .. + RPI - 1; lane i -> row + i / CPR, slot i % CPR
     uint32_t off[IL];
     int cb[IL];
 #pragma unroll
     for (int j = 0; j < IL; ++j) {
-        const int row = 8 * (8 * j + wave) + (lane >> 3);
-        cb[j] = 16 * ((lane & 7) ^ ((row >> 1) & 7));
+        const int row = RPI * (8 * j + wave) + lane / CPR;
+        cb[j] = swzb<CPR>(row, lane % CPR) - row * BKT;  // byte offset of the logical chunk stored in this slot
         off[j] = (uint32_t)row * K + cb[j];
     }
     auto issue = [&](int kt) {
-        const int buf = kt & 1, k0 = kt * BKB;
+        const int buf = kt % NST, k0 = kt * BKT;
 #pragma unroll
         for (int j = 0; j < IL; ++j) {
             const bool in = k0 + cb[j] < K;
@@ -317,28 +404,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
     const int lr = lane & 31, lh = lane >> 5;
-    issue(0);
+#pragma unroll
+    for (int p = 0; p < NST - 1; ++p)
+        if (p < KT) issue(p);
     for (int kt = 0; kt < KT; ++kt) {
-        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wavefront's loads of stage kt have landed
-        asm volatile("s_barrier" ::: "memory");  // everyone's have; everyone is done with stage kt - 1
-        if (kt + 1 < KT) issue(kt + 1);
-        const uint8_t *x_s = sX[kt & 1], *w_s = sW[kt & 1];
-        // four 32-byte k steps per stage; the fragments of step kk + 1 are read (into the other register set)
-        // before the MFMAs of step kk are issued, so LDS latency hides behind matrix-core work
+        // stage kt has landed once at most the loads of the stages after it that are in flight remain outstanding
+        if (kt + NST - 2 < KT)
+            __builtin_amdgcn_s_waitcnt(0x3f70 | ((NST - 2) * 2 * IL));  // vmcnt((NST - 2) * 2 IL)
+        else
+            __builtin_amdgcn_s_waitcnt(0x3f70);                          // vmcnt(0)
+        asm volatile("s_barrier" ::: "memory");  // everyone's loads of stage kt landed; stage kt - 1 is free
+        if (kt + NST - 1 < KT) issue(kt + NST - 1);
+        const uint8_t *x_s = sX[kt % NST], *w_s = sW[kt % NST];
+        // the fragments of k step kk + 1 are read (into the other register set) before the MFMAs of step kk issue
         v4i wf[2][TN], xf[2][TM];
         auto rd = [&](int set, int kk) {
             const int c = 2 * kk + lh;
 #pragma unroll
             for (int i = 0; i < TN; ++i)
-                wf[set][i] = *reinterpret_cast<const v4i *>(w_s + swz128(wn * WNt + 32 * i + lr, c));
+                wf[set][i] = *reinterpret_cast<const v4i *>(w_s + swzb<CPR>(wn * WNt + 32 * i + lr, c));
 #pragma unroll
             for (int j = 0; j < TM; ++j)
-                xf[set][j] = *reinterpret_cast<const v4i *>(x_s + swz128(wm * WMt + 32 * j + lr, c));
+                xf[set][j] = *reinterpret_cast<const v4i *>(x_s + swzb<CPR>(wm * WMt + 32 * j + lr, c));
         };
         rd(0, 0);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            if (kk + 1 < 4) rd((kk + 1) & 1, kk + 1);
+        for (int kk = 0; kk < KS; ++kk) {
+            if (kk + 1 < KS) rd((kk + 1) & 1, kk + 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < TN; ++i)
@@ -348,7 +440,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    store_tile<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lr, lh);
+    __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
+    epilogue<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
+                          smem + wave * stage_bytes<TN>());
 }
 
 // ------------------------------------------------------------------------------------------------ quant_rows
@@ -462,7 +556,12 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
     static const int sh = env_int("LFM2Q_GEMM_SWZ", 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
     if (t.bm == 256 && t.bn == 256) {
-        gemm_i8_big_kernel<OUT><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+        // ring shape (K bytes per stage x stages); LFM2Q_GEMM_RING = 1282 / 644 / 645 forces one
+        switch (env_int("LFM2Q_GEMM_RING", 1282)) {
+        case 644: gemm_i8_big_kernel<OUT, 64, 4><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;
+        case 645: gemm_i8_big_kernel<OUT, 64, 5><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;
+        default: gemm_i8_big_kernel<OUT, 128, 2><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;
+        }
         return;
     }
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
