@@ -71,6 +71,21 @@ int lfm2q_gemv_swiglu(int wtype, const void *W, const float *scale, const lfm2q_
 int lfm2q_gemv_residual(int wtype, const void *W, const float *scale, const lfm2q_bf16 *x, lfm2q_bf16 *h, int B,
                         int N, int K, lfm2q_stream_t stream);
 
+/* Weight-only INT4 GEMV with group-wise scales and zero points: acc[b, n] = sum_k s[n, k/group] (q[n, k] - z[n,
+ * k/group]) x[b, k] in fp32, y[b, n] = bf16(acc[b, n]) (epi 0), the SwiGLU pair of W = w1|w3 [2N, K] (epi 1, same
+ * roundings as lfm2q_gemv_swiglu with the scales folded into acc) or h[b, n] = bf16(h[b, n] + bf16(acc[b, n]))
+ * in place in y (epi 2). Nibble i of 32-bit word w of a weight row holds q for k = 8 w + i in both formats:
+ *   fmt 0: Wq uint8 [R, K/2] holding q + 8 (weight 2j in the low nibble of byte j), S fp32 [R, K/group], Z = NULL,
+ *          zero point 8 -- the reference format;
+ *   fmt 1: Wq int32 [R, K/8] holding q in [0, 15], S fp16 [R, K/group], Z int32 [R, ceil(K/group/8)] with the
+ *          zero point of group 8 w + j in nibble j of word w -- GPTQ-style storage;
+ * R = N (2N for epi 1). x bf16 [B, K], y bf16 [B, N]; any B >= 1; group % 32 == 0, K % group == 0, K <= 8192.
+ * Batches of 2..16 rows run on the matrix cores when group % 128 == 0.
+ * Replaces launch_gemv_w4 kernels/lfm2_decode.cu:938-950 (bound as gemv_w4(), kernels/lfm2_decode.cpp:86-98,
+ * which is fmt 0, epi 0 and batch 1 only). */
+int lfm2q_gemv_w4(int fmt, const void *Wq, const void *S, const int32_t *Z, const lfm2q_bf16 *x, lfm2q_bf16 *y,
+                  int B, int N, int K, int group, int epi, lfm2q_stream_t stream);
+
 /* y[b, i] = bf16( bf16(silu(g[b, i])) * g[b, I + i] ), g bf16 [B, 2I], y bf16 [B, I].
  * Replaces launch_silu_mul kernels/lfm2_decode.cu:954-969 (bound as silu_mul(), kernels/lfm2_decode.cpp:100-103). */
 int lfm2q_silu_mul(const lfm2q_bf16 *g, lfm2q_bf16 *y, int B, int I, lfm2q_stream_t stream);

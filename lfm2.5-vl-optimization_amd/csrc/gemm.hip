@@ -516,32 +516,32 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restr
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
-// Tile choice by a small cost model: time ~ rounds x (K stages + 2) x stage time, rounds = tiles / (CUs x resident
-// workgroups per CU), stage time = tile MACs / relative MFMA efficiency of the configuration (measured on MI355X:
-// the 256 x 256 kernel runs its MFMAs the most densely, 64 x 64 the least). LFM2Q_GEMM_BM / _BN force a tile.
+// Tile choice by a two-term cost model fitted to MI355X timings of the seven configurations over the LFM2 prefill and
+// SigLIP2 vision shapes: with `per` = ceil(tiles / CUs) tiles on the busiest CU, time ~ a x per x BM x BN x K (the
+// CU's matrix-core work, a = microseconds per million MACs, lower for bigger tiles) + b x ceil(per / resident) (b =
+// per-round prologue / epilogue cost, `resident` = workgroups one CU holds). LFM2Q_GEMM_BM / _BN force a tile.
 struct TileCfg {
-    int bm, bn, wgs_per_cu;
-    double eff;
+    int bm, bn, resident;
+    double a, b;
 };
 
 inline TileCfg pick_tile(int M, int N, int K) {
     const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
-    const TileCfg opts[] = {{256, 256, 1, 1.0}, {128, 256, 2, 0.75}, {256, 128, 2, 0.75}, {128, 128, 3, 0.6},
-                            {128, 64, 4, 0.45}, {64, 128, 4, 0.45}, {64, 64, 6, 0.3}};
+    static const TileCfg opts[] = {{256, 256, 1, 0.1488, 18.64}, {128, 256, 2, 0.2726, 10.38},
+                                   {256, 128, 2, 0.2795, 9.88},  {128, 128, 3, 0.3312, 4.92},
+                                   {128, 64, 4, 0.4559, 1.98},   {64, 128, 4, 0.4571, 2.03},
+                                   {64, 64, 6, 0.5926, 0.08}};
     if (force_bm && force_bn)
         for (const TileCfg &o : opts)
             if (o.bm == force_bm && o.bn == force_bn) return o;
-    const int cus = device_cus();
-    double best = 1e30;
+    const long cus = device_cus();
+    double best = 1e300;
     TileCfg bestc = opts[0];
     for (const TileCfg &o : opts) {
         const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
-        const long slots = (long)cus * o.wgs_per_cu;
-        const double rounds = (double)((tiles + slots - 1) / slots) * o.wgs_per_cu;  // a CU runs its residents together
-        const double bk = o.bm == 256 && o.bn == 256 ? 128.0 : 64.0;
-        const double stage = (double)o.bm * o.bn * bk / o.eff;
-        const double t = rounds * ((double)(K + bk - 1) / bk + 2.0) * stage;
-        if (t < best * 0.999) {
+        const long per = (tiles + cus - 1) / cus;
+        const double t = o.a * (double)per * o.bm * o.bn * (double)K * 1e-6 + o.b * (double)((per + o.resident - 1) / o.resident);
+        if (t < best) {
             best = t;
             bestc = o;
         }

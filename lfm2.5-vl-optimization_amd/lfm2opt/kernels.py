@@ -79,6 +79,65 @@ class DecodeOps:
         _capi.call("lfm2q_gemv_swiglu", wtype, W.data_ptr(), _capi.ptr(scale), x.data_ptr(), y.data_ptr(), B, S, K,
                    _capi.stream(x))
 
+    def gemv_w4(self, Wp, S, x, y, rows=0, epi=0):
+        """INT4 weight-only GEMV in the reference format: Wp uint8 [R, K/2] (two int4 + 8 per byte, weight 2j in the
+        low nibble of byte j), S fp32 [R, K/group]; y [B, N] = x [B, K] @ dequant(Wp)^T with R = N.
+        Reference: gemv_w4(), kernels/lfm2_decode.cpp:86-98 (batch 1 there; any B >= 1 here). rows is accepted for
+        the reference's signature and has no effect. epi (an addition): 0 plain, 1 SwiGLU over Wp = w1|w3
+        (R = 2N, y [B, N]), 2 residual add in place into y."""
+        _check_bf16(x, "x")
+        _check_bf16(y, "y")
+        if not (Wp.is_cuda and Wp.is_contiguous() and Wp.dtype == torch.uint8 and Wp.dim() == 2):
+            raise RuntimeError("Wp: contiguous uint8 [N, K/2]")
+        if not (S.is_cuda and S.is_contiguous() and S.dtype == torch.float32):
+            raise RuntimeError("S: contiguous fp32 [N, K/128]")
+        R, K = Wp.size(0), Wp.size(1) * 2
+        group = self._w4_group(S, R, K)
+        B, N = self._w4_shapes(x, y, R, K, epi)
+        _same_device(Wp, S, x, y)
+        _capi.call("lfm2q_gemv_w4", 0, Wp.data_ptr(), S.data_ptr(), None, x.data_ptr(), y.data_ptr(), B, N, K, group,
+                   int(epi), _capi.stream(x))
+
+    def gemv_w4z(self, qweight, scales, qzeros, x, y, epi=0):
+        """INT4 weight-only GEMV in GPTQ-style storage (an addition): qweight int32 [R, K/8] (nibble i of word w =
+        q for k = 8 w + i, q in [0, 15]), scales fp16 [R, K/group], qzeros int32 [R, ceil(K/group/8)] (nibble j of
+        word w = zero point of group 8 w + j); w = s (q - z). epi as in gemv_w4."""
+        _check_bf16(x, "x")
+        _check_bf16(y, "y")
+        if not (qweight.is_cuda and qweight.is_contiguous() and qweight.dtype == torch.int32 and qweight.dim() == 2):
+            raise RuntimeError("qweight: contiguous int32 [N, K/8]")
+        if not (scales.is_cuda and scales.is_contiguous() and scales.dtype == torch.float16):
+            raise RuntimeError("scales: contiguous fp16 [N, K/group]")
+        R, K = qweight.size(0), qweight.size(1) * 8
+        group = self._w4_group(scales, R, K)
+        G = K // group
+        if not (qzeros.is_cuda and qzeros.is_contiguous() and qzeros.dtype == torch.int32
+                and tuple(qzeros.shape) == (R, (G + 7) // 8)):
+            raise RuntimeError("qzeros: contiguous int32 [N, ceil(K/group/8)]")
+        B, N = self._w4_shapes(x, y, R, K, epi)
+        _same_device(qweight, scales, qzeros, x, y)
+        _capi.call("lfm2q_gemv_w4", 1, qweight.data_ptr(), scales.data_ptr(), qzeros.data_ptr(), x.data_ptr(),
+                   y.data_ptr(), B, N, K, group, int(epi), _capi.stream(x))
+
+    @staticmethod
+    def _w4_group(S, R, K):
+        if not (S.dim() == 2 and S.size(0) == R and S.size(1) >= 1 and K % S.size(1) == 0):
+            raise RuntimeError("S must be [N, K / group]")
+        group = K // S.size(1)
+        if group % 32:
+            raise RuntimeError("group size must be a multiple of 32")
+        return group
+
+    @staticmethod
+    def _w4_shapes(x, y, R, K, epi):
+        if epi not in (0, 1, 2):
+            raise RuntimeError("epi 0 (none), 1 (swiglu) or 2 (residual)")
+        N = R // 2 if epi == 1 else R
+        B = x.numel() // K if K else 0
+        if not ((epi != 1 or R % 2 == 0) and B >= 1 and x.numel() == B * K and y.numel() == B * N):
+            raise RuntimeError("x [B, K], y [B, N]")
+        return B, N
+
     def silu_mul(self, g, y):
         """y = silu(a) * b on g = [a | b]; reference: silu_mul(), kernels/lfm2_decode.cpp:100-103."""
         _check_bf16(g, "g")

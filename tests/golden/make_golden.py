@@ -110,6 +110,42 @@ def case_gemm_i8(seed, M, K, N, bias, gelu):
     return d
 
 
+def pack_ref_int4(q):
+    """q in [-8, 7] [N, K] -> uint8 [N, K/2]: weight 2j in the low nibble of byte j, stored as q + 8."""
+    u = (np.asarray(q) + 8).astype(np.uint8)
+    return (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+
+
+def pack_nibbles(v):
+    """ints in [0, 15] [R, C] -> int32 [R, ceil(C/8)], nibble i of word w = column 8 w + i."""
+    R, C = v.shape
+    pad = np.zeros((R, -(-C // 8) * 8), np.uint32)
+    pad[:, :C] = v
+    w = np.zeros((R, pad.shape[1] // 8), np.uint32)
+    for i in range(8):
+        w |= pad[:, i::8] << np.uint32(4 * i)
+    return w.view(np.int32)
+
+
+def case_gemv_w4(seed, B, N, K, group):
+    r = np.random.default_rng(seed)
+    q = r.integers(-8, 8, (N, K))
+    S = (np.abs(r.standard_normal((N, K // group))) * 0.02 + 1e-3).astype(np.float32)
+    x = bf16(r.standard_normal((B, K)))
+    Wp = pack_ref_int4(q)
+    return dict(Wp=Wp, S=S, x=x, y=oracle.gemv_w4(Wp, S, x))
+
+
+def case_gemv_w4z(seed, B, R, K, group, swiglu):
+    r = np.random.default_rng(seed)
+    q = r.integers(0, 16, (R, K))
+    z = r.integers(0, 16, (R, K // group))
+    S = (np.abs(r.standard_normal((R, K // group))) * 0.02 + 1e-3).astype(np.float16)
+    x = bf16(r.standard_normal((B, K)))
+    Wq, Z = pack_nibbles(q), pack_nibbles(z)
+    return dict(Wq=Wq, S=S.view(np.uint16), Z=Z, x=x, y=oracle.gemv_w4z(Wq, S, Z, x, group, swiglu=swiglu))
+
+
 CASES = {
     "gemv_w8_b1_n80_k1024": (case_gemv_w8, (1, 1, 80, 1024)),
     "gemv_w8_b3_n80_k1024": (case_gemv_w8, (2, 3, 80, 1024)),
@@ -130,6 +166,11 @@ CASES = {
     "gemm_i8_m70_k1152_n100": (case_gemm_i8, (17, 70, 1152, 100, False, False)),
     "gemm_i8_m33_k576_n40_bias_gelu": (case_gemm_i8, (18, 33, 576, 40, True, True)),
     "gemm_i8_m129_k4304_n72_bias": (case_gemm_i8, (19, 129, 4304, 72, True, False)),
+    "gemv_w4_b1_n80_k1024_g128": (case_gemv_w4, (20, 1, 80, 1024, 128)),
+    "gemv_w4_b4_n48_k2048_g128": (case_gemv_w4, (21, 4, 48, 2048, 128)),
+    "gemv_w4_b2_n40_k512_g64": (case_gemv_w4, (22, 2, 40, 512, 64)),
+    "gemv_w4z_b1_r64_k2048_g128": (case_gemv_w4z, (23, 1, 64, 2048, 128, False)),
+    "gemv_w4z_b8_r96_k1024_g128_swiglu": (case_gemv_w4z, (24, 8, 96, 1024, 128, True)),
 }
 
 
