@@ -33,6 +33,11 @@ import torch.nn.functional as F  # noqa: E402
 METRIC = "W8 GEMV HBM GB/s (% of peak) + W8A8 GEMM int8 TOPS (% MFMA) at LFM2 shapes"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+# HBM bytes per launch of the dominant decode kernel (w1|w3 16384 x 2048 INT8 + SwiGLU, batch 1), from two rocprofv3
+# --pmc runs of `bench.py --eager-kind 'w1|w3+swiglu'` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled
+# by what the counter reads for a 256 MiB device copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0): the run recorded in
+# profiles/hbm_traffic_counters.md. Re-measure after changing that kernel.
+W13_TRAFFIC_BYTES = 34216117
 # W8A8 shapes (M, K, N, bias, gelu, name): LFM2 prefill at 512 / 2048 / 4096 tokens, SigLIP2 vision at 10 tiles
 W8A8_SHAPES = ([(M, K, N, False, False, f"prefill M={M} {n}") for M in (512, 2048, 4096)
                 for K, N, n in ((2048, 3072, "qkv"), (2048, 16384, "w1|w3"), (8192, 2048, "w2"))]
@@ -51,10 +56,23 @@ def swiglu_bytes(S, K, B):
     return 2 * S * K + 4 * 2 * S + 2 * B * K + 2 * B * S
 
 
-class DecodeStep:
-    """All GEMVs of one decode step with distinct weights per layer, as a list of zero-argument launches."""
+W4_GROUP = 128
 
-    def __init__(self, B, device, seed=0):
+
+def w4_bytes(N, K, B, residual=False, out=None):
+    """Algorithmic bytes of one GPTQ-style INT4 GEMV over N weight rows: packed weights N K / 2, fp16 scales
+    2 N K / 128, 4-bit zero points N K / 256, x, y (out columns; N unless SwiGLU) and the residual read."""
+    out = N if out is None else out
+    return N * K // 2 + 2 * N * K // W4_GROUP + N * K // (2 * W4_GROUP) + 2 * B * K + 2 * B * out \
+        + (2 * B * out if residual else 0)
+
+
+class DecodeStep:
+    """All GEMVs of one decode step with distinct weights per layer, as a list of zero-argument launches.
+    wfmt "int8": weight-only INT8 (per-row fp32 scales); "int4": GPTQ-style INT4 (int32 [N, K/8] packed weights,
+    fp16 group scales |N(0,1)| 0.02 + 1e-3 and 4-bit zero points uniform over [0, 15], group 128)."""
+
+    def __init__(self, B, device, seed=0, wfmt="int8"):
         from lfm2opt.kernels import ext
 
         E = ext()
@@ -65,6 +83,18 @@ class DecodeStep:
             W = torch.randint(-127, 128, (N, K), device=device, dtype=torch.int8, generator=g)
             s = torch.rand(N, device=device, generator=g) * 0.01 + 1e-3
             return W, s
+
+        def w4(N, K):
+            G = K // W4_GROUP
+            qw = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 8), device=device, dtype=torch.int32, generator=g)
+            sc = (torch.randn(N, G, device=device, generator=g).abs() * 0.02 + 1e-3).half()
+            qz = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, (G + 7) // 8), device=device, dtype=torch.int32,
+                               generator=g)
+            return qw, sc, qz
+
+        if wfmt == "int4":
+            self._init_w4(E, B, device, g, w4)
+            return
 
         self.x = torch.randn(B, H, device=device, generator=g).to(bf)       # normed residual stream
         self.mix = torch.randn(B, H, device=device, generator=g).to(bf)     # attention / conv output
@@ -102,6 +132,36 @@ class DecodeStep:
         self.weights += [Wh, sh]
         self.bytes = sum(b for _, _, b in self.ops)
         self.weight_bytes = sum(w.numel() * w.element_size() for w in self.weights if w.dtype == torch.int8)
+
+    def _init_w4(self, E, B, device, g, w4):
+        bf = torch.bfloat16
+        self.x = torch.randn(B, H, device=device, generator=g).to(bf)
+        self.mix = torch.randn(B, H, device=device, generator=g).to(bf)
+        self.h = torch.randn(B, H, device=device, generator=g).to(bf)
+        self.qkv = torch.empty(B, QKV, device=device, dtype=bf)
+        self.bcx = torch.empty(B, CONV_IN, device=device, dtype=bf)
+        self.act = torch.empty(B, FFN, device=device, dtype=bf)
+        self.logits = torch.empty(B, VOCAB, device=device, dtype=bf)
+        self.ops, self.weights = [], []
+
+        def op(kind, N, K, x, y, epi, out=None):
+            Wt = w4(N, K)
+            self.weights += list(Wt)
+            self.ops.append((kind, lambda Wt=Wt: E.gemv_w4z(*Wt, x, y, epi),
+                             w4_bytes(N, K, B, residual=epi == 2, out=out)))
+
+        for t in LAYER_TYPES:
+            if t == "A":
+                op("qkv", QKV, H, self.x, self.qkv, 0)
+                op("o+res", H, H, self.mix, self.h, 2)
+            else:
+                op("in", CONV_IN, H, self.x, self.bcx, 0)
+                op("out+res", H, H, self.mix, self.h, 2)
+            op("w1|w3+swiglu", 2 * FFN, H, self.x, self.act, 1, out=FFN)
+            op("w2+res", H, FFN, self.act, self.h, 2)
+        op("lm_head", VOCAB, H, self.x, self.logits, 0)
+        self.bytes = sum(b for _, _, b in self.ops)
+        self.weight_bytes = sum(w.numel() * w.element_size() for w in self.weights)
 
     def run(self, kinds=None):
         for kind, fn, _ in self.ops:
@@ -186,9 +246,9 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def decode_results(B, steps, warmup):
-    log(f"decode step, batch {B}: allocating weights")
-    step = DecodeStep(B, "cuda")
+def decode_results(B, steps, warmup, wfmt="int8"):
+    log(f"decode step ({wfmt}), batch {B}: allocating weights")
+    step = DecodeStep(B, "cuda", wfmt=wfmt)
     graph = capture(step.run)
     ms, wall = time_graph(graph, steps, warmup)
     res = {"batch": B, "ms_per_step": ms, "wall_ms_per_step": wall, "bytes_per_step": step.bytes,
@@ -204,7 +264,7 @@ def decode_results(B, steps, warmup):
                        "bytes_per_launch": kb // n}
         del g
     res["kinds"] = kinds
-    log(f"decode step, batch {B}: {ms * 1e3:.1f} us/step, {res['gbs']:.0f} GB/s")
+    log(f"decode step ({wfmt}), batch {B}: {ms * 1e3:.1f} us/step, {res['gbs']:.0f} GB/s")
     del graph, step
     torch.cuda.empty_cache()
     return res
@@ -241,29 +301,47 @@ def w8a8_results(reps):
             for W in Ws:
                 E.gemm_i8(xq, sx, W, sw, b, y, gelu)
 
-        g_full, g_gemm = capture(full), capture(gemm_only)
+        def int_mm():  # hipBLASLt's int8 GEMM with int32 output (no epilogue), the platform library's figure
+            for W in Ws:
+                torch._int_mm(xq, W.t())
+
+        g_full, g_gemm, g_lib = capture(full), capture(gemm_only), capture(int_mm)
         t_full, _ = time_graph(g_full, reps, 2)
         t_gemm, _ = time_graph(g_gemm, reps, 2)
-        us_full, us_gemm = t_full * 1e3 / ncopy, t_gemm * 1e3 / ncopy
+        t_lib, _ = time_graph(g_lib, reps, 2)
+        us_full, us_gemm, us_lib = t_full * 1e3 / ncopy, t_gemm * 1e3 / ncopy, t_lib * 1e3 / ncopy
         ops = 2.0 * M * N * K
         out.append({"name": name, "M": M, "K": K, "N": N, "bias": bias, "gelu": gelu,
                     "us_gemm": round(us_gemm, 2), "us_quant_gemm": round(us_full, 2),
                     "tops_gemm": round(ops / us_gemm / 1e6, 1), "tops_quant_gemm": round(ops / us_full / 1e6, 1),
-                    "mfma_frac_gemm": round(ops / us_gemm / 1e6 / INT8_PEAK_TOPS, 4)})
-        del g_full, g_gemm, Ws
+                    "mfma_frac_gemm": round(ops / us_gemm / 1e6 / INT8_PEAK_TOPS, 4),
+                    "us_hipblaslt_int_mm_i32": round(us_lib, 2), "tops_hipblaslt_int_mm_i32": round(ops / us_lib / 1e6, 1)})
+        del g_full, g_gemm, g_lib, Ws
         torch.cuda.empty_cache()
     return out
 
 
-def eager_kind(kind, B, reps):
-    """Counter-collection mode: the launches of one decode kind (or a plain 256 MiB device copy, kind "copy", the
+def eager_kind(kind, B, reps, wfmt="int8"):
+    """Counter-collection mode: the launches of one decode kind (of the `wfmt` decode step), one W8A8 GEMM shape
+    ("gemm:M,K,N", gemm kernel only, on one weight matrix) or a plain 256 MiB device copy (kind "copy", the
     calibration of the HBM byte counters) run eagerly, one kernel per dispatch, `reps` times over."""
     if kind == "copy":
         src = torch.randint(-127, 128, (256 << 20,), device="cuda", dtype=torch.int8)
         dst = torch.empty_like(src)
         fns, nbytes = [lambda: dst.copy_(src)], 2 * src.numel()
+    elif kind.startswith("gemm:"):
+        from lfm2opt.kernels import int8_ext
+
+        E8 = int8_ext()
+        M, K, N = (int(v) for v in kind[5:].split(","))
+        g = torch.Generator(device="cuda").manual_seed(M + K + N)
+        w = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+        xq = torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8, generator=g)
+        sx, sw = torch.rand(M, device="cuda", generator=g), torch.rand(N, device="cuda", generator=g) * 0.01
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        fns, nbytes = [lambda: E8.gemm_i8(xq, sx, w, sw, None, y, False)], M * K + N * K + 4 * (M + N) + 2 * M * N
     else:
-        step = DecodeStep(B, "cuda")
+        step = DecodeStep(B, "cuda", wfmt=wfmt)
         sel = [(fn, b) for k, fn, b in step.ops if k == kind]
         if not sel:
             raise SystemExit(f"unknown kind {kind!r}: one of {sorted(set(k for k, _, _ in step.ops))} or copy")
@@ -279,8 +357,8 @@ def eager_kind(kind, B, reps):
     t1.record()
     t1.synchronize()
     us = t0.elapsed_time(t1) * 1e3 / (reps * len(fns))
-    print(json.dumps({"kind": kind, "batch": B, "launches": reps * len(fns), "us_per_launch_eager": round(us, 2),
-                      "bytes_per_launch": nbytes}))
+    print(json.dumps({"kind": kind, "wfmt": wfmt, "batch": B, "launches": reps * len(fns),
+                      "us_per_launch_eager": round(us, 2), "bytes_per_launch": nbytes}))
 
 
 def main():
@@ -291,9 +369,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--batches", default="1,4,16", help="decode batch sizes to run (the first one is `value`)")
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 GEMM shapes")
+    ap.add_argument("--w4-batches", default="1,8", help="INT4 decode batch sizes ('' to skip)")
     ap.add_argument("--only-w8a8", action="store_true", help="W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--eager-kind", default=None,
-                    help="run one decode kind (e.g. 'w1|w3+swiglu') or 'copy' eagerly, for counter collection")
+                    help="run one decode kind (e.g. 'w1|w3+swiglu'), 'gemm:M,K,N' or 'copy' eagerly, for counter "
+                         "collection")
+    ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -301,7 +382,7 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
 
     if args.eager_kind:
-        eager_kind(args.eager_kind, int(args.batches.split(",")[0]), args.steps)
+        eager_kind(args.eager_kind, int(args.batches.split(",")[0]), args.steps, args.wfmt)
         return
     if args.only_w8a8:
         print(json.dumps({"w8a8_shapes": w8a8_results(max(5, args.steps // 10))}))
@@ -331,10 +412,13 @@ def main():
         "hbm_frac": round(res1["hbm_frac"], 4),
         "roofline": {"bound": "hbm", "kernel": "gemv_b1_kernel<int8,1,2,SWIGLU> (w1|w3 16384x2048 + SwiGLU)",
                      "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": W13_TRAFFIC_BYTES,
                      "us_per_launch": dom["us_per_launch"], "bytes_per_launch": dom["bytes_per_launch"]},
         "decode": {str(B): r for B, r in [(batches[0], res1)] + list(extra.items())},
     }
+    w4b = [int(b) for b in args.w4_batches.split(",") if b]
+    if w4b:
+        out["decode_w4"] = {str(B): decode_results(B, max(20, args.steps // 2), args.warmup, "int4") for B in w4b}
     if not args.no_w8a8:
         shapes = w8a8_results(max(5, args.steps // 10))
         ops = sum(2.0 * r["M"] * r["N"] * r["K"] for r in shapes)
@@ -342,7 +426,13 @@ def main():
         t_full = sum(r["us_quant_gemm"] for r in shapes)
         vis = [r for r in shapes if r["name"].startswith("vision")]
         vops = sum(2.0 * r["M"] * r["N"] * r["K"] for r in vis)
+        t_lib = sum(r["us_hipblaslt_int_mm_i32"] for r in shapes)
+        big = next(r for r in shapes if r["M"] == 4096 and r["N"] == 16384)
         out["w8a8"] = {"unit": "TOPS", "peak": INT8_PEAK_TOPS,
+                       "roofline": {"bound": "mfma", "kernel": "gemm_i8_big_kernel<0,128,2> (4096 x 2048 x 16384)",
+                                    "achieved": big["tops_gemm"], "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                                    "frac": round(big["tops_gemm"] / INT8_PEAK_TOPS, 4)},
+                       "all_shapes_tops_hipblaslt_int_mm_i32": round(ops / t_lib / 1e6, 1),
                        "all_shapes_tops_gemm": round(ops / t_gemm / 1e6, 1),
                        "all_shapes_tops_quant_gemm": round(ops / t_full / 1e6, 1),
                        "vision_layer_tops_gemm": round(vops / sum(r["us_gemm"] for r in vis) / 1e6, 1),

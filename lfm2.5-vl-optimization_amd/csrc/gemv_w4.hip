@@ -85,23 +85,9 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
     int n = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (n >= N) return;  // no block-level synchronization in this kernel
 
-    uint32_t xp[CPL][16];  // activation pairs, word-major: xp[u][4 j + p] = (x[8 j + p], x[8 j + p + 4])
-    float xs[CPL];
     int gl[CPL];  // group of the lane's chunk u (clamped for chunks past K)
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) {
-        const int c = lane + 64 * u;
-        xs[u] = 0.f;
-        gl[u] = min(32 * c / group, G - 1);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const v4i d = c < C ? ld16(x + (size_t)c * 32 + 8 * j) : v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int p = 0; p < 4; ++p) xp[u][4 * j + p] = xpair(d, p);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) xs[u] += bf2f_lo((uint32_t)d[e]) + bf2f_hi((uint32_t)d[e]);
-        }
-    }
+    for (int u = 0; u < CPL; ++u) gl[u] = min(32 * (lane + 64 * u) / group, G - 1);
     const uint32_t rowb = (uint32_t)K / 2;
     struct Item {
         v4i w[CPL][NROW];
@@ -124,6 +110,27 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
         }
         if (EPI == EPI_RESIDUAL) it.h = y[rc];
     };
+    // the first rows' weights are requested before the activations are repacked, so the two memory latencies
+    // overlap instead of adding up
+    Item buf[NB];
+#pragma unroll
+    for (int j = 0; j < NB - 1; ++j) load(buf[j], n + j * nw);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t xp[CPL][16];  // activation pairs, word-major: xp[u][4 j + p] = (x[8 j + p], x[8 j + p + 4])
+    float xs[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+        const int c = lane + 64 * u;
+        xs[u] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const v4i d = c < C ? ld16(x + (size_t)c * 32 + 8 * j) : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) xp[u][4 * j + p] = xpair(d, p);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xs[u] += bf2f_lo((uint32_t)d[e]) + bf2f_hi((uint32_t)d[e]);
+        }
+    }
     auto finish = [&](const Item &it, int row) {
         float acc[NROW];
 #pragma unroll
@@ -145,9 +152,6 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
         const float v = epi_value(EPI, acc[0], acc[NROW - 1], EPI == EPI_RESIDUAL ? it.h : 0u);
         if (lane == 0) y[row] = (uint16_t)f2bf(v);
     };
-    Item buf[NB];
-#pragma unroll
-    for (int j = 0; j < NB - 1; ++j) load(buf[j], n + j * nw);
     bool more = true;
     while (more) {
 #pragma unroll
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
 template <int FMT, int EPI>
 void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int N, int K,
                   int group, hipStream_t st) {
-    static const int wpc = env_int("LFM2Q_GEMV_WPC", 8);
+    static const int wpc = env_int("LFM2Q_W4_WPC", 8);
     const int C = K / 32;
     const int blocks = std::min((N + 3) / 4, std::max(1, device_cus() * wpc / 4));
     const dim3 grid(blocks);
@@ -295,8 +299,8 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
         gemv_w4_b1_kernel<FMT, 4, EPI><<<grid, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
 }
 
-// NWK: the smallest of 1, 2, 4, 8 dividing the 128-k steps that gives >= 1024 wavefronts per 16-row tile count,
-// else the largest that divides (narrow outputs split K wider to fill 256 CUs). RT: 16-row tiles per workgroup, 4 for outputs of 32768+ rows
+// NWK: the smallest of 1, 2, 4, 8 dividing the 128-k steps with (16-row weight tiles) x NWK >= 4096, else the largest
+// that divides: 2048+ wavefronts even when a SwiGLU workgroup holds two tiles (8 per CU, the streaming optimum). RT: 16-row tiles per workgroup, 4 for outputs of 32768+ rows
 // (not with SwiGLU, whose tile pairs double the registers), else 1.
 template <int FMT, int EPI>
 void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int B, int N,
@@ -311,7 +315,7 @@ void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uin
     for (int c = 1; c <= 8; c <<= 1)
         if (steps % c == 0) {
             nwk = c;
-            if (tiles16 * c >= 1024) break;
+            if (tiles16 * c >= 4096) break;
         }
     const dim3 grid(wgs);
 #define LFM2Q_W4M(RT_, NWK_)                                                                                         \
