@@ -446,26 +446,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 }
 
 // ------------------------------------------------------------------------------------------------ quant_rows
-// One wavefront per row: s = max(amax, 1e-8) / 127 (IEEE division), q = clamp(rint(x / s), -127, 127) with
-// round-half-even. x / s is evaluated as x * (1 / s) unless that product lies within 2^-12 of a half-integer,
-// where the correctly rounded quotient is computed instead: |x / s| <= 127 keeps the product within 2 ulp
-// (< 2^-15) of the true quotient, so outside that band both round to the same integer and the result is the
-// true-division one bit for bit.
-__device__ __forceinline__ int quant1(float v, float s, float r) {
-    float t = v * r;
+// One wavefront per row: s = max(amax, 1e-8) / 127 (IEEE division), q = rint(x / s) with round-half-even (the
+// reference's integer clamp to [-127, 127] never binds: |x| <= amax keeps |x / s| < 127.5). x / s is evaluated as
+// t = x * fl(1 / s): two roundings put t within 127.5 * 2^-23 < 2^-16 of the real quotient, and the correctly rounded
+// quotient fl(x / s) is within half an ulp (<= 2^-17) of it, so unless t lies within 2^-15 of a half-integer, rint(t)
+// and rint(fl(x / s)) are the same integer. Near a half-integer the IEEE quotient itself is computed; that test runs
+// per 8 values and the division only when one of them needs it (about one vector in 2000).
+__device__ __forceinline__ bool near_half(float t) {
     const float f = t - floorf(t);
-    if (fabsf(f - 0.5f) < 0.000244140625f) t = v / s;
-    return (int)fminf(fmaxf(rintf(t), -127.f), 127.f);
+    return fabsf(f - 0.5f) < 0.000030517578125f;  // 2^-15
 }
 
 // 8 bf16 (one 16-byte vector) -> 8 int8 packed in two dwords
 __device__ __forceinline__ void quant8(v4i xv, float s, float r, int &lo, int &hi) {
-    int q[8];
+    float v[8], t[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        q[2 * j] = quant1(bf2f_lo((uint32_t)xv[j]), s, r);
-        q[2 * j + 1] = quant1(bf2f_hi((uint32_t)xv[j]), s, r);
+        v[2 * j] = bf2f_lo((uint32_t)xv[j]);
+        v[2 * j + 1] = bf2f_hi((uint32_t)xv[j]);
     }
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        t[e] = v[e] * r;
+        any |= near_half(t[e]);
+    }
+    if (__builtin_expect(any, 0)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (near_half(t[e])) t[e] = v[e] / s;
+    }
+    int q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = (int)rintf(t[e]);
     lo = (q[0] & 255) | ((q[1] & 255) << 8) | ((q[2] & 255) << 16) | ((q[3] & 255) << 24);
     hi = (q[4] & 255) | ((q[5] & 255) << 8) | ((q[6] & 255) << 16) | ((q[7] & 255) << 24);
 }
@@ -476,8 +489,9 @@ __device__ __forceinline__ float absmax8(v4i xv, float m) {
     return m;
 }
 
-// rows of K bf16, K % 8 == 0. CH > 0: K = 512 CH exactly, the row stays in registers (CH 16-byte vectors per lane);
-// CH == 0: any K, two passes over the row (the second one hits the cache).
+// rows of K bf16, K % 8 == 0. CH > 0: K <= 512 CH, the row stays in registers (CH 16-byte vectors per lane, the last
+// ones masked), one read and one write of the row; CH == 0: any K, two passes over the row (the second one hits the
+// cache).
 template <int CH>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restrict__ x, int8_t *__restrict__ q,
                                                          float *__restrict__ s, int rows, int K) {
@@ -486,23 +500,29 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restr
     if (row >= rows) return;
     const uint16_t *xr = x + (size_t)row * K;
     int8_t *qr = q + (size_t)row * K;
+    const int C = K / 8;  // 16-byte vectors in the row
     if constexpr (CH > 0) {
         v4i v[CH];
         float m = 0.f;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) v[c] = ld_nt16(xr + (size_t)(c * 64 + lane) * 8);
+        for (int c = 0; c < CH; ++c) {
+            const int i = c * 64 + lane;
+            v[c] = i < C ? ld_nt16(xr + (size_t)i * 8) : v4i{0, 0, 0, 0};
+        }
 #pragma unroll
         for (int c = 0; c < CH; ++c) m = absmax8(v[c], m);
         const float sc = fmaxf(wave_max(m), 1e-8f) / 127.f, rc = 1.f / sc;
         if (lane == 0) s[row] = sc;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            int lo, hi;
-            quant8(v[c], sc, rc, lo, hi);
-            *reinterpret_cast<int2 *>(qr + (size_t)(c * 64 + lane) * 8) = make_int2(lo, hi);
+            const int i = c * 64 + lane;
+            if (i < C) {
+                int lo, hi;
+                quant8(v[c], sc, rc, lo, hi);
+                *reinterpret_cast<int2 *>(qr + (size_t)i * 8) = make_int2(lo, hi);
+            }
         }
     } else {
-        const int C = K / 8;
         float m = 0.f;
         for (int c = lane; c < C; c += 64) m = absmax8(ld16(xr + (size_t)c * 8), m);
         const float sc = fmaxf(wave_max(m), 1e-8f) / 127.f, rc = 1.f / sc;
@@ -621,12 +641,13 @@ extern "C" int lfm2q_quant_rows(const lfm2q_bf16 *x, int8_t *q, float *s, int ro
                   "quant_rows: x must be 16-byte and q 8-byte aligned");
     const dim3 grid((rows + 3) / 4);
     hipStream_t st = (hipStream_t)stream;
-    switch (K % 512 == 0 ? K / 512 : 0) {
-        case 1: quant_rows_kernel<1><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
-        case 2: quant_rows_kernel<2><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
-        case 4: quant_rows_kernel<4><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
-        case 8: quant_rows_kernel<8><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
-        case 16: quant_rows_kernel<16><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
+    // vectors per lane with the row in registers (K <= 8192); longer rows take the two-pass kernel
+    switch ((K + 511) / 512) {
+#define LFM2Q_QR(CH_) \
+    case CH_: quant_rows_kernel<CH_><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
+        LFM2Q_QR(1) LFM2Q_QR(2) LFM2Q_QR(3) LFM2Q_QR(4) LFM2Q_QR(5) LFM2Q_QR(6) LFM2Q_QR(7) LFM2Q_QR(8)
+        LFM2Q_QR(9) LFM2Q_QR(10) LFM2Q_QR(11) LFM2Q_QR(12) LFM2Q_QR(13) LFM2Q_QR(14) LFM2Q_QR(15) LFM2Q_QR(16)
+#undef LFM2Q_QR
         default: quant_rows_kernel<0><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
     }
     return launch_status("quant_rows");
