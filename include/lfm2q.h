@@ -98,6 +98,31 @@ int lfm2q_silu_mul(const lfm2q_bf16 *g, lfm2q_bf16 *y, int B, int I, lfm2q_strea
  * Replaces launch_quant_rows kernels/int8_gemm.cu:822-825 (bound as quant_rows(), kernels/int8_gemm.cpp:83-96). */
 int lfm2q_quant_rows(const lfm2q_bf16 *x, int8_t *q, float *s, int rows, int K, lfm2q_stream_t stream);
 
+/* Grouped activation quantization: one scale per row and group of 64 columns, sT[g, r] = max(max |x[r, 64 g ..
+ * 64 g + 63]|, 1e-8) / 127 written transposed (sT fp32 [K/64, rows]), q as in lfm2q_quant_rows with that scale;
+ * K % 64 == 0. Replaces launch_quant_groups kernels/int8_gemm.cu:435-474 (quant_rows() with a 2-D s,
+ * kernels/int8_gemm.cpp:83-96, which also requires K % 128 == 0). */
+int lfm2q_quant_groups(const lfm2q_bf16 *x, int8_t *q, float *sT, int rows, int K, lfm2q_stream_t stream);
+
+/* Fused INT8 producers. Each computes a bf16 row x and quantizes it into q [rows, L] with per-row scales s [rows]
+ * (grouped == 0) or per-row-and-64-column scales sT [L/64, rows] (grouped != 0), bit-identically to
+ * lfm2q_quant_rows / lfm2q_quant_groups of x; x itself is also written when the x pointer is not NULL.
+ * Row length L <= 8192, L % 8 == 0 (L % 64 == 0 when grouped).
+ * add_rmsnorm_q (L = H): if y != NULL, h = bf16(h + y) in place; x = bf16(w * bf16(h * rs)),
+ *   rs = 1 / sqrt(sum(h^2) / H + eps). Replaces launch_add_rmsnorm_q kernels/int8_gemm.cu:590-642 (binding
+ *   add_rmsnorm_q(), kernels/int8_gemm.cpp:122-132). */
+int lfm2q_add_rmsnorm_q(lfm2q_bf16 *h, const lfm2q_bf16 *y, const lfm2q_bf16 *w, int8_t *q, float *s,
+                        lfm2q_bf16 *x, int rows, int H, float eps, int grouped, lfm2q_stream_t stream);
+/* add_layernorm_q (L = D): if y != NULL, h = bf16(h + y) in place; x = bf16(((h - mean) * rstd) * w + b),
+ * rstd = 1 / sqrt(sum((h - mean)^2) / D + eps). Replaces launch_add_layernorm_q kernels/int8_gemm.cu:529-585 (binding
+ * add_layernorm_q(), kernels/int8_gemm.cpp:108-119, which requires D % 128 == 0 and D <= 2048). */
+int lfm2q_add_layernorm_q(lfm2q_bf16 *h, const lfm2q_bf16 *y, const lfm2q_bf16 *w, const lfm2q_bf16 *b, int8_t *q,
+                          float *s, lfm2q_bf16 *x, int rows, int D, float eps, int grouped, lfm2q_stream_t stream);
+/* silu_mul_q (L = I): g bf16 [rows, 2I] = w1 | w3 outputs, x = bf16(bf16(silu(g1)) * g3) exactly as lfm2q_silu_mul.
+ * Replaces launch_silu_mul_q kernels/int8_gemm.cu:646-682 (binding silu_mul_q(), kernels/int8_gemm.cpp:135-141). */
+int lfm2q_silu_mul_q(const lfm2q_bf16 *g, int8_t *q, float *s, lfm2q_bf16 *x, int rows, int I, int grouped,
+                     lfm2q_stream_t stream);
+
 /* W8A8 GEMM with the dequant epilogue: Y[m, n] = bf16( g( ((float)acc[m, n] * sa[m]) * sb[n] + bias[n] ) ),
  * acc[m, n] = sum_k A[m, k] B[n, k] exact in int32, the three fp32 operations separately rounded (no FMA),
  * g = GELU (tanh approximation) if gelu != 0, else identity. A int8 [M, K], sa fp32 [M], B int8 [N, K],

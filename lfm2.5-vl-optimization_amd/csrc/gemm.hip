@@ -9,11 +9,11 @@
 // ds_read_b128 phase reads at one logical chunk, and the 8 chunks a ds_write_b128 phase writes, fall in 8 distinct
 // 16-byte bank groups. M, N and K tails are zero-filled at load time (K % 16 == 0); stores are predicated.
 //
-// Activation quantization is its own memory-bound kernel (quant_rows_kernel): quantizing inside the GEMM's main
-// loop would redo the per-element VALU work once per N tile, about twice the MFMA time of the tile.
+// Activation quantization is its own memory-bound kernel (quant.hip): quantizing inside the GEMM's main loop would
+// redo the per-element VALU work once per N tile, about twice the MFMA time of the tile.
 //
 // Reference: kernels/int8_gemm.cu:125-297 (gemm_i8_kernel, per-token path), :93-115 (store_tile epilogue),
-// :391-432 (quant_rows_kernel), :690-702 (pick_bm); bound as gemm_i8 / quant_rows in kernels/int8_gemm.cpp.
+// :690-702 (pick_bm); bound as gemm_i8 in kernels/int8_gemm.cpp.
 #include "common.hpp"
 #include "status.hpp"
 
@@ -445,96 +445,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                           smem + wave * stage_bytes<TN>());
 }
 
-// ------------------------------------------------------------------------------------------------ quant_rows
-// One wavefront per row: s = max(amax, 1e-8) / 127 (IEEE division), q = rint(x / s) with round-half-even (the
-// reference's integer clamp to [-127, 127] never binds: |x| <= amax keeps |x / s| < 127.5). x / s is evaluated as
-// t = x * fl(1 / s): two roundings put t within 127.5 * 2^-23 < 2^-16 of the real quotient, and the correctly rounded
-// quotient fl(x / s) is within half an ulp (<= 2^-17) of it, so unless t lies within 2^-15 of a half-integer, rint(t)
-// and rint(fl(x / s)) are the same integer. Near a half-integer the IEEE quotient itself is computed; that test runs
-// per 8 values and the division only when one of them needs it (about one vector in 2000).
-__device__ __forceinline__ bool near_half(float t) {
-    const float f = t - floorf(t);
-    return fabsf(f - 0.5f) < 0.000030517578125f;  // 2^-15
-}
-
-// 8 bf16 (one 16-byte vector) -> 8 int8 packed in two dwords
-__device__ __forceinline__ void quant8(v4i xv, float s, float r, int &lo, int &hi) {
-    float v[8], t[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        v[2 * j] = bf2f_lo((uint32_t)xv[j]);
-        v[2 * j + 1] = bf2f_hi((uint32_t)xv[j]);
-    }
-    bool any = false;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        t[e] = v[e] * r;
-        any |= near_half(t[e]);
-    }
-    if (__builtin_expect(any, 0)) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            if (near_half(t[e])) t[e] = v[e] / s;
-    }
-    int q[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) q[e] = (int)rintf(t[e]);
-    lo = (q[0] & 255) | ((q[1] & 255) << 8) | ((q[2] & 255) << 16) | ((q[3] & 255) << 24);
-    hi = (q[4] & 255) | ((q[5] & 255) << 8) | ((q[6] & 255) << 16) | ((q[7] & 255) << 24);
-}
-
-__device__ __forceinline__ float absmax8(v4i xv, float m) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf2f_lo((uint32_t)xv[j])), fabsf(bf2f_hi((uint32_t)xv[j]))));
-    return m;
-}
-
-// rows of K bf16, K % 8 == 0. CH > 0: K <= 512 CH, the row stays in registers (CH 16-byte vectors per lane, the last
-// ones masked), one read and one write of the row; CH == 0: any K, two passes over the row (the second one hits the
-// cache).
-template <int CH>
-__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restrict__ x, int8_t *__restrict__ q,
-                                                         float *__restrict__ s, int rows, int K) {
-    const int lane = threadIdx.x & 63;
-    const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    if (row >= rows) return;
-    const uint16_t *xr = x + (size_t)row * K;
-    int8_t *qr = q + (size_t)row * K;
-    const int C = K / 8;  // 16-byte vectors in the row
-    if constexpr (CH > 0) {
-        v4i v[CH];
-        float m = 0.f;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int i = c * 64 + lane;
-            v[c] = i < C ? ld_nt16(xr + (size_t)i * 8) : v4i{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int c = 0; c < CH; ++c) m = absmax8(v[c], m);
-        const float sc = fmaxf(wave_max(m), 1e-8f) / 127.f, rc = 1.f / sc;
-        if (lane == 0) s[row] = sc;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int i = c * 64 + lane;
-            if (i < C) {
-                int lo, hi;
-                quant8(v[c], sc, rc, lo, hi);
-                *reinterpret_cast<int2 *>(qr + (size_t)i * 8) = make_int2(lo, hi);
-            }
-        }
-    } else {
-        float m = 0.f;
-        for (int c = lane; c < C; c += 64) m = absmax8(ld16(xr + (size_t)c * 8), m);
-        const float sc = fmaxf(wave_max(m), 1e-8f) / 127.f, rc = 1.f / sc;
-        if (lane == 0) s[row] = sc;
-        for (int c = lane; c < C; c += 64) {
-            int lo, hi;
-            quant8(ld16(xr + (size_t)c * 8), sc, rc, lo, hi);
-            *reinterpret_cast<int2 *>(qr + (size_t)c * 8) = make_int2(lo, hi);
-        }
-    }
-}
-
 // ------------------------------------------------------------------------------------------------ dispatch
 // Tile choice by a two-term cost model fitted to MI355X timings of the seven configurations over the LFM2 prefill and
 // SigLIP2 vision shapes: with `per` = ceil(tiles / CUs) tiles on the busiest CU, time ~ a x per x BM x BN x K (the
@@ -633,22 +543,3 @@ extern "C" int lfm2q_gemm_i8_i32(const int8_t *A, const int8_t *B, int32_t *C, i
     return launch_status("gemm_i8_i32");
 }
 
-extern "C" int lfm2q_quant_rows(const lfm2q_bf16 *x, int8_t *q, float *s, int rows, int K, lfm2q_stream_t stream) {
-    LFM2Q_REQUIRE(x && q && s, LFM2Q_ERR_ARG, "quant_rows: null pointer");
-    LFM2Q_REQUIRE(rows >= 1 && K >= 8 && K % 8 == 0, LFM2Q_ERR_SHAPE,
-                  "quant_rows: K must be a multiple of 8 (rows=%d K=%d)", rows, K);
-    LFM2Q_REQUIRE(aligned16(x) && ((uintptr_t)q & 7) == 0, LFM2Q_ERR_ALIGN,
-                  "quant_rows: x must be 16-byte and q 8-byte aligned");
-    const dim3 grid((rows + 3) / 4);
-    hipStream_t st = (hipStream_t)stream;
-    // vectors per lane with the row in registers (K <= 8192); longer rows take the two-pass kernel
-    switch ((K + 511) / 512) {
-#define LFM2Q_QR(CH_) \
-    case CH_: quant_rows_kernel<CH_><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
-        LFM2Q_QR(1) LFM2Q_QR(2) LFM2Q_QR(3) LFM2Q_QR(4) LFM2Q_QR(5) LFM2Q_QR(6) LFM2Q_QR(7) LFM2Q_QR(8)
-        LFM2Q_QR(9) LFM2Q_QR(10) LFM2Q_QR(11) LFM2Q_QR(12) LFM2Q_QR(13) LFM2Q_QR(14) LFM2Q_QR(15) LFM2Q_QR(16)
-#undef LFM2Q_QR
-        default: quant_rows_kernel<0><<<grid, 256, 0, st>>>(x, q, s, rows, K); break;
-    }
-    return launch_status("quant_rows");
-}

@@ -1,0 +1,423 @@
+// Activation quantization for the W8A8 GEMM on gfx950 and the fused producers that emit its INT8 input directly:
+//   quant_rows      s = max(amax, 1e-8) / 127 per row,            q = rint(x / s)
+//   quant_groups    the same per row and group of 64 columns, scales written transposed sT[K/64][rows]
+//   add_rmsnorm_q   h = bf16(h + y); x = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))           -> quantized x
+//   add_layernorm_q h = bf16(h + y); x = bf16(((h - mean) * rstd) * w + b)                    -> quantized x
+//   silu_mul_q      x = bf16(bf16(silu(g1)) * g3) on g = [g1 | g3], exactly lfm2q_silu_mul's -> quantized x
+// One wavefront per row, the row in registers: lane l holds the 16-byte vectors c * 64 + l (c < CH, 8 bf16 each) of
+// the row, so a row of up to 8192 values takes one read and one write. Every producer can also write its bf16 x:
+// the INT8 output is then bit-identical to quant_rows / quant_groups of that x (the same quantizer code runs on the
+// same bf16 values), which is the reference's own test of the fused kernels.
+//
+// Reference: kernels/int8_gemm.cu:391-474 (quant_rows_kernel, quant_groups_kernel), :491-682 (warp_quant_store,
+// add_layernorm_q_kernel, add_rmsnorm_q_kernel, silu_mul_q_kernel); bf16 forms kernels/lfm2_decode.cu:96-121
+// (add_rmsnorm), kernels/vision_ops.cu:29-80 (add_layernorm); bound in kernels/int8_gemm.cpp:83-141.
+#include "common.hpp"
+#include "status.hpp"
+
+#include <algorithm>
+
+namespace lfm2q {
+namespace {
+
+// ------------------------------------------------------------------------------------------------ quantizer
+// q = rint(x / s) with round-half-even (the reference's integer clamp to [-127, 127] never binds: |x| <= amax keeps
+// |x / s| < 127.5). x / s is evaluated as t = x * fl(1 / s): two roundings put t within 127.5 * 2^-23 < 2^-16 of the
+// real quotient, and the correctly rounded quotient fl(x / s) is within half an ulp (<= 2^-17) of it, so unless t
+// lies within 2^-15 of a half-integer, rint(t) and rint(fl(x / s)) are the same integer. Near a half-integer the
+// IEEE quotient itself is computed; the test runs per 8 values and the division only when one of them needs it.
+__device__ __forceinline__ bool near_half(float t) {
+    const float f = t - floorf(t);
+    return fabsf(f - 0.5f) < 0.000030517578125f;  // 2^-15
+}
+
+// 8 bf16 (one 16-byte vector) -> 8 int8 packed in two dwords
+__device__ __forceinline__ void quant8(v4i xv, float s, float r, int &lo, int &hi) {
+    float v[8], t[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[2 * j] = bf2f_lo((uint32_t)xv[j]);
+        v[2 * j + 1] = bf2f_hi((uint32_t)xv[j]);
+    }
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        t[e] = v[e] * r;
+        any |= near_half(t[e]);
+    }
+    if (__builtin_expect(any, 0)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (near_half(t[e])) t[e] = v[e] / s;
+    }
+    int q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = (int)rintf(t[e]);
+    lo = (q[0] & 255) | ((q[1] & 255) << 8) | ((q[2] & 255) << 16) | ((q[3] & 255) << 24);
+    hi = (q[4] & 255) | ((q[5] & 255) << 8) | ((q[6] & 255) << 16) | ((q[7] & 255) << 24);
+}
+
+__device__ __forceinline__ float absmax8(v4i xv, float m) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf2f_lo((uint32_t)xv[j])), fabsf(bf2f_hi((uint32_t)xv[j]))));
+    return m;
+}
+
+__device__ __forceinline__ float scale_of(float amax) { return fmaxf(amax, 1e-8f) / 127.f; }
+
+// Quantize one row held as above (C = vectors in the row; lanes past it hold zeros) into qr and its scale(s):
+// GROUPED = false: one scale s[row]; true: one scale per 64 columns, i.e. per 8 consecutive lanes of a vector index
+// c, written to s[g * rows + row] (g = the group's index in the row).
+template <int CH, bool GROUPED>
+__device__ __forceinline__ void quant_store(const v4i (&v)[CH], int C, int8_t *__restrict__ qr, float *__restrict__ s,
+                                            int row, int rows, int lane) {
+    float sc_row = 0.f, rc_row = 0.f;
+    if (!GROUPED) {
+        float m = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) m = absmax8(v[c], m);
+        sc_row = scale_of(wave_max(m));
+        rc_row = 1.f / sc_row;
+        if (lane == 0) s[row] = sc_row;
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        float sc = sc_row, rc = rc_row;
+        if (GROUPED) {
+            float m = absmax8(v[c], 0.f);
+            m = fmaxf(m, __shfl_xor(m, 1));
+            m = fmaxf(m, __shfl_xor(m, 2));
+            m = fmaxf(m, __shfl_xor(m, 4));
+            sc = scale_of(m);
+            rc = 1.f / sc;
+            if (i < C && (lane & 7) == 0) s[(size_t)(i >> 3) * rows + row] = sc;
+        }
+        if (i < C) {
+            int lo, hi;
+            quant8(v[c], sc, rc, lo, hi);
+            *reinterpret_cast<int2 *>(qr + (size_t)i * 8) = make_int2(lo, hi);
+        }
+    }
+}
+
+__device__ __forceinline__ int row_of_wave() {
+    return __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+}
+
+// ------------------------------------------------------------------------------------------------ quant_rows / groups
+// CH > 0: K <= 512 CH, the row in registers. CH == 0: longer rows; per-row scales take two passes over the row (the
+// second one hits the cache), grouped scales one (64 lanes x one vector = 8 whole groups per step).
+template <int CH, bool GROUPED>
+__global__ __launch_bounds__(256) void quant_kernel(const uint16_t *__restrict__ x, int8_t *__restrict__ q,
+                                                    float *__restrict__ s, int rows, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = row_of_wave();
+    if (row >= rows) return;
+    const uint16_t *xr = x + (size_t)row * K;
+    int8_t *qr = q + (size_t)row * K;
+    const int C = K / 8;
+    if constexpr (CH > 0) {
+        v4i v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int i = c * 64 + lane;
+            v[c] = i < C ? ld_nt16(xr + (size_t)i * 8) : v4i{0, 0, 0, 0};
+        }
+        quant_store<CH, GROUPED>(v, C, qr, s, row, rows, lane);
+    } else if constexpr (GROUPED) {
+        for (int c0 = 0; c0 < C; c0 += 64) {
+            const int i = c0 + lane;
+            const v4i v[1] = {i < C ? ld16(xr + (size_t)i * 8) : v4i{0, 0, 0, 0}};
+            quant_store<1, true>(v, C - c0, qr + (size_t)c0 * 8, s + (size_t)(c0 >> 3) * rows, row, rows, lane);
+        }
+    } else {
+        float m = 0.f;
+        for (int c = lane; c < C; c += 64) m = absmax8(ld16(xr + (size_t)c * 8), m);
+        const float sc = scale_of(wave_max(m)), rc = 1.f / sc;
+        if (lane == 0) s[row] = sc;
+        for (int c = lane; c < C; c += 64) {
+            int lo, hi;
+            quant8(ld16(xr + (size_t)c * 8), sc, rc, lo, hi);
+            *reinterpret_cast<int2 *>(qr + (size_t)c * 8) = make_int2(lo, hi);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ producers
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// row (+ residual) -> registers. ADD: h = bf16(h + y), written back. Lanes past the row get zeros.
+template <int CH>
+__device__ __forceinline__ void load_row_add(uint16_t *__restrict__ hr, const uint16_t *__restrict__ yr, int C,
+                                             int lane, v4i (&hv)[CH]) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        hv[c] = v4i{0, 0, 0, 0};
+        if (i < C) {
+            hv[c] = ld16(hr + (size_t)i * 8);
+            if (yr) {
+                const v4i yv = ld16(yr + (size_t)i * 8);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    hv[c][j] = (int)pack2(bf2f_lo((uint32_t)hv[c][j]) + bf2f_lo((uint32_t)yv[j]),
+                                          bf2f_hi((uint32_t)hv[c][j]) + bf2f_hi((uint32_t)yv[j]));
+                *reinterpret_cast<v4i *>(hr + (size_t)i * 8) = hv[c];
+            }
+        }
+    }
+}
+
+template <int CH>
+__device__ __forceinline__ void store_row(uint16_t *__restrict__ xr, const v4i (&xv)[CH], int C, int lane) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        if (i < C) *reinterpret_cast<v4i *>(xr + (size_t)i * 8) = xv[c];
+    }
+}
+
+template <int CH, bool GROUPED>
+__global__ __launch_bounds__(256) void add_rmsnorm_q_kernel(uint16_t *__restrict__ h, const uint16_t *__restrict__ y,
+                                                            const uint16_t *__restrict__ w, int8_t *__restrict__ q,
+                                                            float *__restrict__ s, uint16_t *__restrict__ xo, int rows,
+                                                            int H, float eps) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int row = row_of_wave();
+    if (row >= rows) return;
+    const int C = H / 8;
+    v4i hv[CH];
+    load_row_add<CH>(h + (size_t)row * H, y ? y + (size_t)row * H : nullptr, C, lane, hv);
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float a = bf2f_lo((uint32_t)hv[c][j]), b = bf2f_hi((uint32_t)hv[c][j]);
+            ss += a * a;
+            ss += b * b;
+        }
+    ss = wave_sum(ss);
+    const float rs = 1.f / sqrtf(ss / (float)H + eps);
+    v4i xv[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        xv[c] = v4i{0, 0, 0, 0};
+        if (i < C) {
+            const v4i wv = ld16(w + (size_t)i * 8);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xv[c][j] = (int)pack2(bf2f_lo((uint32_t)wv[j]) * rbf(bf2f_lo((uint32_t)hv[c][j]) * rs),
+                                      bf2f_hi((uint32_t)wv[j]) * rbf(bf2f_hi((uint32_t)hv[c][j]) * rs));
+        }
+    }
+    if (xo) store_row<CH>(xo + (size_t)row * H, xv, C, lane);
+    quant_store<CH, GROUPED>(xv, C, q + (size_t)row * H, s, row, rows, lane);
+}
+
+template <int CH, bool GROUPED>
+__global__ __launch_bounds__(256) void add_layernorm_q_kernel(uint16_t *__restrict__ h,
+                                                              const uint16_t *__restrict__ y,
+                                                              const uint16_t *__restrict__ w,
+                                                              const uint16_t *__restrict__ b, int8_t *__restrict__ q,
+                                                              float *__restrict__ s, uint16_t *__restrict__ xo,
+                                                              int rows, int D, float eps) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int row = row_of_wave();
+    if (row >= rows) return;
+    const int C = D / 8;
+    v4i hv[CH];
+    load_row_add<CH>(h + (size_t)row * D, y ? y + (size_t)row * D : nullptr, C, lane, hv);
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sum += bf2f_lo((uint32_t)hv[c][j]) + bf2f_hi((uint32_t)hv[c][j]);
+    const float mean = wave_sum(sum) / (float)D;
+    float qs = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        if (c * 64 + lane < C) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float a = bf2f_lo((uint32_t)hv[c][j]) - mean, d = bf2f_hi((uint32_t)hv[c][j]) - mean;
+                qs += a * a;
+                qs += d * d;
+            }
+        }
+    }
+    const float rstd = 1.f / sqrtf(wave_sum(qs) / (float)D + eps);
+    v4i xv[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        xv[c] = v4i{0, 0, 0, 0};
+        if (i < C) {
+            const v4i wv = ld16(w + (size_t)i * 8), bv = ld16(b + (size_t)i * 8);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float lo = ((bf2f_lo((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_lo((uint32_t)wv[j]);
+                const float hi = ((bf2f_hi((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_hi((uint32_t)wv[j]);
+                xv[c][j] = (int)pack2(lo + bf2f_lo((uint32_t)bv[j]), hi + bf2f_hi((uint32_t)bv[j]));
+            }
+        }
+    }
+    if (xo) store_row<CH>(xo + (size_t)row * D, xv, C, lane);
+    quant_store<CH, GROUPED>(xv, C, q + (size_t)row * D, s, row, rows, lane);
+}
+
+template <int CH, bool GROUPED>
+__global__ __launch_bounds__(256) void silu_mul_q_kernel(const uint16_t *__restrict__ g, int8_t *__restrict__ q,
+                                                         float *__restrict__ s, uint16_t *__restrict__ xo, int rows,
+                                                         int I) {
+    const int lane = threadIdx.x & 63;
+    const int row = row_of_wave();
+    if (row >= rows) return;
+    const int C = I / 8;
+    const uint16_t *gr = g + (size_t)row * 2 * I;
+    v4i xv[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        xv[c] = v4i{0, 0, 0, 0};
+        if (i < C) {
+            const v4i av = ld_nt16(gr + (size_t)i * 8), uv = ld_nt16(gr + I + (size_t)i * 8);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xv[c][j] = (int)pack2(rbf(silu_f32(bf2f_lo((uint32_t)av[j]))) * bf2f_lo((uint32_t)uv[j]),
+                                      rbf(silu_f32(bf2f_hi((uint32_t)av[j]))) * bf2f_hi((uint32_t)uv[j]));
+        }
+    }
+    if (xo) store_row<CH>(xo + (size_t)row * I, xv, C, lane);
+    quant_store<CH, GROUPED>(xv, C, q + (size_t)row * I, s, row, rows, lane);
+}
+
+// ------------------------------------------------------------------------------------------------ dispatch
+// CH = vectors of 8 per lane holding a row of `len` values: len <= 512 CH <= 8192
+#define LFM2Q_CH_SWITCH(len, CALL)                                                                                  \
+    switch (((len) + 511) / 512) {                                                                                   \
+        case 1: CALL(1); break;                                                                                      \
+        case 2: CALL(2); break;                                                                                      \
+        case 3: CALL(3); break;                                                                                      \
+        case 4: CALL(4); break;                                                                                      \
+        case 5: CALL(5); break;                                                                                      \
+        case 6: CALL(6); break;                                                                                      \
+        case 7: CALL(7); break;                                                                                      \
+        case 8: CALL(8); break;                                                                                      \
+        case 9: CALL(9); break;                                                                                      \
+        case 10: CALL(10); break;                                                                                    \
+        case 11: CALL(11); break;                                                                                    \
+        case 12: CALL(12); break;                                                                                    \
+        case 13: CALL(13); break;                                                                                    \
+        case 14: CALL(14); break;                                                                                    \
+        case 15: CALL(15); break;                                                                                    \
+        default: CALL(16); break;                                                                                    \
+    }
+
+int check_rows(const char *name, int rows, int len, int grouped, int maxlen) {
+    LFM2Q_REQUIRE(rows >= 1 && len >= 8, LFM2Q_ERR_SHAPE, "%s: need rows >= 1 and a row length >= 8 (rows=%d, %d)",
+                  name, rows, len);
+    LFM2Q_REQUIRE(len % (grouped ? 64 : 8) == 0, LFM2Q_ERR_SHAPE, "%s: row length must be a multiple of %d (%d)", name,
+                  grouped ? 64 : 8, len);
+    LFM2Q_REQUIRE(len <= maxlen, LFM2Q_ERR_SHAPE, "%s: row length must be <= %d (%d)", name, maxlen, len);
+    return LFM2Q_OK;
+}
+
+}  // namespace
+}  // namespace lfm2q
+
+using namespace lfm2q;
+
+extern "C" int lfm2q_quant_rows(const lfm2q_bf16 *x, int8_t *q, float *s, int rows, int K, lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(x && q && s, LFM2Q_ERR_ARG, "quant_rows: null pointer");
+    LFM2Q_REQUIRE(rows >= 1 && K >= 8 && K % 8 == 0, LFM2Q_ERR_SHAPE,
+                  "quant_rows: K must be a multiple of 8 (rows=%d K=%d)", rows, K);
+    LFM2Q_REQUIRE(aligned16(x) && ((uintptr_t)q & 7) == 0, LFM2Q_ERR_ALIGN,
+                  "quant_rows: x must be 16-byte and q 8-byte aligned");
+    const dim3 grid((rows + 3) / 4);
+    const hipStream_t st = (hipStream_t)stream;
+#define LFM2Q_Q(CH_) quant_kernel<CH_, false><<<grid, 256, 0, st>>>(x, q, s, rows, K)
+    if (K > 8192)
+        LFM2Q_Q(0);
+    else
+        LFM2Q_CH_SWITCH(K, LFM2Q_Q)
+#undef LFM2Q_Q
+    return launch_status("quant_rows");
+}
+
+extern "C" int lfm2q_quant_groups(const lfm2q_bf16 *x, int8_t *q, float *sT, int rows, int K, lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(x && q && sT, LFM2Q_ERR_ARG, "quant_groups: null pointer");
+    LFM2Q_REQUIRE(rows >= 1 && K >= 64 && K % 64 == 0, LFM2Q_ERR_SHAPE,
+                  "quant_groups: K must be a multiple of 64 (rows=%d K=%d)", rows, K);
+    LFM2Q_REQUIRE(aligned16(x) && ((uintptr_t)q & 7) == 0, LFM2Q_ERR_ALIGN,
+                  "quant_groups: x must be 16-byte and q 8-byte aligned");
+    const dim3 grid((rows + 3) / 4);
+    const hipStream_t st = (hipStream_t)stream;
+#define LFM2Q_Q(CH_) quant_kernel<CH_, true><<<grid, 256, 0, st>>>(x, q, sT, rows, K)
+    if (K > 8192)
+        LFM2Q_Q(0);
+    else
+        LFM2Q_CH_SWITCH(K, LFM2Q_Q)
+#undef LFM2Q_Q
+    return launch_status("quant_groups");
+}
+
+extern "C" int lfm2q_add_rmsnorm_q(lfm2q_bf16 *h, const lfm2q_bf16 *y, const lfm2q_bf16 *w, int8_t *q, float *s,
+                                   lfm2q_bf16 *x, int rows, int H, float eps, int grouped, lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(h && w && q && s, LFM2Q_ERR_ARG, "add_rmsnorm_q: null pointer");
+    if (int st = check_rows("add_rmsnorm_q", rows, H, grouped, 8192)) return st;
+    LFM2Q_REQUIRE(aligned16(h) && aligned16(w) && (!y || aligned16(y)) && (!x || aligned16(x)) && ((uintptr_t)q & 7) == 0,
+                  LFM2Q_ERR_ALIGN, "add_rmsnorm_q: h, y, w, x must be 16-byte and q 8-byte aligned");
+    const dim3 grid((rows + 3) / 4);
+    const hipStream_t st = (hipStream_t)stream;
+#define LFM2Q_P(CH_)                                                                                                 \
+    if (grouped)                                                                                                     \
+        add_rmsnorm_q_kernel<CH_, true><<<grid, 256, 0, st>>>(h, y, w, q, s, x, rows, H, eps);                       \
+    else                                                                                                             \
+        add_rmsnorm_q_kernel<CH_, false><<<grid, 256, 0, st>>>(h, y, w, q, s, x, rows, H, eps)
+    LFM2Q_CH_SWITCH(H, LFM2Q_P)
+#undef LFM2Q_P
+    return launch_status("add_rmsnorm_q");
+}
+
+extern "C" int lfm2q_add_layernorm_q(lfm2q_bf16 *h, const lfm2q_bf16 *y, const lfm2q_bf16 *w, const lfm2q_bf16 *b,
+                                     int8_t *q, float *s, lfm2q_bf16 *x, int rows, int D, float eps, int grouped,
+                                     lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(h && w && b && q && s, LFM2Q_ERR_ARG, "add_layernorm_q: null pointer");
+    if (int st = check_rows("add_layernorm_q", rows, D, grouped, 8192)) return st;
+    LFM2Q_REQUIRE(aligned16(h) && aligned16(w) && aligned16(b) && (!y || aligned16(y)) && (!x || aligned16(x)) &&
+                      ((uintptr_t)q & 7) == 0,
+                  LFM2Q_ERR_ALIGN, "add_layernorm_q: h, y, w, b, x must be 16-byte and q 8-byte aligned");
+    const dim3 grid((rows + 3) / 4);
+    const hipStream_t st = (hipStream_t)stream;
+#define LFM2Q_P(CH_)                                                                                                 \
+    if (grouped)                                                                                                     \
+        add_layernorm_q_kernel<CH_, true><<<grid, 256, 0, st>>>(h, y, w, b, q, s, x, rows, D, eps);                  \
+    else                                                                                                             \
+        add_layernorm_q_kernel<CH_, false><<<grid, 256, 0, st>>>(h, y, w, b, q, s, x, rows, D, eps)
+    LFM2Q_CH_SWITCH(D, LFM2Q_P)
+#undef LFM2Q_P
+    return launch_status("add_layernorm_q");
+}
+
+extern "C" int lfm2q_silu_mul_q(const lfm2q_bf16 *g, int8_t *q, float *s, lfm2q_bf16 *x, int rows, int I, int grouped,
+                                lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(g && q && s, LFM2Q_ERR_ARG, "silu_mul_q: null pointer");
+    if (int st = check_rows("silu_mul_q", rows, I, grouped, 8192)) return st;
+    LFM2Q_REQUIRE(aligned16(g) && (!x || aligned16(x)) && ((uintptr_t)q & 7) == 0, LFM2Q_ERR_ALIGN,
+                  "silu_mul_q: g, x must be 16-byte and q 8-byte aligned");
+    const dim3 grid((rows + 3) / 4);
+    const hipStream_t st = (hipStream_t)stream;
+#define LFM2Q_P(CH_)                                                                                                 \
+    if (grouped)                                                                                                     \
+        silu_mul_q_kernel<CH_, true><<<grid, 256, 0, st>>>(g, q, s, x, rows, I);                                     \
+    else                                                                                                             \
+        silu_mul_q_kernel<CH_, false><<<grid, 256, 0, st>>>(g, q, s, x, rows, I)
+    LFM2Q_CH_SWITCH(I, LFM2Q_P)
+#undef LFM2Q_P
+    return launch_status("silu_mul_q");
+}

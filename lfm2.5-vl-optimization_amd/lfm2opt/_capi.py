@@ -14,6 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent.parent / "lib" / "liblfm2q.so
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
+_F = ctypes.c_float
 
 # name -> argument types (every entry point returns an int status)
 SIGNATURES = {
@@ -24,6 +25,10 @@ SIGNATURES = {
     "lfm2q_gemv_w4": [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "lfm2q_silu_mul": [_P, _P, _I, _I, _P],
     "lfm2q_quant_rows": [_P, _P, _P, _I, _I, _P],
+    "lfm2q_quant_groups": [_P, _P, _P, _I, _I, _P],
+    "lfm2q_add_rmsnorm_q": [_P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _P],
+    "lfm2q_add_layernorm_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _P],
+    "lfm2q_silu_mul_q": [_P, _P, _P, _P, _I, _I, _I, _P],
     "lfm2q_gemm_i8": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_i32": [_P, _P, _P, _I, _I, _I, _P],
 }

@@ -193,8 +193,8 @@ class DecodeOps:
 
 
 class Int8Ops:
-    """INT8 prefill / vision ops (reference: kernels/int8_gemm.cpp). Grouped-64 activation scales (2-D sx) and the
-    fused producers are not provided by this build: asking for them raises RuntimeError."""
+    """INT8 prefill / vision ops (reference: kernels/int8_gemm.cpp): quantizers, fused producers, W8A8 GEMM. The
+    grouped-64 GEMM (2-D sx), gemm_i8_q and gemm_w8 are not provided by this build: asking for them raises."""
 
     def __init__(self):
         _capi.lib()
@@ -233,21 +233,102 @@ class Int8Ops:
         _capi.call("lfm2q_gemm_i8_i32", xq.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, _capi.stream(xq))
 
     def quant_rows(self, x, q, s):
-        """Per-row symmetric quantization: s = max|x| / 127, q = round(x / s). Reference: quant_rows(),
-        kernels/int8_gemm.cpp:83-96 (a 2-D s asks for grouped scales, not provided by this build)."""
+        """Symmetric quantization: s = max|x| / 127, q = round(x / s), per row (1-D s [rows]) or per row and group of
+        64 columns (2-D s [K/64, rows], transposed as gemm_i8 reads it). Reference: quant_rows(),
+        kernels/int8_gemm.cpp:83-96 (K % 128 and, per row, K <= 2048 there; K % 8, grouped K % 64, any K here)."""
         _check_bf16(x, "x")
         _check_t(q, torch.int8, "q")
         _check_t(s, torch.float32, "s")
         K = x.size(-1)
         rows = x.numel() // K if K else 0
         if s.dim() == 2:
-            raise RuntimeError("quant_rows: grouped scales (s [K/64, rows]) are not provided by this build")
+            if not (K % 64 == 0 and K > 0 and s.size(0) == K // 64 and s.size(1) == rows and q.numel() == x.numel()):
+                raise RuntimeError("grouped shapes")
+            _same_device(x, q, s)
+            _capi.call("lfm2q_quant_groups", x.data_ptr(), q.data_ptr(), s.data_ptr(), rows, K, _capi.stream(x))
+            return
         if K % 8 or K == 0:
             raise RuntimeError("K must be a multiple of 8")
         if q.numel() != x.numel() or s.numel() != rows:
             raise RuntimeError("q / s shape")
         _same_device(x, q, s)
         _capi.call("lfm2q_quant_rows", x.data_ptr(), q.data_ptr(), s.data_ptr(), rows, K, _capi.stream(x))
+
+    # ---- fused producers (kernels/int8_gemm.cpp:99-141). x (an addition): also write the bf16 row that was
+    # quantized; q / s are then exactly quant_rows(x, ...) of it.
+    @staticmethod
+    def _check_qs(q, s, rows, L):
+        """kernels/int8_gemm.cpp:99-105: per-row (1-D s) or grouped (2-D s [L/64, rows])."""
+        _check_t(q, torch.int8, "q")
+        _check_t(s, torch.float32, "s")
+        grouped = s.dim() == 2
+        if q.numel() != rows * L:
+            raise RuntimeError("q shape")
+        if not (s.size(0) == L // 64 and s.size(1) == rows and L % 64 == 0 if grouped else s.numel() == rows):
+            raise RuntimeError("s shape")
+        return int(grouped)
+
+    def add_layernorm_q(self, h, y, w, b, q, s, eps, x=None):
+        """vision: h += y (optional, in place, bf16-rounded); (q, s) = quant(LayerNorm(h) * w + b).
+        Reference: add_layernorm_q(), kernels/int8_gemm.cpp:108-119 (D % 128, D <= 2048 there; D % 8, D <= 8192)."""
+        _check_bf16(h, "h")
+        _check_bf16(w, "w")
+        _check_bf16(b, "b")
+        if y is not None:
+            _check_bf16(y, "y")
+            if y.numel() != h.numel():
+                raise RuntimeError("y shape")
+        D = h.size(-1)
+        rows = h.numel() // D if D else 0
+        if not (D % 8 == 0 and 0 < D <= 8192 and w.numel() == D and b.numel() == D):
+            raise RuntimeError("D must be a multiple of 8, <= 8192")
+        grouped = self._check_qs(q, s, rows, D)
+        if x is not None:
+            _check_bf16(x, "x")
+            if x.numel() != h.numel():
+                raise RuntimeError("x shape")
+        _same_device(h, y, w, b, q, s, x)
+        _capi.call("lfm2q_add_layernorm_q", h.data_ptr(), _capi.ptr(y), w.data_ptr(), b.data_ptr(), q.data_ptr(),
+                   s.data_ptr(), _capi.ptr(x), rows, D, float(eps), grouped, _capi.stream(h))
+
+    def add_rmsnorm_q(self, h, y, w, q, s, eps, x=None):
+        """LM prefill: h += y (optional, in place, bf16-rounded); (q, s) = quant(bf16(w * bf16(rmsnorm(h)))).
+        Reference: add_rmsnorm_q(), kernels/int8_gemm.cpp:122-132 (H <= 8192 here)."""
+        _check_bf16(h, "h")
+        _check_bf16(w, "w")
+        if y is not None:
+            _check_bf16(y, "y")
+            if y.numel() != h.numel():
+                raise RuntimeError("y shape")
+        H = h.size(-1)
+        rows = h.numel() // H if H else 0
+        if not (w.numel() == H and H % 8 == 0 and 0 < H <= 8192):
+            raise RuntimeError("w shape")
+        grouped = self._check_qs(q, s, rows, H)
+        if x is not None:
+            _check_bf16(x, "x")
+            if x.numel() != h.numel():
+                raise RuntimeError("x shape")
+        _same_device(h, y, w, q, s, x)
+        _capi.call("lfm2q_add_rmsnorm_q", h.data_ptr(), _capi.ptr(y), w.data_ptr(), q.data_ptr(), s.data_ptr(),
+                   _capi.ptr(x), rows, H, float(eps), grouped, _capi.stream(h))
+
+    def silu_mul_q(self, g, q, s, x=None):
+        """LM prefill: g [rows, 2I] = w1 | w3 outputs -> (q, s) = quant(bf16(bf16(silu(g1)) * g3)).
+        Reference: silu_mul_q(), kernels/int8_gemm.cpp:135-141 (I % 64, I <= 20000 there; I % 8, I <= 8192)."""
+        _check_bf16(g, "g")
+        I = g.size(-1) // 2
+        rows = g.numel() // (2 * I) if I else 0
+        if not (I % 8 == 0 and 0 < I <= 8192 and g.size(-1) == 2 * I):
+            raise RuntimeError("I shape")
+        grouped = self._check_qs(q, s, rows, I)
+        if x is not None:
+            _check_bf16(x, "x")
+            if x.numel() != rows * I:
+                raise RuntimeError("x shape")
+        _same_device(g, q, s, x)
+        _capi.call("lfm2q_silu_mul_q", g.data_ptr(), q.data_ptr(), s.data_ptr(), _capi.ptr(x), rows, I, grouped,
+                   _capi.stream(g))
 
     @staticmethod
     def _check_common(w, sw, bias, y, M, K):

@@ -28,6 +28,8 @@ _SIGS = {
     "orc_silu_mul": ([_P, _I64, _I64, _P], None),
     "orc_quant_rows": ([_P, _I64, _I64, _P, _P], None),
     "orc_quant_groups": ([_P, _I64, _I64, _P, _P], None),
+    "orc_add_rmsnorm": ([_P, _P, _P, _I64, _I64, ctypes.c_float, _P], None),
+    "orc_add_layernorm": ([_P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P], None),
     "orc_gemm_i8_i32": ([_P, _P, _I64, _I64, _I64, _P], None),
     "orc_gemm_i8_epilogue": ([_P, _P, _P, _P, _I64, _I64, _INT, _P], None),
     "orc_gemm_i8_grouped": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P], None),
@@ -86,6 +88,27 @@ def quant_rows(x):
     s = np.empty(rows, np.float32)
     lib().orc_quant_rows(_p(x), rows, K, _p(q), _p(s))
     return q, s
+
+
+def add_rmsnorm(h, y, w, eps):
+    """-> (h_new, x): h_new = bf16(h + y) (h unchanged if y is None), x = bf16(w * bf16(h_new * rsqrt(mean(h_new^2) +
+    eps))); bf16 as uint16 bits (kernels/lfm2_decode.cu:96-121, the input of add_rmsnorm_q)."""
+    hn = _c(np.array(h, copy=True), np.uint16)
+    rows, H = hn.shape
+    x = np.empty_like(hn)
+    lib().orc_add_rmsnorm(_p(hn), None if y is None else _p(_c(y, np.uint16)), _p(_c(w, np.uint16)), rows, H,
+                          float(eps), _p(x))
+    return hn, x
+
+
+def add_layernorm(h, y, w, b, eps):
+    """-> (h_new, x): h_new = bf16(h + y), x = bf16(LayerNorm(h_new) * w + b) (kernels/vision_ops.cu:29-80)."""
+    hn = _c(np.array(h, copy=True), np.uint16)
+    rows, D = hn.shape
+    x = np.empty_like(hn)
+    lib().orc_add_layernorm(_p(hn), None if y is None else _p(_c(y, np.uint16)), _p(_c(w, np.uint16)),
+                            _p(_c(b, np.uint16)), rows, D, float(eps), _p(x))
+    return hn, x
 
 
 def quant_groups(x):

@@ -92,6 +92,56 @@ void orc_quant_groups(const uint16_t *x, int64_t rows, int64_t K, int8_t *q, flo
         }
 }
 
+/* ------------------------------------------------------------------------------------------ INT8 producers */
+/* The bf16 outputs the fused INT8 producers quantize (kernels/int8_gemm.cu:527-682): the row statistics are summed
+ * in fp64 and rounded to fp32 once (the kernels' fp32 reduction order is their own), everything after follows the
+ * kernels' fp32 / bf16 rounding points. y (the residual input) may be NULL; h is updated in place when it is not. */
+
+/* LM prefill, = add_rmsnorm (kernels/lfm2_decode.cu:96-121): h = bf16(h + y); ms = sum h^2 / H;
+ * rs = 1 / sqrt(ms + eps) (correctly rounded); x = bf16(w * bf16(h * rs)) */
+void orc_add_rmsnorm(uint16_t *h, const uint16_t *y, const uint16_t *w, int64_t rows, int64_t H, float eps,
+                     uint16_t *x) {
+    for (int64_t r = 0; r < rows; ++r) {
+        uint16_t *hr = h + r * H;
+        double ss = 0.0;
+        for (int64_t i = 0; i < H; ++i) {
+            if (y) hr[i] = f2bf(bf2f(hr[i]) + bf2f(y[r * H + i]));
+            const double v = bf2f(hr[i]);
+            ss += v * v;
+        }
+        const float ms = (float)ss / (float)H;
+        const float rs = (float)(1.0 / sqrt((double)(ms + eps)));
+        for (int64_t i = 0; i < H; ++i) x[r * H + i] = f2bf(bf2f(w[i]) * rbf(bf2f(hr[i]) * rs));
+    }
+}
+
+/* vision, = add_layernorm (kernels/vision_ops.cu:29-80): h = bf16(h + y); mean = sum h / D;
+ * var = sum (h - mean)^2 / D; rstd = 1 / sqrt(var + eps); x = bf16(((h - mean) * rstd) * w + b) */
+void orc_add_layernorm(uint16_t *h, const uint16_t *y, const uint16_t *w, const uint16_t *b, int64_t rows,
+                       int64_t D, float eps, uint16_t *x) {
+    for (int64_t r = 0; r < rows; ++r) {
+        uint16_t *hr = h + r * D;
+        double sum = 0.0;
+        for (int64_t i = 0; i < D; ++i) {
+            if (y) hr[i] = f2bf(bf2f(hr[i]) + bf2f(y[r * D + i]));
+            sum += bf2f(hr[i]);
+        }
+        const float mean = (float)sum / (float)D;
+        double qs = 0.0;
+        for (int64_t i = 0; i < D; ++i) {
+            const double d = (double)(bf2f(hr[i]) - mean);
+            qs += d * d;
+        }
+        const float var = (float)qs / (float)D;
+        const float rstd = (float)(1.0 / sqrt((double)(var + eps)));
+        for (int64_t i = 0; i < D; ++i) {
+            float v = (bf2f(hr[i]) - mean) * rstd;
+            v = v * bf2f(w[i]);
+            x[r * D + i] = f2bf(v + bf2f(b[i]));
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------------------------ W8A8 GEMM */
 /* exact integer product C[m, n] = sum_k A[m, k] B[n, k] (A [M, K], B [N, K], both int8). |C| <= 127^2 K fits
  * int32 for K < 133144, so the int64 sum is cast without loss. */

@@ -110,6 +110,35 @@ def case_gemm_i8(seed, M, K, N, bias, gelu):
     return d
 
 
+def case_quant_groups(seed, M, K):
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((M, K)) * r.uniform(0.01, 4, (M, 1))
+    x[0, 3] = 37.0
+    if M > 2:
+        x[2, :64] = 0.0  # an all-zero group: s = 1e-8 / 127
+    xb = bf16(x)
+    if K == 64:
+        xb[: min(M, 12)] = division_trap_rows(seed)[: min(M, 12)]
+    q, sT = oracle.quant_groups(xb)
+    return dict(x=xb, q=q, sT=sT)
+
+
+def case_add_rmsnorm(seed, rows, H, eps):
+    r = np.random.default_rng(seed)
+    h, y = bf16(r.standard_normal((rows, H)) * 2), bf16(r.standard_normal((rows, H)))
+    w = bf16(r.random(H) + 0.5)
+    hn, x = oracle.add_rmsnorm(h, y, w, eps)
+    return dict(h=h, y=y, w=w, eps=np.float32(eps), h_out=hn, x=x)
+
+
+def case_add_layernorm(seed, rows, D, eps):
+    r = np.random.default_rng(seed)
+    h, y = bf16(r.standard_normal((rows, D)) * 3), bf16(r.standard_normal((rows, D)))
+    w, b = bf16(r.random(D) + 0.5), bf16(r.standard_normal(D))
+    hn, x = oracle.add_layernorm(h, y, w, b, eps)
+    return dict(h=h, y=y, w=w, b=b, eps=np.float32(eps), h_out=hn, x=x)
+
+
 def pack_ref_int4(q):
     """q in [-8, 7] [N, K] -> uint8 [N, K/2]: weight 2j in the low nibble of byte j, stored as q + 8."""
     u = (np.asarray(q) + 8).astype(np.uint8)
@@ -171,6 +200,10 @@ CASES = {
     "gemv_w4_b2_n40_k512_g64": (case_gemv_w4, (22, 2, 40, 512, 64)),
     "gemv_w4z_b1_r64_k2048_g128": (case_gemv_w4z, (23, 1, 64, 2048, 128, False)),
     "gemv_w4z_b8_r96_k1024_g128_swiglu": (case_gemv_w4z, (24, 8, 96, 1024, 128, True)),
+    "quant_groups_traps_k64": (case_quant_groups, (25, 12, 64)),
+    "quant_groups_m37_k1152": (case_quant_groups, (26, 37, 1152)),
+    "add_rmsnorm_r9_h512": (case_add_rmsnorm, (27, 9, 512, 1e-5)),
+    "add_layernorm_r7_d1152": (case_add_layernorm, (28, 7, 1152, 1e-6)),
 }
 
 

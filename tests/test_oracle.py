@@ -377,3 +377,58 @@ def test_gemv_w4z_zero_points_and_swiglu():
     assert ulps(y, bf16_bits(torch.from_numpy(exact).float())) <= 1
     ys = oracle.gemv_w4z(Wq, S16, Z, x, group, swiglu=True)
     assert np.array_equal(ys, oracle.silu_mul(y))
+
+
+# ------------------------------------------------------------------------------------------------ INT8 producers
+def test_add_rmsnorm_against_torch_fp64():
+    """h = bf16(h + y) exactly as torch's bf16 add; x within 1 bf16 ulp of bf16(w * bf16(F.rms_norm(h) in fp64))."""
+    rows, H, eps = 37, 512, 1e-5
+    h, y = rand_bf16((rows, H), 2.0), rand_bf16((rows, H))
+    w = bf16_bits(torch.from_numpy(RNG.random(H).astype(np.float32) + 0.5))
+    hn, x = oracle.add_rmsnorm(h, y, w, eps)
+    assert np.array_equal(hn, bf16_bits((from_bits(h).float() + from_bits(y).float())))
+    hd = from_bits(hn).double()
+    n = F.rms_norm(hd, (H,), eps=eps).to(torch.bfloat16).float()
+    ref = bf16_bits(from_bits(w).float()[None, :] * n)
+    assert ulps(x, ref) <= 1 and (x != ref).mean() < 0.01
+    # no residual input: h is left as it is
+    hn2, x2 = oracle.add_rmsnorm(hn, None, w, eps)
+    assert np.array_equal(hn2, hn) and np.array_equal(x2, x)
+
+
+def test_add_rmsnorm_constant_rows_closed_form():
+    """A constant row c (|c| >= 1, eps = 1e-5) normalizes to exactly sign(c), so x = sign(c) * w bit for bit."""
+    H = 256
+    c = np.array([1.0, -3.0, 40.0, -1.5], np.float32)
+    h = bf16_bits(torch.from_numpy(np.repeat(c[:, None], H, 1)))
+    w = rand_bf16((H,))
+    _, x = oracle.add_rmsnorm(h, None, w, 1e-5)
+    wf = oracle.bf2f(w)
+    for r in range(4):
+        assert np.array_equal(x[r], oracle.f2bf(np.sign(c[r]) * wf))
+
+
+def test_add_layernorm_against_torch_fp64():
+    rows, D, eps = 29, 1152, 1e-6
+    h, y = rand_bf16((rows, D), 3.0), rand_bf16((rows, D))
+    h[:, :7] = bf16_bits(from_bits(h[:, :7]).float() + 5.0)  # a mean far from zero
+    w = bf16_bits(torch.from_numpy(RNG.random(D).astype(np.float32) + 0.5))
+    b = rand_bf16((D,))
+    hn, x = oracle.add_layernorm(h, y, w, b, eps)
+    assert np.array_equal(hn, bf16_bits((from_bits(h).float() + from_bits(y).float())))
+    ref = F.layer_norm(from_bits(hn).double(), (D,), from_bits(w).double(), from_bits(b).double(), eps)
+    assert ulps(x, bf16_bits(ref.float())) <= 1
+
+
+def test_add_layernorm_two_level_rows_closed_form():
+    """Rows alternating a and -a: mean 0, var a^2, so (h - mean) * rstd = +-1 up to eps and x = bf16(+-w + b)."""
+    D = 128
+    a = np.array([2.0, 0.5, 8.0], np.float32)
+    sign = np.where(np.arange(D) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    h = bf16_bits(torch.from_numpy(a[:, None] * sign[None, :]))
+    w = rand_bf16((D,))
+    b = rand_bf16((D,))
+    _, x = oracle.add_layernorm(h, None, w, b, 1e-9)
+    wf, bf = oracle.bf2f(w), oracle.bf2f(b)
+    for r in range(3):
+        assert np.array_equal(x[r], oracle.f2bf(sign * wf + bf))
