@@ -132,6 +132,21 @@ int lfm2q_silu_mul_q(const lfm2q_bf16 *g, int8_t *q, float *s, lfm2q_bf16 *x, in
 int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
                   lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream);
 
+/* W8A8 GEMM with grouped-64 activation scales saT fp32 [K/64, M] (lfm2q_quant_groups' layout): per 64-wide K group g
+ * the exact int32 partial sum folds into fp32 as facc = fma((float)part_g, saT[g, m], facc) in group order, then
+ * Y[m, n] = bf16( gelu?( facc * sb[n] + bias[n] ) ) (two separately rounded ops). K % 64 == 0.
+ * Replaces launch_gemm_i8(..., grouped = true, ...) kernels/int8_gemm.cu:741-748 (gemm_i8() with a 2-D sx). */
+int lfm2q_gemm_i8_grouped(const int8_t *A, const float *saT, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
+                          lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream);
+
+/* The grouped W8A8 GEMM writing the next W8A8 GEMM's input: the bf16 values lfm2q_gemm_i8_grouped would write are
+ * quantized per row and group of 64 columns exactly as lfm2q_quant_groups does, into Yq int8 [M, N] and
+ * YsT fp32 [N/64, M]. K % 64 == 0, N % 64 == 0; sb 16-byte, bias and Yq 8-byte aligned.
+ * Replaces launch_gemm_i8_q kernels/int8_gemm.cu:750-760 (binding gemm_i8_q(), kernels/int8_gemm.cpp:53-69, which
+ * requires N % 128 == 0). */
+int lfm2q_gemm_i8_q(const int8_t *A, const float *saT, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
+                    int8_t *Yq, float *YsT, int M, int N, int K, int gelu, lfm2q_stream_t stream);
+
 /* The exact int32 accumulators of the W8A8 GEMM: C[m, n] = sum_k A[m, k] B[n, k], C int32 [M, N]. No counterpart
  * entry point in the reference (whose tests use torch._int_mm for this, tests/test_int8_gemm.py:236). */
 int lfm2q_gemm_i8_i32(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, lfm2q_stream_t stream);

@@ -15,6 +15,7 @@
 // Reference: kernels/int8_gemm.cu:125-297 (gemm_i8_kernel, per-token path), :93-115 (store_tile epilogue),
 // :690-702 (pick_bm); bound as gemm_i8 in kernels/int8_gemm.cpp.
 #include "common.hpp"
+#include "quantize.hpp"
 #include "status.hpp"
 
 #include <algorithm>
@@ -28,13 +29,24 @@ constexpr int BK = 64;   // bytes of K per stage
 // LDS byte offset of 16-byte chunk c of 64-byte row r: chunk c is stored at slot c ^ ((r >> sh) & 3)
 __device__ __forceinline__ int swz(int r, int c, int sh) { return (r * 4 + (c ^ ((r >> sh) & 3))) * 16; }
 
-enum GemmOut { OUT_BF16 = 0, OUT_BF16_GELU = 1, OUT_I32 = 2 };
+// bf16 out, bf16 out after GELU, the int32 accumulators, or INT8 + per-64-column scales (after GELU) for the next GEMM
+enum GemmOut { OUT_BF16 = 0, OUT_BF16_GELU = 1, OUT_I32 = 2, OUT_Q8 = 3, OUT_Q8_GELU = 4 };
+constexpr bool out_gelu(int o) { return o == OUT_BF16_GELU || o == OUT_Q8_GELU; }
+constexpr bool out_q8(int o) { return o == OUT_Q8 || o == OUT_Q8_GELU; }
 
-// ((float)acc * sx) * sw + b, each op rounded separately (no FMA contraction)
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// per-token: ((float)acc * sx) * sw + b, each op rounded separately (no FMA contraction)
 __device__ __forceinline__ float dequant(int acc, float sx, float sw, float b) {
 #pragma clang fp contract(off)
     float v = (float)acc * sx;
     v = v * sw;
+    return v + b;
+}
+// grouped: the fp32 accumulator already carries the activation scales; facc * sw + b
+__device__ __forceinline__ float dequant(float facc, float, float sw, float b) {
+#pragma clang fp contract(off)
+    const float v = facc * sw;
     return v + b;
 }
 
@@ -77,6 +89,11 @@ __device__ __forceinline__ void lds_dma16(v4i desc, uint32_t voff, uint32_t lds_
                  "s"(lds_base)
                  : "memory", "m0");
 }
+// 4 bytes per lane from buffer offset `voff` into LDS at lds_base + 4 * lane
+__device__ __forceinline__ void lds_dma4(v4i desc, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "s"(lds_base)
+                 : "memory", "m0");
+}
 // LDS address of p as a wavefront-uniform (SGPR) value for M0
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(p));
@@ -84,8 +101,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 
 // Epilogue of one wavefront block: tokens mb .. mb + 32 TM - 1 x weight rows nb .. nb + 32 TN - 1. Per tile (i, j)
 // and run q the lane holds 4 consecutive output columns n .. n + 3 of token row m.
-template <int TM, int TN, int OUT>
-__device__ __forceinline__ void store_tile(const v16i (&acc)[TN][TM], const float *__restrict__ sx,
+template <int TM, int TN, int OUT, typename ACC>
+__device__ __forceinline__ void store_tile(const ACC (&acc)[TN][TM], const float *__restrict__ sx,
                                            const float *__restrict__ sw, const uint16_t *__restrict__ bias,
                                            void *__restrict__ Y, int M, int N, int mb, int nb, int lr, int lh) {
     // 4-wide vector path: rows of 4k elements and aligned Y (16 B), sw (16 B) and bias (8 B)
@@ -94,7 +111,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[TN][TM], const floa
     for (int j = 0; j < TM; ++j) {
         const int m = mb + 32 * j + lr;
         if (m >= M) continue;
-        const float s_m = OUT == OUT_I32 ? 0.f : sx[m];
+        const float s_m = (OUT == OUT_I32 || !sx) ? 0.f : sx[m];
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -102,7 +119,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[TN][TM], const floa
                 const int n = nb + 32 * i + 8 * q + 4 * lh;
                 if (n >= N) continue;
                 const size_t o = (size_t)m * N + n;
-                if (OUT == OUT_I32) {
+                if constexpr (OUT == OUT_I32) {
                     if (vec) {
                         *reinterpret_cast<v4i *>(reinterpret_cast<int32_t *>(Y) + o) =
                             v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
@@ -132,7 +149,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[TN][TM], const floa
                             v[e] = dequant(acc[i][j][4 * q + e], s_m, sw[ne], bias ? bf2f(bias[ne]) : 0.f);
                         }
                     }
-                    if (OUT == OUT_BF16_GELU)
+                    if (out_gelu(OUT))
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f32(v[e]);
                     uint16_t *yo = reinterpret_cast<uint16_t *>(Y) + o;
@@ -157,11 +174,11 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[TN][TM], const floa
 template <int TN>
 constexpr int stage_bytes() { return 32 * (64 * TN + 8); }
 
-template <int TM, int TN, int OUT>
-__device__ __forceinline__ void store_tile_staged(const v16i (&acc)[TN][TM], const float *__restrict__ sx,
+template <int TM, int TN, int OUT, typename ACC>
+__device__ __forceinline__ void store_tile_staged(const ACC (&acc)[TN][TM], const float *__restrict__ sx,
                                                   const float *__restrict__ sw, const uint16_t *__restrict__ bias,
-                                                  uint16_t *__restrict__ Y, int M, int N, int mb, int nb, int lane,
-                                                  uint8_t *stage) {
+                                                  void *__restrict__ Y, float *__restrict__ YsT, int M, int N, int mb,
+                                                  int nb, int lane, uint8_t *stage) {
     constexpr int WN = 32 * TN;      // output columns of the block
     constexpr int P = 2 * WN + 8;    // LDS row pitch (bytes)
     constexpr int CPRo = WN / 8;     // 16-byte chunks per output row
@@ -171,7 +188,7 @@ __device__ __forceinline__ void store_tile_staged(const v16i (&acc)[TN][TM], con
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
         const int m = mb + 32 * j + lr;
-        const float s_m = sx[min(m, M - 1)];
+        const float s_m = sx ? sx[min(m, M - 1)] : 0.f;
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -189,7 +206,7 @@ __device__ __forceinline__ void store_tile_staged(const v16i (&acc)[TN][TM], con
                 v[1] = dequant(acc[i][j][4 * q + 1], s_m, w4[1], bf2f_hi(b01));
                 v[2] = dequant(acc[i][j][4 * q + 2], s_m, w4[2], bf2f_lo(b23));
                 v[3] = dequant(acc[i][j][4 * q + 3], s_m, w4[3], bf2f_hi(b23));
-                if (OUT == OUT_BF16_GELU)
+                if (out_gelu(OUT))
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f32(v[e]);
                 *reinterpret_cast<uint2 *>(stage + lr * P + 2 * (32 * i + 8 * q + 4 * lh)) =
@@ -203,22 +220,46 @@ __device__ __forceinline__ void store_tile_staged(const v16i (&acc)[TN][TM], con
             const uint2 v0 = *reinterpret_cast<const uint2 *>(stage + r * P + 16 * c);
             const uint2 v1 = *reinterpret_cast<const uint2 *>(stage + r * P + 16 * c + 8);
             const int mo = mb + 32 * j + r, no = nb + 8 * c;
-            if (mo < M && no < N) *reinterpret_cast<uint4 *>(Y + (size_t)mo * N + no) = make_uint4(v0.x, v0.y, v1.x, v1.y);
+            if constexpr (out_q8(OUT)) {
+                // the 8 lanes c0 .. c0 + 7 (c0 % 8 == 0) of this row hold one 64-column group of bf16 outputs:
+                // quantize it exactly as quant_groups does
+                const v4i xv = v4i{(int)v0.x, (int)v0.y, (int)v1.x, (int)v1.y};
+                float am = absmax8(xv, 0.f);
+                am = fmaxf(am, __shfl_xor(am, 1));
+                am = fmaxf(am, __shfl_xor(am, 2));
+                am = fmaxf(am, __shfl_xor(am, 4));
+                const float sc = scale_of(am);
+                if (mo < M && no < N) {
+                    int lo, hi;
+                    quant8(xv, sc, 1.f / sc, lo, hi);
+                    *reinterpret_cast<int2 *>(reinterpret_cast<int8_t *>(Y) + (size_t)mo * N + no) = make_int2(lo, hi);
+                    if ((c & 7) == 0) YsT[(size_t)(no >> 6) * M + mo] = sc;
+                }
+            } else if (mo < M && no < N) {
+                *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(Y) + (size_t)mo * N + no) =
+                    make_uint4(v0.x, v0.y, v1.x, v1.y);
+            }
         }
         __builtin_amdgcn_wave_barrier();
     }
 }
 
-template <int TM, int TN, int OUT>
-__device__ __forceinline__ void epilogue(const v16i (&acc)[TN][TM], const float *__restrict__ sx,
+// INT8 output always takes the staged path (its callers guarantee N % 64 == 0 and the alignments)
+template <int TM, int TN, int OUT, typename ACC>
+__device__ __forceinline__ void epilogue(const ACC (&acc)[TN][TM], const float *__restrict__ sx,
                                          const float *__restrict__ sw, const uint16_t *__restrict__ bias,
-                                         void *__restrict__ Y, int M, int N, int mb, int nb, int lane,
-                                         uint8_t *stage) {
+                                         void *__restrict__ Y, float *__restrict__ YsT, int M, int N, int mb, int nb,
+                                         int lane, uint8_t *stage) {
     const int lr = lane & 31, lh = lane >> 5;
-    if (OUT != OUT_I32 && (N & 7) == 0 && (((uintptr_t)Y | (uintptr_t)sw) & 15) == 0 && ((uintptr_t)bias & 7) == 0)
-        store_tile_staged<TM, TN, OUT>(acc, sx, sw, bias, reinterpret_cast<uint16_t *>(Y), M, N, mb, nb, lane, stage);
-    else
-        store_tile<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, mb, nb, lr, lh);
+    if constexpr (out_q8(OUT)) {
+        store_tile_staged<TM, TN, OUT>(acc, sx, sw, bias, Y, YsT, M, N, mb, nb, lane, stage);
+    } else {
+        if (OUT != OUT_I32 && (N & 7) == 0 && (((uintptr_t)Y | (uintptr_t)sw) & 15) == 0 &&
+            ((uintptr_t)bias & 7) == 0)
+            store_tile_staged<TM, TN, OUT>(acc, sx, sw, bias, Y, YsT, M, N, mb, nb, lane, stage);
+        else
+            store_tile<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, mb, nb, lr, lh);
+    }
 }
 
 // BM: token rows (M) per workgroup, BN: weight rows (N). Wavefront (wm, wn) of the 2 x 2 grid owns BM/2 tokens x
@@ -230,19 +271,28 @@ __device__ __forceinline__ void epilogue(const v16i (&acc)[TN][TM], const float 
 // LDS in lane order, i.e. 16 rows of 64 bytes, so lane i fetches the logical chunk c = (i % 4) ^ key(row) that the
 // swizzled layout keeps in that slot. Rows past M and chunks past K read zeros (buffer range check). The loads of
 // stage s + 2 are issued before the MFMAs of stage s; one s_waitcnt + barrier per stage makes stage s visible.
-template <int BM, int BN, int OUT>
+// GRP (grouped-64 activation scales, sx = sxT [K/64, M]): a 64-byte stage is one scale group. The stage's int32
+// sums (the first k step starts from zero) are folded into fp32 accumulators after its MFMAs,
+// facc = fma((float)acc, sxT[kt, m], facc), in stage order -- the reference's fold, exact per group since |acc| <=
+// 64 * 127^2 < 2^24. The group's scales for the tile's rows travel with the operands (one 4-byte direct load per
+// wavefront per stage into a 1 KiB LDS slot) and are read after the stage's barrier. YsT: OUT_Q8 scales.
+template <int BM, int BN, int OUT, bool GRP = false>
 __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
-    int sh) {
+    int sh, float *__restrict__ YsT = nullptr) {
     constexpr int WMt = BM / 2, WNt = BN / 2;   // wavefront block: tokens x weight rows
     constexpr int TM = WMt / 32, TN = WNt / 32;  // 32 x 32 MFMA tiles per wavefront
     constexpr int IX = BM / 64, IW = BN / 64;    // direct-load instructions per wavefront per stage (16 rows each)
+    constexpr int IS = GRP ? 1 : 0;               // scale loads per wavefront per stage
     static_assert(IX >= 1 && IW >= 1 && TM >= 1 && TN >= 1, "tile too small");
     static_assert(4 * stage_bytes<TN>() <= STAGES * (BM + BN) * BK, "epilogue staging exceeds the LDS ring");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * (BM + BN) * BK];
+    static_assert(!out_q8(OUT) || (GRP && WNt % 64 == 0), "INT8 output needs grouped input and 64-column blocks");
+    constexpr int RING = STAGES * (BM + BN) * BK;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + (GRP ? STAGES * 1024 : 0)];
     uint8_t(*sX)[BM * BK] = reinterpret_cast<uint8_t(*)[BM * BK]>(smem);
     uint8_t(*sW)[BN * BK] = reinterpret_cast<uint8_t(*)[BN * BK]>(smem + STAGES * BM * BK);
+    float(*sS)[256] = reinterpret_cast<float(*)[256]>(smem + RING);  // GRP: [stage][tile row]
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
@@ -254,6 +304,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     // this lane's share of the direct loads: instruction j of wavefront w covers tile rows 16 (4 j + w) + lane / 4
     const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
     const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
+    const v4i rs = make_desc(GRP ? (const void *)sx : (const void *)W, GRP ? (uint32_t)std::min<long>((long)(K / 64) * M * 4, 0x7fffffffL) : 0u);
     uint32_t ox[IX], ow[IW];
     int cx[IX], cw[IW];  // byte offset of the fetched chunk within the 64-byte row slice of a stage
 #pragma unroll
@@ -280,7 +331,19 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
             const uint32_t vo = k0 + cw[j] < K ? ow[j] + k0 : 0xfffffff0u;
             lds_dma16(rw, vo, lds_addr(sW[buf] + 1024 * (4 * j + wave)));
         }
+        if (GRP)  // scales sxT[kt, m0 + 64 wave + lane] (rows past the tile are loaded and not used)
+            lds_dma4(rs, (uint32_t)(((long)kt * M + m0 + 64 * wave + lane) * 4),
+                     lds_addr(reinterpret_cast<uint8_t *>(sS[buf]) + 256 * wave));
     };
+
+    v16f facc[GRP ? TN : 1][GRP ? TM : 1];
+    if (GRP)
+#pragma unroll
+        for (int i = 0; i < (GRP ? TN : 1); ++i)
+#pragma unroll
+            for (int j = 0; j < (GRP ? TM : 1); ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) facc[i][j][e] = 0.f;
 
     v16i acc[TN][TM];
 #pragma unroll
@@ -305,7 +368,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     for (int kt = 0; kt < KT; ++kt) {
         // stage kt has landed once at most the loads of stage kt + 1 are outstanding
         if (kt + 1 < KT)
-            __builtin_amdgcn_s_waitcnt(0x3f70 | (IX + IW));  // vmcnt(IX + IW), expcnt / lgkmcnt unchanged (max)
+            __builtin_amdgcn_s_waitcnt(0x3f70 | (IX + IW + IS));  // vmcnt(one stage's loads), other counters max
         else
             __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
         // stage kt visible to all; everyone is done with stage kt - 1, whose buffer refills next. A bare s_barrier:
@@ -324,18 +387,37 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
             for (int j = 0; j < TM; ++j) xf[kk][j] = *reinterpret_cast<const v4i *>(x_s + fx[kk][j]);
         }
         __builtin_amdgcn_sched_barrier(0);
+        const v16i zero = {};
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
             for (int i = 0; i < TN; ++i)
 #pragma unroll
                 for (int j = 0; j < TM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk][i], xf[kk][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk][i], xf[kk][j],
+                                                                     (GRP && kk == 0) ? zero : acc[i][j], 0, 0, 0);
+        if (GRP) {
+            const float *s_s = sS[kt % STAGES];
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const float sj = s_s[wm * WMt + 32 * j + lr];
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        facc[GRP ? i : 0][GRP ? j : 0][e] =
+                            __builtin_fmaf((float)acc[i][j][e], sj, facc[GRP ? i : 0][GRP ? j : 0][e]);
+            }
+        }
     }
 
     __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
-    epilogue<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
-                          smem + wave * stage_bytes<TN>());
+    if constexpr (GRP)
+        epilogue<TM, TN, OUT>(facc, nullptr, sw, bias, Y, YsT, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
+                              smem + wave * stage_bytes<TN>());
+    else
+        epilogue<TM, TN, OUT>(acc, sx, sw, bias, Y, YsT, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
+                              smem + wave * stage_bytes<TN>());
 }
 
 // ------------------------------------------------------------------------------------------------ big tiles
@@ -441,7 +523,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
     }
     __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
-    epilogue<TM, TN, OUT>(acc, sx, sw, bias, Y, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
+    epilogue<TM, TN, OUT>(acc, sx, sw, bias, Y, nullptr, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
                           smem + wave * stage_bytes<TN>());
 }
 
@@ -455,7 +537,17 @@ struct TileCfg {
     double a, b;
 };
 
-inline TileCfg pick_tile(int M, int N, int K) {
+// Tile sets: per-token (all seven), grouped (the four tiles whose fp32 accumulators fit beside the int32 ones), and
+// INT8 output (grouped tiles with 64-column wavefront blocks).
+enum TileSet { TILES_ALL = 0, TILES_GROUPED = 1, TILES_Q8 = 2 };
+
+inline bool tile_in(const TileCfg &o, int set) {
+    if (set == TILES_ALL) return true;
+    const bool small = o.bm <= 128 && o.bn <= 128;
+    return set == TILES_GROUPED ? small : small && o.bn == 128;
+}
+
+inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
     const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
     static const TileCfg opts[] = {{256, 256, 1, 0.1488, 18.64}, {128, 256, 2, 0.2726, 10.38},
                                    {256, 128, 2, 0.2795, 9.88},  {128, 128, 3, 0.3312, 4.92},
@@ -463,11 +555,12 @@ inline TileCfg pick_tile(int M, int N, int K) {
                                    {64, 64, 6, 0.5926, 0.08}};
     if (force_bm && force_bn)
         for (const TileCfg &o : opts)
-            if (o.bm == force_bm && o.bn == force_bn) return o;
+            if (o.bm == force_bm && o.bn == force_bn && tile_in(o, set)) return o;
     const long cus = device_cus();
     double best = 1e300;
-    TileCfg bestc = opts[0];
+    TileCfg bestc = opts[3];
     for (const TileCfg &o : opts) {
+        if (!tile_in(o, set)) continue;
         const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
         const long per = (tiles + cus - 1) / cus;
         const double t = o.a * (double)per * o.bm * o.bn * (double)K * 1e-6 + o.b * (double)((per + o.resident - 1) / o.resident);
@@ -508,6 +601,27 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
 #undef LFM2Q_GEMM
 }
 
+// grouped-64 activation scales (sxT [K/64, M]); OUT_Q8*: Y = Yq int8 [M, N], YsT [N/64, M]
+template <int OUT>
+void launch_gemm_grouped(const int8_t *A, const int8_t *B, const float *sxT, const float *sw, const uint16_t *bias,
+                         void *Y, float *YsT, int M, int N, int K, hipStream_t st) {
+    const TileCfg t = pick_tile(M, N, K, out_q8(OUT) ? TILES_Q8 : TILES_GROUPED);
+    static const int sh = env_int("LFM2Q_GEMM_SWZ", 2);
+    const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
+#define LFM2Q_GEMM(BM_, BN_)                                                                                        \
+    if (t.bm == BM_ && t.bn == BN_) {                                                                                \
+        gemm_i8_kernel<BM_, BN_, OUT, true><<<grid, GT, 0, st>>>(A, B, sxT, sw, bias, Y, M, N, K, sh, YsT);          \
+        return;                                                                                                      \
+    }
+    LFM2Q_GEMM(128, 128)
+    LFM2Q_GEMM(64, 128)
+    if constexpr (!out_q8(OUT)) {
+        LFM2Q_GEMM(128, 64)
+        LFM2Q_GEMM(64, 64)
+    }
+#undef LFM2Q_GEMM
+}
+
 int check_gemm(const char *name, const int8_t *A, const int8_t *B, const void *Y, int M, int N, int K) {
     LFM2Q_REQUIRE(A && B && Y, LFM2Q_ERR_ARG, "%s: null pointer", name);
     LFM2Q_REQUIRE(M >= 1 && N >= 1 && K >= 16, LFM2Q_ERR_SHAPE, "%s: need M, N >= 1 and K >= 16 (M=%d N=%d K=%d)",
@@ -534,6 +648,37 @@ extern "C" int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, 
     else
         launch_gemm<OUT_BF16>(A, B, sa, sb, bias, Y, M, N, K, (hipStream_t)stream);
     return launch_status("gemm_i8");
+}
+
+extern "C" int lfm2q_gemm_i8_grouped(const int8_t *A, const float *saT, const int8_t *B, const float *sb,
+                                     const lfm2q_bf16 *bias, lfm2q_bf16 *Y, int M, int N, int K, int gelu,
+                                     lfm2q_stream_t stream) {
+    if (int st = check_gemm("gemm_i8", A, B, Y, M, N, K)) return st;
+    LFM2Q_REQUIRE(saT && sb, LFM2Q_ERR_ARG, "gemm_i8: sxT and sw are required");
+    LFM2Q_REQUIRE(K % 64 == 0, LFM2Q_ERR_SHAPE, "gemm_i8: grouped activation scales need K %% 64 == 0 (K=%d)", K);
+    LFM2Q_REQUIRE((long)(K / 64) * M * 4 < (1L << 31), LFM2Q_ERR_SHAPE, "gemm_i8: sxT must be smaller than 2 GiB");
+    if (gelu)
+        launch_gemm_grouped<OUT_BF16_GELU>(A, B, saT, sb, bias, Y, nullptr, M, N, K, (hipStream_t)stream);
+    else
+        launch_gemm_grouped<OUT_BF16>(A, B, saT, sb, bias, Y, nullptr, M, N, K, (hipStream_t)stream);
+    return launch_status("gemm_i8");
+}
+
+extern "C" int lfm2q_gemm_i8_q(const int8_t *A, const float *saT, const int8_t *B, const float *sb,
+                               const lfm2q_bf16 *bias, int8_t *Yq, float *YsT, int M, int N, int K, int gelu,
+                               lfm2q_stream_t stream) {
+    if (int st = check_gemm("gemm_i8_q", A, B, Yq, M, N, K)) return st;
+    LFM2Q_REQUIRE(saT && sb && YsT, LFM2Q_ERR_ARG, "gemm_i8_q: sxT, sw and ysT are required");
+    LFM2Q_REQUIRE(K % 64 == 0 && N % 64 == 0, LFM2Q_ERR_SHAPE, "gemm_i8_q: need K %% 64 == 0 and N %% 64 == 0 (N=%d K=%d)",
+                  N, K);
+    LFM2Q_REQUIRE((long)(K / 64) * M * 4 < (1L << 31), LFM2Q_ERR_SHAPE, "gemm_i8_q: sxT must be smaller than 2 GiB");
+    LFM2Q_REQUIRE(aligned16(sb) && ((uintptr_t)bias & 7) == 0 && ((uintptr_t)Yq & 7) == 0, LFM2Q_ERR_ALIGN,
+                  "gemm_i8_q: sw must be 16-byte, bias and yq 8-byte aligned");
+    if (gelu)
+        launch_gemm_grouped<OUT_Q8_GELU>(A, B, saT, sb, bias, Yq, YsT, M, N, K, (hipStream_t)stream);
+    else
+        launch_gemm_grouped<OUT_Q8>(A, B, saT, sb, bias, Yq, YsT, M, N, K, (hipStream_t)stream);
+    return launch_status("gemm_i8_q");
 }
 
 extern "C" int lfm2q_gemm_i8_i32(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K,

@@ -1,0 +1,53 @@
+// Symmetric INT8 quantization of bf16 values, shared by the standalone quantizers, the fused producers and the
+// INT8-output GEMM epilogue, so every path that quantizes the same bf16 values produces the same bytes.
+#pragma once
+
+#include "common.hpp"
+
+namespace lfm2q {
+
+// q = rint(x / s) with round-half-even (the reference's integer clamp to [-127, 127] never binds: |x| <= amax keeps
+// |x / s| < 127.5). x / s is evaluated as t = x * fl(1 / s): two roundings put t within 127.5 * 2^-23 < 2^-16 of the
+// real quotient, and the correctly rounded quotient fl(x / s) is within half an ulp (<= 2^-17) of it, so unless t
+// lies within 2^-15 of a half-integer, rint(t) and rint(fl(x / s)) are the same integer. Near a half-integer the
+// IEEE quotient itself is computed; the test runs per 8 values and the division only when one of them needs it.
+__device__ __forceinline__ bool near_half(float t) {
+    const float f = t - floorf(t);
+    return fabsf(f - 0.5f) < 0.000030517578125f;  // 2^-15
+}
+
+// 8 bf16 (one 16-byte vector) -> 8 int8 packed in two dwords
+__device__ __forceinline__ void quant8(v4i xv, float s, float r, int &lo, int &hi) {
+    float v[8], t[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[2 * j] = bf2f_lo((uint32_t)xv[j]);
+        v[2 * j + 1] = bf2f_hi((uint32_t)xv[j]);
+    }
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        t[e] = v[e] * r;
+        any |= near_half(t[e]);
+    }
+    if (__builtin_expect(any, 0)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (near_half(t[e])) t[e] = v[e] / s;
+    }
+    int q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = (int)rintf(t[e]);
+    lo = (q[0] & 255) | ((q[1] & 255) << 8) | ((q[2] & 255) << 16) | ((q[3] & 255) << 24);
+    hi = (q[4] & 255) | ((q[5] & 255) << 8) | ((q[6] & 255) << 16) | ((q[7] & 255) << 24);
+}
+
+__device__ __forceinline__ float absmax8(v4i xv, float m) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf2f_lo((uint32_t)xv[j])), fabsf(bf2f_hi((uint32_t)xv[j]))));
+    return m;
+}
+
+__device__ __forceinline__ float scale_of(float amax) { return fmaxf(amax, 1e-8f) / 127.f; }
+
+}  // namespace lfm2q

@@ -30,6 +30,8 @@ SIGNATURES = {
     "lfm2q_add_layernorm_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _P],
     "lfm2q_silu_mul_q": [_P, _P, _P, _P, _I, _I, _I, _P],
     "lfm2q_gemm_i8": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "lfm2q_gemm_i8_grouped": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "lfm2q_gemm_i8_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_i32": [_P, _P, _P, _I, _I, _I, _P],
 }
 

@@ -5,8 +5,8 @@
   a16 (W8A16): BF16 activations against INT8 weights -- not provided by this build (Int8Linear(a8=False) raises).
 
 act_group() keeps the reference's environment semantics (LFM2_INT8_GROUP, LFM2_INT8_GROUP_KINDS, K > 2048 forced
-to groups of 64); grouped-64 activation scales are not provided by this build, so a layer that resolves to
-grouped scales raises RuntimeError when called. Set LFM2_INT8_GROUP=0 for per-token scales everywhere.
+to groups of 64): a layer quantizes its activations per token and group of 64 channels by default, per token with
+LFM2_INT8_GROUP=0. quant_out returns the next W8A8 layer's INT8 input straight from this GEMM's epilogue.
 """
 
 import os
@@ -40,7 +40,7 @@ def qbuf(rows, K, group, device):
 
 
 def quantize_rows(x2, group=0):
-    """[M, K] bf16 -> (int8 [M, K], fp32 scales [M]) with one absmax / 127 scale per row."""
+    """[M, K] bf16 -> (int8 [M, K], fp32 scales): [M] (absmax / 127 per row) or, group=64, [K / 64, M]."""
     M, K = x2.shape
     q = torch.empty(x2.shape, device=x2.device, dtype=torch.int8)
     s = torch.empty((K // 64, M) if group else (M,), device=x2.device, dtype=torch.float32)
@@ -63,9 +63,15 @@ class Int8Linear:
         self.ext = int8_ext()
 
     def __call__(self, x, gelu=False, quant_out=False):
-        """x: bf16 [..., K], or an already quantized (int8 [..., K], scales) pair -> bf16 [..., N]."""
+        """x: bf16 [..., K], or an already quantized (int8 [..., K], scales) pair -> bf16 [..., N].
+        quant_out: return (int8 [M, N], scales [N/64, M]), the next W8A8 layer's grouped input, quantized in this
+        GEMM's epilogue (grouped activation scales, N % 64 == 0); src/lfm2opt/int8.py:70-80."""
         if quant_out:
-            raise RuntimeError("Int8Linear: quant_out (the INT8-output epilogue) is not provided by this build")
+            xq, sx = x if isinstance(x, tuple) else quantize_rows(x.reshape(-1, self.K).contiguous(), 64)
+            M = xq.numel() // self.K
+            yq, ys = qbuf(M, self.N, 64, xq.device)
+            self.ext.gemm_i8_q(xq, sx, self.q, self.s, self.bias, yq, ys, gelu)
+            return yq, ys
         if not self.a8:
             raise RuntimeError("Int8Linear: W8A16 (a8=False) is not provided by this build")
         if isinstance(x, tuple):

@@ -193,27 +193,52 @@ class DecodeOps:
 
 
 class Int8Ops:
-    """INT8 prefill / vision ops (reference: kernels/int8_gemm.cpp): quantizers, fused producers, W8A8 GEMM. The
-    grouped-64 GEMM (2-D sx), gemm_i8_q and gemm_w8 are not provided by this build: asking for them raises."""
+    """INT8 prefill / vision ops (reference: kernels/int8_gemm.cpp): quantizers, fused producers, the W8A8 GEMM with
+    per-token or grouped-64 activation scales, its INT8-output form gemm_i8_q. The W8A16 gemm_w8 is not provided."""
 
     def __init__(self):
         _capi.lib()
 
     def gemm_i8(self, xq, sx, w, sw, bias, y, gelu):
-        """W8A8: y [M, N] = bf16(gelu?((xq . w^T) * sx[m] * sw[n] + bias[n])), exact int32 accumulation.
+        """W8A8: y [M, N] = bf16(gelu?((xq . w^T) * sx[m] * sw[n] + bias[n])), exact int32 accumulation; with 2-D sx
+        [K/64, M] (grouped-64 activation scales) the per-group sums fold into fp32 with their scales first.
         Reference: gemm_i8(), kernels/int8_gemm.cpp:39-50."""
         _check_t(xq, torch.int8, "xq")
         _check_t(sx, torch.float32, "sx")
         K = xq.size(-1)
         M = xq.numel() // K if K else 0
-        if sx.dim() == 2:
-            raise RuntimeError("gemm_i8: grouped activation scales (sx [K/64, M]) are not provided by this build")
-        if sx.numel() != M:
+        grouped = sx.dim() == 2
+        if not ((K % 64 == 0 and sx.size(0) == K // 64 and sx.size(1) == M) if grouped else sx.numel() == M):
             raise RuntimeError("sx shape")
         N = self._check_common(w, sw, bias, y, M, K)
         _same_device(xq, sx, w, sw, bias, y)
-        _capi.call("lfm2q_gemm_i8", xq.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias),
-                   y.data_ptr(), M, N, K, int(bool(gelu)), _capi.stream(xq))
+        _capi.call("lfm2q_gemm_i8_grouped" if grouped else "lfm2q_gemm_i8", xq.data_ptr(), sx.data_ptr(),
+                   w.data_ptr(), sw.data_ptr(), _capi.ptr(bias), y.data_ptr(), M, N, K, int(bool(gelu)),
+                   _capi.stream(xq))
+
+    def gemm_i8_q(self, xq, sxT, w, sw, bias, yq, ysT, gelu):
+        """Grouped W8A8 writing the next W8A8 GEMM's input: (yq [M, N], ysT [N/64, M]) = quant_groups(the bf16 output
+        gemm_i8 would write), bit-identical to that pair of calls. Reference: gemm_i8_q(), kernels/int8_gemm.cpp:53-69
+        (N % 128 there, N % 64 here)."""
+        for t, dt, name in ((xq, torch.int8, "xq"), (sxT, torch.float32, "sxT"), (w, torch.int8, "w"),
+                            (sw, torch.float32, "sw"), (yq, torch.int8, "yq"), (ysT, torch.float32, "ysT")):
+            _check_t(t, dt, name)
+        K = xq.size(-1)
+        M = xq.numel() // K if K else 0
+        N = w.size(0)
+        if not (sxT.dim() == 2 and K % 64 == 0 and sxT.size(0) == K // 64 and sxT.size(1) == M):
+            raise RuntimeError("sxT shape")
+        if not (w.dim() == 2 and w.size(1) == K and N % 64 == 0 and sw.numel() == N):
+            raise RuntimeError("w [N, K] with N % 64 == 0")
+        if not (yq.numel() == M * N and ysT.dim() == 2 and ysT.size(0) == N // 64 and ysT.size(1) == M):
+            raise RuntimeError("yq / ysT shape")
+        if bias is not None:
+            _check_bf16(bias, "bias")
+            if bias.numel() != N:
+                raise RuntimeError("bias shape")
+        _same_device(xq, sxT, w, sw, bias, yq, ysT)
+        _capi.call("lfm2q_gemm_i8_q", xq.data_ptr(), sxT.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias),
+                   yq.data_ptr(), ysT.data_ptr(), M, N, K, int(bool(gelu)), _capi.stream(xq))
 
     def gemm_i8_i32(self, xq, w, c):
         """The exact int32 accumulators c [M, N] = xq [M, K] . w [N, K]^T (the torch._int_mm analogue)."""

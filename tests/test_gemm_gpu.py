@@ -174,8 +174,8 @@ def test_gemm_argument_errors(E):
     with pytest.raises(RuntimeError, match="K % 16"):
         E.gemm_i8(torch.zeros(4, 40, device="cuda", dtype=torch.int8), sx,
                   torch.zeros(8, 40, device="cuda", dtype=torch.int8), sw, None, y, False)
-    with pytest.raises(RuntimeError, match="grouped"):
-        E.gemm_i8(xq, torch.ones(1, 4, device="cuda"), w, sw, None, y, False)
+    with pytest.raises(RuntimeError, match="sx shape"):  # grouped scales must be [K/64, M]
+        E.gemm_i8(xq, torch.ones(2, 4, device="cuda"), w, sw, None, y, False)
     with pytest.raises(RuntimeError, match="multiple of 8"):
         E.quant_rows(torch.zeros(2, 12, device="cuda", dtype=torch.bfloat16), torch.empty(2, 12, device="cuda",
                      dtype=torch.int8), torch.empty(2, device="cuda"))

@@ -1,0 +1,148 @@
+"""Grouped-64 W8A8 GEMM and its INT8-output form on the GPU (through the C ABI via lfm2opt.kernels.int8_ext()).
+
+Parity bar: the grouped fold is the reference's operation sequence (exact int32 partial per 64-wide K group,
+facc = fma((float)part, sxT[g, m], facc) in group order, then facc * sw + b), so the bf16 output is bit-exact against
+the oracle without GELU and within 1 bf16 ulp with it (tests/test_int8_gemm.py:81-104 accepts far more: 1.05 x the
+bf16 rounding error of the exact result, also checked here at full shape); gemm_i8_q is bit-identical to the grouped
+gemm_i8 followed by grouped quant_rows (tests/test_int8_gemm.py:107-120).
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import dev, dev_bf16, host_bits, ulp_dist
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def E(cuda):
+    from lfm2opt.kernels import int8_ext
+
+    return int8_ext()
+
+
+def operands(seed, M, K, N, bias):
+    r = np.random.default_rng(seed)
+    x = oracle.f2bf(r.standard_normal((M, K)).astype(np.float32))
+    x[:, 7] = oracle.f2bf(np.full(M, 25.0, np.float32))  # an outlier channel: its group gets a large scale
+    w = oracle.f2bf((r.standard_normal((N, K)) * 0.02).astype(np.float32))
+    xq, sxT = oracle.quant_groups(x)
+    wq, sw = oracle.quant_rows(w)
+    b = oracle.f2bf(r.standard_normal(N).astype(np.float32)) if bias else None
+    return xq, sxT, wq, sw, b
+
+
+def run_grouped(E, xq, sxT, wq, sw, b, gelu):
+    M, N = xq.shape[0], wq.shape[0]
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(dev(xq), dev(sxT), dev(wq), dev(sw), None if b is None else dev_bf16(b), y, gelu)
+    return y
+
+
+@pytest.mark.parametrize("M,K,N,bias,gelu", [(37, 320, 24, True, False), (300, 1152, 520, False, False),
+                                             (129, 4352, 72, True, False), (65, 2048, 3072, False, True),
+                                             (17, 256, 1000, True, True)])
+def test_gemm_grouped_vs_oracle(E, M, K, N, bias, gelu):
+    xq, sxT, wq, sw, b = operands(M + K + N, M, K, N, bias)
+    y = run_grouped(E, xq, sxT, wq, sw, b, gelu)
+    ref = oracle.gemm_i8_grouped(xq, sxT, wq, sw, b, gelu)
+    u = int(ulp_dist(host_bits(y), ref).max())
+    assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
+
+
+@pytest.mark.parametrize("tile", ["128x128", "128x64", "64x128", "64x64"])
+def test_gemm_grouped_every_tile(E, tile, monkeypatch):
+    bm, bn = tile.split("x")
+    monkeypatch.setenv("LFM2Q_GEMM_BM", bm)
+    monkeypatch.setenv("LFM2Q_GEMM_BN", bn)
+    xq, sxT, wq, sw, b = operands(5, 200, 576, 264, True)
+    y = run_grouped(E, xq, sxT, wq, sw, b, False)
+    assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 2048, 16384), (4096, 8192, 2048)])
+def test_gemm_grouped_full_shape_error_rule(E, M, K, N):
+    """Full LFM2 prefill shapes: against the exact fp64 per-group sum on the GPU, the reference's rule (relative
+    Frobenius error <= 1.05 x that of the bf16 rounding of the exact result), and 48 sampled rows against the
+    oracle bit for bit."""
+    g = torch.Generator(device="cuda").manual_seed(M + N)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    wq = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+    sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    xq = torch.empty(M, K, device="cuda", dtype=torch.int8)
+    sxT = torch.empty(K // 64, M, device="cuda")
+    E.quant_rows(x, xq, sxT)
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(xq, sxT, wq, sw, None, y, False)
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(0))[:48].sort().values.cuda()
+    r = torch.zeros(48, N, device="cuda", dtype=torch.float64)
+    xs = xq[rows].double()
+    for gi in range(K // 64):
+        part = xs[:, gi * 64:(gi + 1) * 64] @ wq[:, gi * 64:(gi + 1) * 64].double().t()
+        r += part * sxT[gi, rows].double()[:, None]
+    r *= sw.double()[None, :]
+    e_ours = ((y[rows].double() - r).norm() / r.norm()).item()
+    e_round = ((r.to(torch.bfloat16).double() - r).norm() / r.norm()).item()
+    assert e_ours <= 1.05 * e_round + 1e-6, (e_ours, e_round)
+    ref = oracle.gemm_i8_grouped(xq[rows].cpu().numpy(), sxT[:, rows].cpu().numpy().copy(), wq.cpu().numpy(),
+                                 sw.cpu().numpy())
+    assert np.array_equal(host_bits(y[rows]), ref)
+
+
+@pytest.mark.parametrize("M,K,N,bias,gelu", [(300, 1152, 1152, True, False), (65, 2048, 3072, False, True),
+                                             (17, 256, 192, True, True), (129, 4352, 4352, False, False)])
+def test_gemm_i8_q_equals_gemm_then_quant_groups(E, M, K, N, bias, gelu):
+    xq, sxT, wq, sw, b = operands(M * 3 + N, M, K, N, bias)
+    y = run_grouped(E, xq, sxT, wq, sw, b, gelu)
+    rq = torch.empty(M, N, device="cuda", dtype=torch.int8)
+    rs = torch.empty(N // 64, M, device="cuda")
+    E.quant_rows(y, rq, rs)
+    q = torch.empty_like(rq)
+    s = torch.empty_like(rs)
+    E.gemm_i8_q(dev(xq), dev(sxT), dev(wq), dev(sw), None if b is None else dev_bf16(b), q, s, gelu)
+    assert torch.equal(q, rq) and torch.equal(s, rs), f"q mismatches {(q != rq).sum().item()}"
+
+
+def test_int8_linear_grouped_and_quant_out(cuda, monkeypatch):
+    """Int8Linear's default (grouped-64 activation scales) and quant_out path, against the ops by hand."""
+    monkeypatch.delenv("LFM2_INT8_GROUP", raising=False)
+    from lfm2opt.int8 import Int8Linear, quantize_rows
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    g = torch.Generator(device="cuda").manual_seed(4)
+    w = (torch.randn(256, 1152, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(256, device="cuda", generator=g).to(torch.bfloat16)
+    x = torch.randn(3, 50, 1152, device="cuda", generator=g).to(torch.bfloat16)
+    lin = Int8Linear(w, b)
+    assert lin.group == 64
+    y = lin(x)
+    xq, sx = quantize_rows(x.reshape(-1, 1152), 64)
+    ref = torch.empty(150, 256, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(xq, sx, lin.q, lin.s, b, ref, False)
+    assert torch.equal(y.reshape(150, 256), ref)
+    yq, ys = lin(x, gelu=True, quant_out=True)
+    rq, rs = torch.empty_like(yq), torch.empty_like(ys)
+    E.gemm_i8_q(xq, sx, lin.q, lin.s, b, rq, rs, True)
+    assert torch.equal(yq, rq) and torch.equal(ys, rs)
+
+
+def test_grouped_argument_errors(E):
+    xq = torch.zeros(4, 128, device="cuda", dtype=torch.int8)
+    w = torch.zeros(96, 128, device="cuda", dtype=torch.int8)
+    sxT, sw = torch.ones(2, 4, device="cuda"), torch.ones(96, device="cuda")
+    yq, ys = torch.empty(4, 96, device="cuda", dtype=torch.int8), torch.empty(1, 4, device="cuda")
+    with pytest.raises(RuntimeError, match=r"w \[N, K\] with N % 64 == 0"):
+        E.gemm_i8_q(xq, sxT, w, sw, None, yq, ys, False)
+    w64, sw64 = w[:64].contiguous(), sw[:64].contiguous()
+    yq64 = torch.empty(4, 64, device="cuda", dtype=torch.int8)
+    with pytest.raises(RuntimeError, match="sxT shape"):
+        E.gemm_i8_q(xq, torch.ones(4, device="cuda"), w64, sw64, None, yq64, ys, False)
+    with pytest.raises(RuntimeError, match="yq / ysT shape"):
+        E.gemm_i8_q(xq, sxT, w64, sw64, None, yq64, torch.empty(2, 4, device="cuda"), False)
+    torch.cuda.synchronize()
