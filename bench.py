@@ -361,6 +361,90 @@ def eager_kind(kind, B, reps, wfmt="int8"):
                       "us_per_launch_eager": round(us, 2), "bytes_per_launch": nbytes}))
 
 
+def grouped_results(reps):
+    """Grouped-64 W8A8 (grouped quant_rows + gemm_i8 with sxT [K/64, M]) and its INT8-output form gemm_i8_q, at the
+    prefill / vision shapes whose K is a multiple of 64, each call on its own weights (>= 512 MB rotated)."""
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    out = []
+    for M, K, N, bias, gelu, name in W8A8_SHAPES:
+        if K % 64:
+            continue
+        g = torch.Generator(device="cuda").manual_seed(M + K + N + 1)
+        ncopy = max(2, -(-512 * 2 ** 20 // (N * K)))
+        Ws = [torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g) for _ in range(ncopy)]
+        sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+        b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        xq = torch.empty(M, K, device="cuda", dtype=torch.int8)
+        sxT = torch.empty(K // 64, M, device="cuda")
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        yq = torch.empty(M, N, device="cuda", dtype=torch.int8)
+        ysT = torch.empty(N // 64, M, device="cuda") if N % 64 == 0 else None
+        E.quant_rows(x, xq, sxT)
+        g_gemm = capture(lambda: [E.gemm_i8(xq, sxT, W, sw, b, y, gelu) for W in Ws])
+        t_gemm, _ = time_graph(g_gemm, reps, 2)
+        ops = 2.0 * M * N * K
+        r = {"name": name, "M": M, "K": K, "N": N, "us_gemm": round(t_gemm * 1e3 / ncopy, 2),
+             "tops_gemm": round(ops / (t_gemm * 1e3 / ncopy) / 1e6, 1)}
+        if ysT is not None:
+            g_q = capture(lambda: [E.gemm_i8_q(xq, sxT, W, sw, b, yq, ysT, gelu) for W in Ws])
+            t_q, _ = time_graph(g_q, reps, 2)
+            r["us_gemm_i8_q"] = round(t_q * 1e3 / ncopy, 2)
+            r["tops_gemm_i8_q"] = round(ops / (t_q * 1e3 / ncopy) / 1e6, 1)
+            del g_q
+        out.append(r)
+        del g_gemm, Ws
+        torch.cuda.empty_cache()
+    return out
+
+
+def producer_results(reps):
+    """The activation quantizers and fused INT8 producers at prefill / vision shapes: algorithmic bytes (inputs and
+    outputs once, at their dtypes) per call / time."""
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    dev, bf = "cuda", torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(7)
+    res = []
+
+    def run(name, rows, L, fn, nbytes):
+        gr = capture(fn)
+        t, _ = time_graph(gr, reps, 2)
+        res.append({"op": name, "rows": rows, "len": L, "us": round(t * 1e3, 2), "gbs": round(nbytes / t / 1e6, 1)})
+        del gr
+
+    for rows, L, grouped in ((4096, 2048, False), (4096, 2048, True), (10240, 1152, False), (4096, 8192, True)):
+        x = torch.randn(rows, L, device=dev, generator=g).to(bf)
+        q = torch.empty(rows, L, device=dev, dtype=torch.int8)
+        s = torch.empty((L // 64, rows) if grouped else (rows,), device=dev)
+        run("quant_groups" if grouped else "quant_rows", rows, L, lambda: E.quant_rows(x, q, s), 3 * rows * L + 4 * s.numel())
+    for rows, H, grouped in ((4096, 2048, False), (4096, 2048, True)):
+        h = torch.randn(rows, H, device=dev, generator=g).to(bf)
+        y = torch.randn(rows, H, device=dev, generator=g).to(bf)
+        w = (torch.rand(H, device=dev, generator=g) + 0.5).to(bf)
+        q = torch.empty(rows, H, device=dev, dtype=torch.int8)
+        s = torch.empty((H // 64, rows) if grouped else (rows,), device=dev)
+        run(f"add_rmsnorm_q{' grouped' if grouped else ''}", rows, H, lambda: E.add_rmsnorm_q(h, y, w, q, s, 1e-5),
+            7 * rows * H + 2 * H + 4 * s.numel())
+    rows, Dm = 10240, 1152
+    h = torch.randn(rows, Dm, device=dev, generator=g).to(bf)
+    y = torch.randn(rows, Dm, device=dev, generator=g).to(bf)
+    w = (torch.rand(Dm, device=dev, generator=g) + 0.5).to(bf)
+    bb = torch.randn(Dm, device=dev, generator=g).to(bf)
+    q = torch.empty(rows, Dm, device=dev, dtype=torch.int8)
+    s = torch.empty(rows, device=dev)
+    run("add_layernorm_q", rows, Dm, lambda: E.add_layernorm_q(h, y, w, bb, q, s, 1e-6), 7 * rows * Dm + 4 * Dm + 4 * rows)
+    rows, I = 4096, 8192
+    gg = torch.randn(rows, 2 * I, device=dev, generator=g).to(bf)
+    q = torch.empty(rows, I, device=dev, dtype=torch.int8)
+    s = torch.empty(rows, device=dev)
+    run("silu_mul_q", rows, I, lambda: E.silu_mul_q(gg, q, s), 5 * rows * I + 4 * rows)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -438,6 +522,11 @@ def main():
                        "vision_layer_tops_gemm": round(vops / sum(r["us_gemm"] for r in vis) / 1e6, 1),
                        "vision_layer_tops_quant_gemm": round(vops / sum(r["us_quant_gemm"] for r in vis) / 1e6, 1),
                        "shapes": shapes}
+    if not args.no_w8a8:
+        log("grouped w8a8")
+        out["w8a8_grouped"] = grouped_results(max(5, args.steps // 10))
+        log("producers")
+        out["producers"] = producer_results(max(10, args.steps // 5))
     if not args.no_cpu:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline()
