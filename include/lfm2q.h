@@ -147,6 +147,13 @@ int lfm2q_gemm_i8_grouped(const int8_t *A, const float *saT, const int8_t *B, co
 int lfm2q_gemm_i8_q(const int8_t *A, const float *saT, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
                     int8_t *Yq, float *YsT, int M, int N, int K, int gelu, lfm2q_stream_t stream);
 
+/* W8A16 GEMM: Y[m, n] = bf16( g( acc[m, n] * sw[n] + bias[n] ) ), acc = sum_k X[m, k] W[n, k] accumulated in fp32
+ * on the bf16 matrix cores (int8 weights converted exactly), g = GELU-tanh if gelu != 0. X bf16 [M, K], W int8 [N, K],
+ * sw fp32 [N], bias bf16 [N] or NULL, Y bf16 [M, N]; K % 16 == 0. Replaces launch_gemm_w8
+ * kernels/int8_gemm.cu:762-771 (binding gemm_w8(), kernels/int8_gemm.cpp:72-79). */
+int lfm2q_gemm_w8(const lfm2q_bf16 *X, const int8_t *W, const float *sw, const lfm2q_bf16 *bias, lfm2q_bf16 *Y, int M,
+                  int N, int K, int gelu, lfm2q_stream_t stream);
+
 /* The exact int32 accumulators of the W8A8 GEMM: C[m, n] = sum_k A[m, k] B[n, k], C int32 [M, N]. No counterpart
  * entry point in the reference (whose tests use torch._int_mm for this, tests/test_int8_gemm.py:236). */
 int lfm2q_gemm_i8_i32(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, lfm2q_stream_t stream);

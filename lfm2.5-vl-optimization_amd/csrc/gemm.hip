@@ -420,6 +420,127 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
                               smem + wave * stage_bytes<TN>());
 }
 
+// LDS byte offset of 16-byte chunk c of a CPR-chunk row r: chunk c is stored at slot c ^ ((r / (8 / CPR * 2)) % CPR), so
+// the 16 rows a 16-lane phase of ds_read_b128 reads at one logical chunk hit 16 distinct bank groups (64 banks)
+template <int CPR>
+__device__ __forceinline__ int swzb(int r, int c) {
+    constexpr int SH = CPR == 8 ? 1 : 2;
+    return (r * CPR + (c ^ ((r >> SH) & (CPR - 1)))) * 16;
+}
+
+// ------------------------------------------------------------------------------------------------ W8A16
+// y[m, n] = bf16( gelu?( acc * sw[n] + b[n] ) ), acc = sum_k x[m, k] w[n, k] in fp32 on the bf16 matrix cores
+// (v_mfma_f32_32x32x16_bf16), the int8 weights converted to bf16 exactly in registers after their LDS read. Same
+// workgroup shape, XCD tile order, direct-to-LDS staging and staged epilogue as the W8A8 kernel; a stage is 64 k:
+// 128-byte activation rows (chunk c of row r at slot c ^ ((r >> 1) & 7)) and 64-byte weight rows (the W8A8 layout).
+
+// 8 int8 weights (two dwords) -> 8 bf16, exact (|q| <= 128 fits the 8-bit bf16 significand): the upper halves of the
+// fp32 conversions, paired by v_perm_b32
+__device__ __forceinline__ v8bf w8x8_to_bf16(uint32_t d0, uint32_t d1) {
+    auto hi2 = [](float lo, float hi) {
+        return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+    };
+    v4u r;
+    r[0] = hi2((float)(int8_t)d0, (float)(int8_t)(d0 >> 8));
+    r[1] = hi2((float)(int8_t)(d0 >> 16), (float)((int)d0 >> 24));
+    r[2] = hi2((float)(int8_t)d1, (float)(int8_t)(d1 >> 8));
+    r[3] = hi2((float)(int8_t)(d1 >> 16), (float)((int)d1 >> 24));
+    return __builtin_bit_cast(v8bf, r);
+}
+
+template <int BM, int BN, int OUT>
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_w8_kernel(
+    const uint16_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sw,
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ Y, int M, int N, int K) {
+    constexpr int BKE = 64;                       // k per stage
+    constexpr int WMt = BM / 2, WNt = BN / 2, TM = WMt / 32, TN = WNt / 32;
+    constexpr int IX = BM / 32, IW = BN / 64;     // direct loads per wavefront per stage: X 8 rows, W 16 rows each
+    constexpr int XS = BM * 2 * BKE, WS = BN * BKE;
+    static_assert(IX >= 1 && IW >= 1 && TM >= 1 && TN >= 1, "tile too small");
+    static_assert(4 * stage_bytes<TN>() <= STAGES * (XS + WS), "epilogue staging exceeds the LDS ring");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * (XS + WS)];
+    uint8_t(*sX)[XS] = reinterpret_cast<uint8_t(*)[XS]>(smem);
+    uint8_t(*sW)[WS] = reinterpret_cast<uint8_t(*)[WS]>(smem + STAGES * XS);
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = (K + BKE - 1) / BKE;
+    const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K * 2, 0x7fffffffL));
+    const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
+    // X: instruction j of wavefront w fills rows 8 (4 j + w) .. + 7; lane i -> row + i / 8, slot i % 8
+    uint32_t ox[IX], ow[IW];
+    int cx[IX], cw[IW];
+#pragma unroll
+    for (int j = 0; j < IX; ++j) {
+        const int row = 8 * (4 * j + wave) + (lane >> 3);
+        cx[j] = swzb<8>(row, lane & 7) - row * 128;  // byte offset of the logical chunk stored in this slot
+        ox[j] = (uint32_t)row * K * 2 + cx[j];
+    }
+#pragma unroll
+    for (int j = 0; j < IW; ++j) {
+        const int row = 16 * (4 * j + wave) + (lane >> 2);
+        cw[j] = 16 * ((lane & 3) ^ ((row >> 2) & 3));
+        ow[j] = (uint32_t)row * K + cw[j];
+    }
+    auto issue = [&](int kt) {
+        const int buf = kt % STAGES, k0 = kt * BKE;
+#pragma unroll
+        for (int j = 0; j < IX; ++j) {
+            const uint32_t vo = 2 * k0 + cx[j] < 2 * K ? ox[j] + 2 * k0 : 0xfffffff0u;
+            lds_dma16(rx, vo, lds_addr(sX[buf] + 1024 * (4 * j + wave)));
+        }
+#pragma unroll
+        for (int j = 0; j < IW; ++j) {
+            const uint32_t vo = k0 + cw[j] < K ? ow[j] + k0 : 0xfffffff0u;
+            lds_dma16(rw, vo, lds_addr(sW[buf] + 1024 * (4 * j + wave)));
+        }
+    };
+
+    v16f acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const int lr = lane & 31, lh = lane >> 5;
+
+    issue(0);
+    if (KT > 1) issue(1);
+    for (int kt = 0; kt < KT; ++kt) {
+        if (kt + 1 < KT)
+            __builtin_amdgcn_s_waitcnt(0x3f70 | (IX + IW));
+        else
+            __builtin_amdgcn_s_waitcnt(0x3f70);
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + 2 < KT) issue(kt + 2);
+        const uint8_t *x_s = sX[kt % STAGES], *w_s = sW[kt % STAGES];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {  // k 16 ks .. 16 ks + 15; this lane's k-half 8 lh .. 8 lh + 7
+            v8bf wf[TN], xf[TM];
+#pragma unroll
+            for (int i = 0; i < TN; ++i) {
+                const uint2 d = *reinterpret_cast<const uint2 *>(w_s + swz(wn * WNt + 32 * i + lr, ks, 2) + 8 * lh);
+                wf[i] = w8x8_to_bf16(d.x, d.y);
+            }
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+                xf[j] = *reinterpret_cast<const v8bf *>(x_s + swzb<8>(wm * WMt + 32 * j + lr, 2 * ks + lh));
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
+    epilogue<TM, TN, OUT>(acc, nullptr, sw, bias, Y, nullptr, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
+                          smem + wave * stage_bytes<TN>());
+}
+
 // ------------------------------------------------------------------------------------------------ big tiles
 // 256 x 256 tiles for the large GEMMs: 512 threads (8 wavefronts as 4 token blocks x 2 weight blocks, each 64 tokens x
 // 128 weight rows = 2 x 4 MFMA tiles, two wavefronts per SIMD). Per MAC this moves 2/3 of the L2 -> LDS operand
@@ -428,11 +549,6 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
 // LDS rows are BKT bytes = CPR 16-byte chunks; chunk c of row r sits at slot c ^ ((r / (8 / CPR * 2)) % CPR), so
 // the 16 rows a 16-lane phase of ds_read_b128 reads at one logical chunk hit 16 distinct 16-byte bank groups of the
 // 64-bank LDS.
-template <int CPR>
-__device__ __forceinline__ int swzb(int r, int c) {
-    constexpr int SH = CPR == 8 ? 1 : 2;
-    return (r * CPR + (c ^ ((r >> SH) & (CPR - 1)))) * 16;
-}
 
 template <int OUT, int BKT, int NST>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_big_kernel(
@@ -622,6 +738,23 @@ void launch_gemm_grouped(const int8_t *A, const int8_t *B, const float *sxT, con
 #undef LFM2Q_GEMM
 }
 
+template <int OUT>
+void launch_gemm_w8(const uint16_t *X, const int8_t *W, const float *sw, const uint16_t *bias, uint16_t *Y, int M,
+                    int N, int K, hipStream_t st) {
+    const TileCfg t = pick_tile(M, N, K, TILES_GROUPED);
+    const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
+#define LFM2Q_GEMM(BM_, BN_)                                                                                        \
+    if (t.bm == BM_ && t.bn == BN_) {                                                                                \
+        gemm_w8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(X, W, sw, bias, Y, M, N, K);                             \
+        return;                                                                                                      \
+    }
+    LFM2Q_GEMM(128, 128)
+    LFM2Q_GEMM(128, 64)
+    LFM2Q_GEMM(64, 128)
+    LFM2Q_GEMM(64, 64)
+#undef LFM2Q_GEMM
+}
+
 int check_gemm(const char *name, const int8_t *A, const int8_t *B, const void *Y, int M, int N, int K) {
     LFM2Q_REQUIRE(A && B && Y, LFM2Q_ERR_ARG, "%s: null pointer", name);
     LFM2Q_REQUIRE(M >= 1 && N >= 1 && K >= 16, LFM2Q_ERR_SHAPE, "%s: need M, N >= 1 and K >= 16 (M=%d N=%d K=%d)",
@@ -679,6 +812,21 @@ extern "C" int lfm2q_gemm_i8_q(const int8_t *A, const float *saT, const int8_t *
     else
         launch_gemm_grouped<OUT_Q8>(A, B, saT, sb, bias, Yq, YsT, M, N, K, (hipStream_t)stream);
     return launch_status("gemm_i8_q");
+}
+
+extern "C" int lfm2q_gemm_w8(const lfm2q_bf16 *X, const int8_t *W, const float *sw, const lfm2q_bf16 *bias,
+                             lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(X && W && sw && Y, LFM2Q_ERR_ARG, "gemm_w8: null pointer");
+    LFM2Q_REQUIRE(M >= 1 && N >= 1 && K >= 16 && K % 16 == 0, LFM2Q_ERR_SHAPE,
+                  "gemm_w8: need M, N >= 1 and K %% 16 == 0 (M=%d N=%d K=%d)", M, N, K);
+    LFM2Q_REQUIRE((long)M * K * 2 < (1L << 31) && (long)N * K < (1L << 31), LFM2Q_ERR_SHAPE,
+                  "gemm_w8: each operand must be smaller than 2 GiB (buffer offsets are 32-bit)");
+    LFM2Q_REQUIRE(aligned16(X) && aligned16(W), LFM2Q_ERR_ALIGN, "gemm_w8: x and w must be 16-byte aligned");
+    if (gelu)
+        launch_gemm_w8<OUT_BF16_GELU>(X, W, sw, bias, Y, M, N, K, (hipStream_t)stream);
+    else
+        launch_gemm_w8<OUT_BF16>(X, W, sw, bias, Y, M, N, K, (hipStream_t)stream);
+    return launch_status("gemm_w8");
 }
 
 extern "C" int lfm2q_gemm_i8_i32(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K,

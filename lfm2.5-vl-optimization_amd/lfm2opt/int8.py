@@ -2,7 +2,7 @@
 
   a8  (W8A8):  activations quantized on the fly (quantize_rows) with one scale per token, int8 x int8 GEMM on the
                matrix cores with exact int32 accumulation and the dequant (+ bias, GELU) epilogue.
-  a16 (W8A16): BF16 activations against INT8 weights -- not provided by this build (Int8Linear(a8=False) raises).
+  a16 (W8A16): BF16 activations against INT8 weights (gemm_w8), fp32 accumulation on the bf16 matrix cores.
 
 act_group() keeps the reference's environment semantics (LFM2_INT8_GROUP, LFM2_INT8_GROUP_KINDS, K > 2048 forced
 to groups of 64): a layer quantizes its activations per token and group of 64 channels by default, per token with
@@ -72,8 +72,6 @@ class Int8Linear:
             yq, ys = qbuf(M, self.N, 64, xq.device)
             self.ext.gemm_i8_q(xq, sx, self.q, self.s, self.bias, yq, ys, gelu)
             return yq, ys
-        if not self.a8:
-            raise RuntimeError("Int8Linear: W8A16 (a8=False) is not provided by this build")
         if isinstance(x, tuple):
             xq, sx = x
             y = torch.empty(xq.numel() // self.K, self.N, device=xq.device, dtype=torch.bfloat16)
@@ -81,6 +79,9 @@ class Int8Linear:
             return y.view(*xq.shape[:-1], self.N)
         x2 = x.reshape(-1, self.K)
         y = torch.empty(x2.shape[0], self.N, device=x.device, dtype=torch.bfloat16)
-        xq, sx = quantize_rows(x2.contiguous(), self.group)
-        self.ext.gemm_i8(xq, sx, self.q, self.s, self.bias, y, gelu)
+        if self.a8:
+            xq, sx = quantize_rows(x2.contiguous(), self.group)
+            self.ext.gemm_i8(xq, sx, self.q, self.s, self.bias, y, gelu)
+        else:
+            self.ext.gemm_w8(x2.contiguous(), self.q, self.s, self.bias, y, gelu)
         return y.view(*x.shape[:-1], self.N)

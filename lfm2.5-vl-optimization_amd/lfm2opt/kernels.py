@@ -194,7 +194,7 @@ class DecodeOps:
 
 class Int8Ops:
     """INT8 prefill / vision ops (reference: kernels/int8_gemm.cpp): quantizers, fused producers, the W8A8 GEMM with
-    per-token or grouped-64 activation scales, its INT8-output form gemm_i8_q. The W8A16 gemm_w8 is not provided."""
+    per-token or grouped-64 activation scales, its INT8-output form gemm_i8_q, and the W8A16 gemm_w8."""
 
     def __init__(self):
         _capi.lib()
@@ -239,6 +239,17 @@ class Int8Ops:
         _same_device(xq, sxT, w, sw, bias, yq, ysT)
         _capi.call("lfm2q_gemm_i8_q", xq.data_ptr(), sxT.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias),
                    yq.data_ptr(), ysT.data_ptr(), M, N, K, int(bool(gelu)), _capi.stream(xq))
+
+    def gemm_w8(self, x, w, sw, bias, y, gelu):
+        """W8A16: y [M, N] = bf16(gelu?((x . w^T) * sw[n] + bias[n])), bf16 x, int8 w, fp32 accumulation.
+        Reference: gemm_w8(), kernels/int8_gemm.cpp:72-79."""
+        _check_bf16(x, "x")
+        K = x.size(-1)
+        M = x.numel() // K if K else 0
+        N = self._check_common(w, sw, bias, y, M, K)
+        _same_device(x, w, sw, bias, y)
+        _capi.call("lfm2q_gemm_w8", x.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias), y.data_ptr(), M, N, K,
+                   int(bool(gelu)), _capi.stream(x))
 
     def gemm_i8_i32(self, xq, w, c):
         """The exact int32 accumulators c [M, N] = xq [M, K] . w [N, K]^T (the torch._int_mm analogue)."""

@@ -29,6 +29,7 @@ _SIGS = {
     "orc_quant_rows": ([_P, _I64, _I64, _P, _P], None),
     "orc_quant_groups": ([_P, _I64, _I64, _P, _P], None),
     "orc_add_rmsnorm": ([_P, _P, _P, _I64, _I64, ctypes.c_float, _P], None),
+    "orc_gemm_w8": ([_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P], None),
     "orc_add_layernorm": ([_P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P], None),
     "orc_gemm_i8_i32": ([_P, _P, _I64, _I64, _I64, _P], None),
     "orc_gemm_i8_epilogue": ([_P, _P, _P, _P, _I64, _I64, _INT, _P], None),
@@ -158,6 +159,17 @@ def gemm_i8_grouped(A, sxT, B, sw, bias=None, gelu=False):
     b = None if bias is None else _c(bias, np.uint16)
     Y = np.empty((M, N), np.uint16)
     lib().orc_gemm_i8_grouped(_p(A), _p(sxT), _p(B), _p(sw), _p(b), M, N, K, int(gelu), _p(Y))
+    return Y
+
+
+def gemm_w8(x, W, sw, bias=None, gelu=False):
+    """W8A16: bf16 x [M, K] (uint16 bits) . int8 W [N, K]^T in fp64 -> fp32, * sw[n] + b[n], GELU, bf16
+    (kernels/int8_gemm.cu:306-388, store_tile without activation scales)."""
+    x, W, sw = _c(x, np.uint16), _c(W, np.int8), _c(sw, np.float32)
+    (M, K), (N, _) = x.shape, W.shape
+    b = None if bias is None else _c(bias, np.uint16)
+    Y = np.empty((M, N), np.uint16)
+    lib().orc_gemm_w8(_p(x), _p(W), _p(sw), _p(b), M, N, K, int(gelu), _p(Y))
     return Y
 
 

@@ -193,6 +193,22 @@ void orc_gemm_i8_grouped(const int8_t *A, const float *sxT, const int8_t *B, con
         }
 }
 
+/* W8A16 (kernels/int8_gemm.cu:306-388 then store_tile with no activation scale): acc = sum_k x[m, k] w[n, k] in fp64
+ * (exact products, the kernel accumulates in fp32 in its own order), rounded once to fp32, then
+ * y = bf16(gelu?(acc * sw[n] + b[n])) with separately rounded ops. */
+void orc_gemm_w8(const uint16_t *X, const int8_t *W, const float *sw, const uint16_t *bias, int64_t M, int64_t N,
+                 int64_t K, int gelu, uint16_t *Y) {
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k) acc += (double)bf2f(X[m * K + k]) * (double)W[n * K + k];
+            float v = (float)acc * sw[n];
+            v = v + (bias ? bf2f(bias[n]) : 0.0f);
+            if (gelu) v = gelu_tanh(v);
+            Y[m * N + n] = f2bf(v);
+        }
+}
+
 /* ------------------------------------------------------------------------------------------ decode GEMVs */
 /* The GEMV accumulators are computed in fp64 (the sum of exact products) and rounded once to fp32, which is where
  * the reference kernel holds its fp32 warp sum; everything after that point follows the kernel's fp32 rounding

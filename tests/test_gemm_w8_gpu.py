@@ -1,0 +1,102 @@
+"""W8A16 GEMM (bf16 activations x int8 weights, fp32 accumulation on the bf16 matrix cores) on the GPU.
+
+Parity bar: the reference's own rule (tests/test_int8_gemm.py:178-195): relative Frobenius error against the fp64
+result at most 1.5 x that of the platform BLAS on the dequantized bf16 weights, + 1e-4; and per element
+max |err| / max |ref| <= 1e-2 against the CPU oracle (fp64 accumulation rounded once), on small shapes in full and
+on sampled rows of the full shapes.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from gpu_util import assert_close_bf16, dev, dev_bf16, host_bits
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def E(cuda):
+    from lfm2opt.kernels import int8_ext
+
+    return int8_ext()
+
+
+def operands(seed, M, K, N, bias):
+    r = np.random.default_rng(seed)
+    x = oracle.f2bf(r.standard_normal((M, K)).astype(np.float32))
+    W = r.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = (np.abs(r.standard_normal(N)) * 0.01 + 1e-3).astype(np.float32)
+    b = oracle.f2bf(r.standard_normal(N).astype(np.float32)) if bias else None
+    return x, W, sw, b
+
+
+def run(E, x, W, sw, b, gelu):
+    y = torch.empty(x.shape[0], W.shape[0], device="cuda", dtype=torch.bfloat16)
+    E.gemm_w8(dev_bf16(x), dev(W), dev(sw), None if b is None else dev_bf16(b), y, gelu)
+    return host_bits(y)
+
+
+@pytest.mark.parametrize("M,K,N,bias,gelu", [(37, 320, 24, True, False), (70, 1152, 100, False, False),
+                                             (33, 576, 40, True, True), (129, 4304, 72, True, False),
+                                             (1, 2048, 264, False, False)])
+def test_gemm_w8_vs_oracle(E, M, K, N, bias, gelu):
+    x, W, sw, b = operands(M + K + N, M, K, N, bias)
+    assert_close_bf16(run(E, x, W, sw, b, gelu), oracle.gemm_w8(x, W, sw, b, gelu),
+                      what=f"gemm_w8 {M}x{K}x{N}{' bias' if bias else ''}{' gelu' if gelu else ''}")
+
+
+@pytest.mark.parametrize("tile", ["128x128", "128x64", "64x128", "64x64"])
+def test_gemm_w8_every_tile(E, tile, monkeypatch):
+    bm, bn = tile.split("x")
+    monkeypatch.setenv("LFM2Q_GEMM_BM", bm)
+    monkeypatch.setenv("LFM2Q_GEMM_BN", bn)
+    x, W, sw, b = operands(3, 200, 576, 264, True)
+    assert_close_bf16(run(E, x, W, sw, b, False), oracle.gemm_w8(x, W, sw, b), what=f"gemm_w8 tile {tile}")
+
+
+@pytest.mark.parametrize("M,K,N,bias,gelu", [(64, 2048, 16384, False, False), (256, 8192, 2048, False, False),
+                                             (10240, 1152, 4304, True, True)])
+def test_gemm_w8_full_shape_error_rule(E, M, K, N, bias, gelu):
+    g = torch.Generator(device="cuda").manual_seed(M + N)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+    from lfm2opt.quant import quantize_int8
+
+    wq, sw = quantize_int8(w)
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_w8(x, wq, sw, b, y, gelu)
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(0))[:64].sort().values.cuda()
+    r64 = (x[rows].double() @ wq.double().t()) * sw.double()[None, :]
+    if b is not None:
+        r64 = r64 + b.double()
+    wd = (wq.float() * sw[:, None]).to(torch.bfloat16)
+    rc = F.linear(x[rows].float(), wd.float(), None if b is None else b.float()).to(torch.bfloat16)
+    if gelu:
+        r64 = F.gelu(r64, approximate="tanh")
+        rc = F.gelu(rc.float(), approximate="tanh").to(torch.bfloat16)
+    e_ours = ((y[rows].double() - r64).norm() / r64.norm()).item()
+    e_blas = ((rc.double() - r64).norm() / r64.norm()).item()
+    print(f"gemm_w8 {M}x{K}x{N}: rel err {e_ours:.3e} (torch on dequantized bf16 W {e_blas:.3e})")
+    assert e_ours <= 1.5 * e_blas + 1e-4
+    ro = oracle.gemm_w8(host_bits(x[rows]), wq.cpu().numpy(), sw.cpu().numpy(),
+                        None if b is None else host_bits(b), gelu)
+    assert_close_bf16(host_bits(y[rows]), ro, what=f"gemm_w8 {M}x{K}x{N} sampled rows vs oracle")
+
+
+def test_int8_linear_w8a16(cuda):
+    from lfm2opt.int8 import Int8Linear
+    from lfm2opt.kernels import int8_ext
+
+    g = torch.Generator(device="cuda").manual_seed(6)
+    w = (torch.randn(192, 1152, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(192, device="cuda", generator=g).to(torch.bfloat16)
+    x = torch.randn(4, 7, 1152, device="cuda", generator=g).to(torch.bfloat16)
+    lin = Int8Linear(w, b, a8=False)
+    y = lin(x, gelu=True)
+    ref = torch.empty(28, 192, device="cuda", dtype=torch.bfloat16)
+    int8_ext().gemm_w8(x.reshape(28, 1152), lin.q, lin.s, b, ref, True)
+    assert torch.equal(y.reshape(28, 192), ref)

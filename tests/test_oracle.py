@@ -432,3 +432,24 @@ def test_add_layernorm_two_level_rows_closed_form():
     wf, bf = oracle.bf2f(w), oracle.bf2f(b)
     for r in range(3):
         assert np.array_equal(x[r], oracle.f2bf(sign * wf + bf))
+
+
+# ------------------------------------------------------------------------------------------------ W8A16
+def test_gemm_w8_against_torch_fp64():
+    """acc in fp64 rounded once, then * sw + b: within 1 bf16 ulp of torch's fp64 (x @ w^T) * sw + b; bit-exact when
+    sw and x are powers of two (every intermediate exact)."""
+    M, K, N = 9, 384, 20
+    x = rand_bf16((M, K))
+    W = RNG.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = (np.abs(RNG.standard_normal(N)) * 0.01 + 1e-3).astype(np.float32)
+    b = rand_bf16((N,))
+    y = oracle.gemm_w8(x, W, sw, b)
+    r = (from_bits(x).double() @ torch.from_numpy(W).double().t()) * torch.from_numpy(sw).double() + from_bits(b).double()
+    assert ulps(y, bf16_bits(r.float())) <= 1
+    x2 = bf16_bits(torch.from_numpy((2.0 ** RNG.integers(-3, 3, (M, K))).astype(np.float32)))
+    sw2 = (2.0 ** RNG.integers(-10, -4, N)).astype(np.float32)
+    y2 = oracle.gemm_w8(x2, W, sw2)
+    r2 = (from_bits(x2).double() @ torch.from_numpy(W).double().t()) * torch.from_numpy(sw2).double()
+    assert np.array_equal(y2, bf16_bits(r2.float()))
+    yg = oracle.gemm_w8(x, W, sw, b, gelu=True)
+    assert ulps(yg, bf16_bits(F.gelu(r.float(), approximate="tanh"))) <= 1
