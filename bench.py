@@ -400,6 +400,37 @@ def grouped_results(reps):
     return out
 
 
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def w8a16_results(reps):
+    """W8A16 gemm_w8 (the large-batch decode fallback and a vision layer), each call on its own weights."""
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    out = []
+    for M, K, N, bias, gelu, name in ((64, 2048, 16384, False, False, "decode M=64 w1|w3"),
+                                      (256, 2048, 16384, False, False, "decode M=256 w1|w3"),
+                                      (256, 8192, 2048, False, False, "decode M=256 w2"),
+                                      (10240, 1152, 4304, True, True, "vision fc1+gelu")):
+        g = torch.Generator(device="cuda").manual_seed(M + K + N + 2)
+        ncopy = max(2, -(-512 * 2 ** 20 // (N * K)))
+        Ws = [torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g) for _ in range(ncopy)]
+        sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+        b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        gr = capture(lambda: [E.gemm_w8(x, W, sw, b, y, gelu) for W in Ws])
+        t, _ = time_graph(gr, reps, 2)
+        us = t * 1e3 / ncopy
+        nbytes = N * K + 2 * M * K + 2 * M * N + 4 * N
+        out.append({"name": name, "M": M, "K": K, "N": N, "us": round(us, 2),
+                    "tflops": round(2.0 * M * N * K / us / 1e6, 1), "gbs": round(nbytes / us / 1e3, 1)})
+        del gr, Ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def producer_results(reps):
     """The activation quantizers and fused INT8 producers at prefill / vision shapes: algorithmic bytes (inputs and
     outputs once, at their dtypes) per call / time."""
@@ -525,6 +556,8 @@ def main():
     if not args.no_w8a8:
         log("grouped w8a8")
         out["w8a8_grouped"] = grouped_results(max(5, args.steps // 10))
+        log("w8a16")
+        out["w8a16"] = {"peak_tflops_bf16": BF16_PEAK_TFLOPS, "shapes": w8a16_results(max(5, args.steps // 10))}
         log("producers")
         out["producers"] = producer_results(max(10, args.steps // 5))
     if not args.no_cpu:
