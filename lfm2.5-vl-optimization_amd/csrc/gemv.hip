@@ -6,12 +6,12 @@
 //                     of each row with non-temporal loads (a wavefront load = 1 KiB contiguous of one row), all of
 //                     a lane's chunks are in flight before the first FMA. int8 -> fp32 is one SDWA convert per
 //                     weight; the row sum is a wave64 butterfly. No LDS.
-//   gemv_mfma_kernel  batch 2..16. A workgroup owns 16 output rows; its NWK wavefronts split K. Each lane loads
-//                     16 weights of one row (row = lane % 16, k-quarter = lane / 16), converts them exactly to
-//                     bf16 in registers and feeds v_mfma_f32_16x16x32_bf16 with the activations as the A operand
-//                     (16 batch rows x 32 k) and the weights as B (32 k x 16 output rows). The NWK partial 16x16
-//                     tiles meet in LDS. The matrix cores take the batch FMAs off the VALU, so the kernel stays
-//                     HBM-bound at B = 16, where a VALU GEMV would need 17 VALU ops per weight.
+//   gemv_mfma_kernel  batch 2..16. A workgroup owns 16 (or 32) output rows; its NWK wavefronts split K into
+//                     128-k blocks. A wave's two loads per block and tile row cover 16 whole 128-byte lines; the
+//                     weights are converted exactly to bf16 in registers and feed v_mfma_f32_16x16x32_bf16 with the
+//                     activations as the A operand (16 batch rows x 32 k) and the weights as B (32 k x 16 output
+//                     rows). The NWK partial 16x16 tiles meet in LDS. The matrix cores take the batch FMAs off the
+//                     VALU (1.5 VALU ops per weight at any batch), so the kernel stays HBM-bound up to B = 16.
 // The per-row accumulation order of each kernel does not depend on which epilogue runs or on how many rows a
 // wavefront owns, so the fused epilogues are bit-identical to the plain GEMV followed by the separate op.
 //
@@ -21,6 +21,8 @@
 #include "status.hpp"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 namespace lfm2q {
 namespace {
@@ -256,106 +258,216 @@ __device__ __forceinline__ v8bf i8x8_to_bf16(int d0, int d1) {
 }
 __device__ __forceinline__ v8bf as_bf16x8(v4i v) { return __builtin_bit_cast(v8bf, v); }
 
-// WG = NWK wavefronts and 16 RT output rows (EPI_SWIGLU: plus the matching 16 RT rows of w3, so NT = 2 RT weight
-// tiles). Wavefront w covers k in [w K/NWK, (w+1) K/NWK) in stages of U 64-k steps; all loads of a stage are
-// issued before its MFMAs. In a step, lane (col = l%16, kq = l/16) loads k0 + 16 kq .. +15 of weight row
-// (tile row) + col for every tile and of activation row col (if col < B): the activation loads are shared by the
-// NT tiles, so the L2 traffic for x is B/(8 RT) of the weight bytes.
-// MFMA layout (v_mfma_f32_16x16x32_bf16): A[i][k] from lane i + 16 (k/8), B[k][j] from lane j + 16 (k/8),
-// D[i][j] in lane j + 16 (i/4), element i%4. A and B use the same k <-> (lane group, slot) map, so the product
-// pairs x[m][k] with W[n][k] whatever order the hardware sums the 32 k in.
-// The NWK partial tiles are summed in LDS in wavefront order, one tile at a time.
-template <typename WT, int RT, int NWK, int U, int EPI>
+// A workgroup owns RT tiles of TR = 16 / KS output rows (EPI_SWIGLU: plus the matching rows of w3, so NT = 2 RT
+// weight tiles); its NWK wavefronts split K into contiguous runs of 128-k blocks, KB blocks per stage (at most 8
+// weight loads per lane), every load of a stage issued before its MFMAs. v_mfma_f32_16x16x32_bf16 computes
+// D[i][c] += sum_k A[i][k] B[k][c] over 16 x 16 outputs; column c of B is weight row c % TR over part c / TR of the
+// wavefront's K run (KS parts of P blocks), row i of A is batch row i % TR over part i / TR of the same run, so the
+// KS diagonal blocks D[TR s + b][TR s + r] are partial sums of output (b, r) and the others are discarded. KS = 2
+// (8-row tiles, batches up to 8) doubles the workgroups of a narrow matrix at the price of idle MFMA lanes.
+// MFMA m (m = 0..3) of a block takes 8 consecutive k per lane (lane l = c + 16 g):
+//   int8 weights: k = 32 g + 8 m + s. A tile block (16 columns x 128 bytes) is read by two wave loads of 8 whole
+//                 128-byte lines each (load q: lane l reads row l % 8 [+ 8 q for KS = 1] of part q [KS = 2], bytes
+//                 16 (l / 8)), so every load covers full cache lines; one DPP row rotation by 8 lanes and three
+//                 selects per dword then give lane (c, g) bytes 32 g .. 32 g + 31 of its column, converted exactly
+//                 to bf16.
+//   bf16 weights: k = 32 m + 8 g + s. Lane (c, g) loads the 16-byte pieces at byte offsets 16 g + 64 m of its
+//                 column's block (piece m feeds MFMA m as loaded).
+// The activation operand A holds x[batch][the same 8 k] in lane i + 16 g: four loads of 64 contiguous bytes per
+// row and block (batch rows >= B read zeros), for int8 weights rearranged by a permlane transpose. A[i][k] and
+// B[k][c] follow the same k <-> (lane group, slot) map, so the product pairs x[b][k] with W[r][k] whatever order the
+// hardware sums the 32 k in; D[i][c] lands in lane c + 16 (i / 4), element i % 4.
+// Every load goes through a buffer resource: rows past N, batch rows past B and k past K (a trailing half block)
+// read zeros without a memory access. The partial tiles (NWK wavefronts x KS parts) are summed in LDS in a fixed
+// order, every thread of the workgroup taking some of the outputs.
+template <typename WT, int KS, int RT, int NWK, int EPI>
 __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restrict__ W, const float *__restrict__ scale,
                                                              const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
                                                              int B, int N, int K, int S) {
+    constexpr bool I8 = sizeof(WT) == 1;
+    constexpr int TR = 16 / KS;             // weight rows per tile, batch rows per part
     constexpr int NT = (EPI == EPI_SWIGLU ? 2 : 1) * RT;
-    constexpr int WL = sizeof(WT) == 1 ? 1 : 2;  // 16-byte weight loads per lane per step
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int col = lane & 15, kq = lane >> 4;
-    const int nbase = blockIdx.x * 16 * RT;
-    const WT *wp[NT];
+    constexpr int WL = I8 ? 2 : 4;          // 16-byte weight loads per lane per tile per block
+    constexpr int KB = NT * WL >= 8 ? 1 : 8 / (NT * WL);  // blocks per stage
+    constexpr uint32_t BB = 128 * sizeof(WT);  // bytes of one row's block
+    constexpr uint32_t OOR = 0x40000000u;   // an offset past every range below: the load returns zeros
+    // the k range is wavefront-uniform: block conditions and offsets stay scalar where the lane does not matter
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int nbase = blockIdx.x * TR * RT;
+    const uint32_t rowb = (uint32_t)K * sizeof(WT);
+    rsrc_t wr[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const int nl = min(nbase + 16 * (t % RT) + col, N - 1);
-        wp[t] = W + (size_t)((EPI == EPI_SWIGLU && t >= RT ? S : 0) + nl) * K;
+        const int r0 = nbase + TR * (t % RT);
+        const int rows = __builtin_amdgcn_readfirstlane(max(0, min(TR, N - r0)));  // keep the resource scalar
+        wr[t] = make_rsrc(W + (size_t)((EPI == EPI_SWIGLU && t >= RT ? S : 0) + min(r0, N - 1)) * K,
+                          (uint32_t)rows * rowb);
     }
-    const bool xm = col < B;
-    const uint16_t *xp = x + (size_t)(xm ? col : 0) * K;
-    const int ks = K / NWK, kb = wave * ks, ke = kb + ks;
+    const rsrc_t xr = make_rsrc(x, (uint32_t)B * K * 2u);
+    const int c8 = lane >> 3;  // int8: the lane's 16-byte chunk of a 128-byte row block
+    const uint32_t woff = I8 ? (lane & 7) * rowb + 16 * c8 : (c % TR) * rowb + 16 * g;
+    const int cpart = c / TR;  // part of this lane's B column (bf16) and A row
+    const uint32_t xoff = (uint32_t)(c % TR) * K * 2u + 16 * g;
+
+    // this wavefront's blocks [kb0, kb1): part s is kb0 + s P .. kb0 + s P + P - 1
+    const int nblk = (K + 127) / 128;
+    const int per = (nblk + NWK - 1) / NWK;
+    const int kb0 = wave * per, kb1 = min(nblk, kb0 + per);
+    const int P = (per + KS - 1) / KS;
+
+    // Output elements (tile t, batch row b, row r -> y[b][nbase + TR t + r]). Through LDS (NWK > 1 or KS > 1):
+    // thread threadIdx.x + 64 NWK i takes element TR TR t + TR b + r; otherwise each lane keeps the 4 RT elements
+    // its MFMA accumulators hold (r = c, b = 4 g + e).
+    constexpr bool VIA_LDS = NWK > 1 || KS > 1;
+    constexpr int TE = TR * TR;
+    constexpr int EL = VIA_LDS ? (RT * TE + 64 * NWK - 1) / (64 * NWK) : 4 * RT;
+    struct Coord {
+        int t, b, r;
+    };
+    auto coord = [&](int i) -> Coord {
+        if constexpr (VIA_LDS) {
+            const int idx = (int)threadIdx.x + i * 64 * NWK;
+            return {idx / TE, (idx % TE) / TR, idx % TR};
+        } else {
+            return {i >> 2, 4 * g + (i & 3), c};
+        }
+    };
+    // the epilogue's operands (scales, residual values) are read before the weight stream starts, so their
+    // latency is not paid again after the last MFMA
+    float sg[EL], su[EL];
+    uint32_t hr[EL];
+#pragma unroll
+    for (int i = 0; i < EL; ++i) {
+        const Coord e = coord(i);
+        const int n = min(nbase + TR * e.t + e.r, N - 1);  // rows past N are never stored
+        sg[i] = scale ? scale[n] : 1.f;
+        su[i] = (EPI == EPI_SWIGLU && scale) ? scale[S + n] : 1.f;
+        hr[i] = (EPI == EPI_RESIDUAL && e.t < RT && e.b < B) ? y[(size_t)e.b * N + n] : 0u;
+    }
 
     v4f acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    for (int s0 = kb; s0 < ke; s0 += 64 * U) {
-        v4i wv[U][NT][WL], xv[U][2];
+    for (int b0 = kb0; b0 < kb0 + P; b0 += KB) {
+        v4i wv[KB][NT][WL], xv[KB][4];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int k = s0 + 64 * u + 16 * kq;
-            const bool in = s0 + 64 * u < ke;
+        for (int u = 0; u < KB; ++u) {
+            const int b = b0 + u;  // block of part 0; part s reads block b + s P
+            const bool step = b < kb0 + P;
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+            for (int h = 0; h < WL; ++h) {
+                uint32_t o;
+                if constexpr (I8) {
+                    const int bh = b + (KS == 2 ? h * P : 0);
+                    const bool in = step && bh < kb1 && bh * 128 + 16 * c8 < K;
+                    o = in ? (KS == 1 ? 8 * h * rowb : 0u) + bh * BB : OOR;
+                } else {
+                    const int bl = b + cpart * P;
+                    const bool in = step && bl < kb1 && bl * 128 + 32 * h < K;
+                    o = in ? 64 * h + bl * BB : OOR;
+                }
 #pragma unroll
-                for (int h = 0; h < WL; ++h) wv[u][t][h] = in ? ld_nt16(wp[t] + k + 8 * h) : v4i{0, 0, 0, 0};
-            xv[u][0] = (in && xm) ? ld16(xp + k) : v4i{0, 0, 0, 0};
-            xv[u][1] = (in && xm) ? ld16(xp + k + 8) : v4i{0, 0, 0, 0};
+                for (int t = 0; t < NT; ++t) wv[u][t][h] = buf_ld16_nt(wr[t], woff + o);
+            }
+            // activations: load p reads bytes 64 p + 16 g of the row's block (64 contiguous bytes per row); bf16
+            // weights consume load p as MFMA p's operand, int8 weights after the transpose below
+            const int bx = b + cpart * P;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const bool in = step && bx < kb1 && bx * 128 + 32 * p < K;
+                xv[u][p] = buf_ld16(xr, xoff + (in ? bx * 256 + 64 * p : OOR));
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the stage is in flight before the first wait
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (s0 + 64 * u < ke) {
+        for (int u = 0; u < KB; ++u) {
+            if constexpr (I8) {
+                // lane (i, g) register p holds 16-byte chunk 4 p + g of the row's block; MFMA m needs chunk 4 g + m
+                // (k = 32 g + 8 m). A 4 x 4 transpose over (register, 16-lane row): swap the upper 32 lanes of
+                // registers 0, 1 with the lower 32 lanes of 2, 3, then the odd rows of 0, 2 with the even rows of 1, 3.
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    v8bf b0, b1;
-                    if (sizeof(WT) == 1) {
-                        b0 = i8x8_to_bf16(wv[u][t][0][0], wv[u][t][0][1]);
-                        b1 = i8x8_to_bf16(wv[u][t][0][2], wv[u][t][0][3]);
-                    } else {
-                        b0 = as_bf16x8(wv[u][t][0]);
-                        b1 = as_bf16x8(wv[u][t][WL - 1]);
+                for (int d = 0; d < 4; ++d) {
+                    const auto s02 = __builtin_amdgcn_permlane32_swap(xv[u][0][d], xv[u][2][d], false, false);
+                    const auto s13 = __builtin_amdgcn_permlane32_swap(xv[u][1][d], xv[u][3][d], false, false);
+                    const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+                    const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+                    xv[u][0][d] = s01[0];
+                    xv[u][1][d] = s01[1];
+                    xv[u][2][d] = s23[0];
+                    xv[u][3][d] = s23[1];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                v4i q[2];  // int8: lane (c, g)'s bytes 32 g .. 32 g + 15 and 32 g + 16 .. 32 g + 31 of its column
+                if constexpr (I8) {
+                    // lanes c < 8 hold their column's chunk 2 g from load 0, lanes c >= 8 chunk 2 g + 1 from load 1;
+                    // the other chunk sits in lane l ^ 8 of the other load (DPP row_ror:8 swaps the row halves)
+                    const bool lowc = (lane & 8) == 0;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const int a0 = wv[u][t][0][d], a1 = wv[u][t][1][d];
+                        const int recv = __builtin_amdgcn_update_dpp(0, lowc ? a1 : a0, 0x128, 0xf, 0xf, false);
+                        q[0][d] = lowc ? a0 : recv;
+                        q[1][d] = lowc ? recv : a1;
                     }
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[u][0]), b0, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[u][1]), b1, acc[t], 0, 0, 0);
+                }
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    v8bf wb;
+                    if constexpr (I8)
+                        wb = i8x8_to_bf16(q[m >> 1][2 * (m & 1)], q[m >> 1][2 * (m & 1) + 1]);
+                    else
+                        wb = as_bf16x8(wv[u][t][m]);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[u][m]), wb, acc[t], 0, 0, 0);
                 }
             }
         }
     }
 
-    if constexpr (NWK > 1) {
-        __shared__ v4f red[NWK][64];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t > 0) __syncthreads();  // wavefront 0 has read the previous tile
-            red[wave][lane] = acc[t];
-            __syncthreads();
-            if (wave == 0) {
-                v4f s = red[0][lane];
-#pragma unroll
-                for (int w = 1; w < NWK; ++w) s += red[w][lane];
-                acc[t] = s;
-            }
+    auto store = [&](int i, float a, float u) {
+        const Coord e = coord(i);
+        const int n = nbase + TR * e.t + e.r;
+        if (e.t >= RT || n >= N || e.b >= B) return;
+        const float av = scale ? a * sg[i] : a;
+        uint16_t *yp = y + (size_t)e.b * N + n;
+        if (EPI == EPI_NONE) {
+            *yp = (uint16_t)f2bf(av);
+        } else if (EPI == EPI_RESIDUAL) {
+            *yp = (uint16_t)f2bf(bf2f(hr[i]) + rbf(av));
+        } else {
+            const float gv = rbf(av), uv = rbf(scale ? u * su[i] : u);
+            *yp = (uint16_t)f2bf(rbf(silu_f32(gv)) * uv);
         }
-        if (wave != 0) return;
-    }
+    };
+    if constexpr (VIA_LDS) {
+        // wavefront w's tile t: D[i][c] at 4 (c + 16 (i / 4)) + i % 4 (lane c + 16 (i / 4), element i % 4)
+        __shared__ __attribute__((aligned(16))) float red[NWK][NT][256];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int n = nbase + 16 * t + col;
-        if (n >= N) continue;
+        for (int t = 0; t < NT; ++t) *reinterpret_cast<v4f *>(&red[wave][t][4 * lane]) = acc[t];
+        __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * kq + i;
-            if (m >= B) continue;
-            const float a = acc[t][i];
-            if (EPI == EPI_NONE) {
-                y[(size_t)m * N + n] = (uint16_t)f2bf(apply_scale(a, scale, n));
-            } else if (EPI == EPI_RESIDUAL) {
-                uint16_t *h = y + (size_t)m * N + n;
-                *h = (uint16_t)f2bf(bf2f(*h) + rbf(apply_scale(a, scale, n)));
-            } else {
-                const float g = rbf(apply_scale(a, scale, n)), u = rbf(apply_scale(acc[RT + t][i], scale, S + n));
-                y[(size_t)m * N + n] = (uint16_t)f2bf(rbf(silu_f32(g)) * u);
-            }
+        for (int i = 0; i < EL; ++i) {
+            const Coord e = coord(i);
+            if (e.t >= RT || nbase + TR * e.t + e.r >= N || e.b >= B) continue;
+            float a = 0.f, u = 0.f;  // summed over wavefronts, then parts, in that fixed order
+#pragma unroll
+            for (int w = 0; w < NWK; ++w)
+#pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    const int ii = TR * s + e.b, cc = TR * s + e.r;
+                    const int at = 4 * (cc + 16 * (ii >> 2)) + (ii & 3);
+                    const float va = red[w][e.t][at], vu = EPI == EPI_SWIGLU ? red[w][NT - RT + e.t][at] : 0.f;
+                    a = (w == 0 && s == 0) ? va : a + va;
+                    u = (w == 0 && s == 0) ? vu : u + vu;
+                }
+            store(i, a, u);
         }
+    } else {
+#pragma unroll
+        for (int i = 0; i < EL; ++i) store(i, acc[i >> 2][i & 3], acc[NT - RT + (i >> 2)][i & 3]);
     }
 }
 
@@ -407,41 +519,53 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 #undef LFM2Q_B1
 }
 
-// K split over NWK wavefronts, from K only (a plain and a fused call of the same weights then split alike, which
-// keeps the fused epilogues bit-identical): 64-k steps per wavefront = U = 4 or 8, so one stage of loads holds all of
-// a wavefront's work. Other K: the largest NWK <= 8 that divides the steps with at least 4 per wavefront, U = 4.
-// RT (16-row tiles per wavefront): 4 for outputs of 32768+ rows, 2 from 8192 (or a SwiGLU pair from 4096 outputs),
-// else 1 -- more tiles share each activation load, fewer workgroups remain for narrow outputs.
+// Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
+// [2 S, K] matrix) then split K alike, which keeps the fused epilogues bit-identical:
+//   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows (256+ workgroups instead of 128);
+//   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2;
+//   NWK (at most 16) from the 128-k blocks per wavefront: 2 when RT = 2, 4 when KS = RT = 1, 8 when KS = 2
+//   (at least 4 wavefronts). Measured on MI355X over the LFM2 decode shapes at batches 4, 8 and 16.
+// LFM2Q_GEMV_MFMA = "KS,RT,NWK" overrides the shape (read on every call; the last bits of the sums change with it).
+template <typename WT, int EPI, int KS, int RT>
+void launch_mfma_shape(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int N, int K, int S,
+                       int nwk, hipStream_t st) {
+    const dim3 grid((N + (16 / KS) * RT - 1) / ((16 / KS) * RT));
+#define LFM2Q_MF(NWK_) \
+    gemv_mfma_kernel<WT, KS, RT, NWK_, EPI><<<grid, 64 * NWK_, 0, st>>>(W, scale, x, y, B, N, K, S)
+    switch (nwk) {
+        case 16: LFM2Q_MF(16); break;
+        case 8: LFM2Q_MF(8); break;
+        case 4: LFM2Q_MF(4); break;
+        case 2: LFM2Q_MF(2); break;
+        default: LFM2Q_MF(1); break;
+    }
+#undef LFM2Q_MF
+}
+
 template <typename WT, int EPI>
 void launch_mfma(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int N, int K, int S,
                  hipStream_t st) {
-    const int wide = EPI == EPI_SWIGLU ? 2 * N : N;
-    const int rt = (wide >= 32768 && EPI != EPI_SWIGLU) ? 4 : (wide >= 8192 ? 2 : 1);
-    const int steps = K / 64;
-    auto grid = [&](int RT) { return dim3((N + 16 * RT - 1) / (16 * RT)); };
-    if (steps == 128) {  // K = 8192: 16 wavefronts x 8 steps
-        gemv_mfma_kernel<WT, 1, 16, 8, EPI><<<grid(1), 1024, 0, st>>>(W, scale, x, y, B, N, K, S);
-    } else if (steps == 32) {  // K = 2048: 8 wavefronts x 4 steps
-        if (rt == 4)
-            gemv_mfma_kernel<WT, 4, 8, 4, EPI><<<grid(4), 512, 0, st>>>(W, scale, x, y, B, N, K, S);
-        else if (rt == 2)
-            gemv_mfma_kernel<WT, 2, 8, 4, EPI><<<grid(2), 512, 0, st>>>(W, scale, x, y, B, N, K, S);
-        else
-            gemv_mfma_kernel<WT, 1, 8, 4, EPI><<<grid(1), 512, 0, st>>>(W, scale, x, y, B, N, K, S);
-    } else {
-        int nwk = 1;
-        for (int c = 8; c > 1; c >>= 1)
-            if (steps % c == 0 && steps / c >= 4) {
-                nwk = c;
-                break;
-            }
-        switch (nwk) {
-            case 8: gemv_mfma_kernel<WT, 1, 8, 4, EPI><<<grid(1), 512, 0, st>>>(W, scale, x, y, B, N, K, S); break;
-            case 4: gemv_mfma_kernel<WT, 1, 4, 4, EPI><<<grid(1), 256, 0, st>>>(W, scale, x, y, B, N, K, S); break;
-            case 2: gemv_mfma_kernel<WT, 1, 2, 4, EPI><<<grid(1), 128, 0, st>>>(W, scale, x, y, B, N, K, S); break;
-            default: gemv_mfma_kernel<WT, 1, 1, 4, EPI><<<grid(1), 64, 0, st>>>(W, scale, x, y, B, N, K, S); break;
+    const long wrows = EPI == EPI_SWIGLU ? 2L * S : N;
+    const int nblk = (K + 127) / 128;
+    int ks = (B <= 8 && wrows <= 2048) ? 2 : 1;
+    int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
+    const int bpw = ks == 2 ? 8 : rt == 2 ? 2 : 4;  // target blocks per wavefront
+    int nwk = 1;
+    while (nwk < 16 && (nblk >= bpw * 2 * nwk || (ks == 2 && nwk < 4))) nwk *= 2;
+    int fk = 0, fr = 0, fn = 0;
+    if (const char *e = getenv("LFM2Q_GEMV_MFMA"))
+        if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
+            (fr == 1 || fr == 2) && (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
+            ks = fk;
+            rt = fr;
+            nwk = fn;
         }
-    }
+    if (ks == 2)
+        launch_mfma_shape<WT, EPI, 2, 1>(W, scale, x, y, B, N, K, S, nwk, st);
+    else if (rt == 2)
+        launch_mfma_shape<WT, EPI, 1, 2>(W, scale, x, y, B, N, K, S, nwk, st);
+    else
+        launch_mfma_shape<WT, EPI, 1, 1>(W, scale, x, y, B, N, K, S, nwk, st);
 }
 
 // y: [B, Nout] (Nout = S for SwiGLU). Batches above 16 run as consecutive chunks of at most 16 rows.
@@ -453,6 +577,7 @@ int gemv_run(const char *name, const WT *W, const float *scale, const uint16_t *
     LFM2Q_REQUIRE(B >= 1 && Nout >= 1 && K >= 64, LFM2Q_ERR_SHAPE, "%s: x [B, K], y [B, N] (B=%d N=%d K=%d)", name,
                   B, Nout, K);
     LFM2Q_REQUIRE(K % 64 == 0, LFM2Q_ERR_SHAPE, "%s: K must be a multiple of 64 (K=%d)", name, K);
+    LFM2Q_REQUIRE(K <= (1 << 24), LFM2Q_ERR_SHAPE, "%s: K above 16777216 (K=%d)", name, K);
     LFM2Q_REQUIRE(aligned16(W) && aligned16(x), LFM2Q_ERR_ALIGN, "%s: W and x must be 16-byte aligned", name);
     const int S = Nout;  // SwiGLU: w3 rows start at S
     for (int b0 = 0; b0 < B; b0 += 16) {

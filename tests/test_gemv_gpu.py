@@ -89,14 +89,41 @@ def _gen(seed, B, N, K):
     return W, scale, x
 
 
-@pytest.mark.parametrize("B", [1, 2, 4, 16, 17])
-@pytest.mark.parametrize("N,K", [(3072, 2048), (2048, 8192), (200, 1152)])
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 17])
+@pytest.mark.parametrize("N,K", [(3072, 2048), (2048, 8192), (200, 1152), (96, 576), (40, 64)])
 def test_gemv_w8_vs_oracle(E, B, N, K):
     W, scale, x = _gen(100 + B, B, N, K)
     y = torch.empty(B, N, device="cuda", dtype=torch.bfloat16)
     E.gemv(W.cuda(), scale.cuda(), x.cuda(), y)
     ref = oracle.gemv(W.numpy(), scale.numpy(), x.view(torch.int16).numpy().view(np.uint16))
     assert_close_bf16(host_bits(y), ref, what=f"gemv int8 B={B} [{N}x{K}]")
+
+
+@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,8", "1,2,1", "2,1,1", "2,1,2", "2,1,16"])
+@pytest.mark.parametrize("wt", ["int8", "bf16"])
+def test_gemv_mfma_launch_shapes(E, monkeypatch, shape, wt):
+    """Every batch-2..16 launch shape (k-parts KS, row tiles RT, wavefronts NWK, forced through LFM2Q_GEMV_MFMA)
+    against the oracle, with a trailing half block (K = 1088) and N not a multiple of the tile rows."""
+    monkeypatch.setenv("LFM2Q_GEMV_MFMA", shape)
+    N, K = 300, 1088
+    g = torch.Generator().manual_seed(len(shape))
+    for B in (3, 8) if shape.startswith("2") else (3, 13):
+        if wt == "int8":
+            W, scale, x = _gen(B, B, N, K)
+            ref = oracle.gemv(W.numpy(), scale.numpy(), host_bits(x))
+            Wd, sd = W.cuda(), scale.cuda()
+        else:
+            W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+            x = torch.randn(B, K, generator=g).to(torch.bfloat16)
+            ref = oracle.gemv(host_bits(W), None, host_bits(x))
+            Wd, sd = W.cuda(), None
+        y = torch.empty(B, N, device="cuda", dtype=torch.bfloat16)
+        E.gemv(Wd, sd, x.cuda(), y)
+        assert_close_bf16(host_bits(y), ref, what=f"gemv {wt} shape {shape} B={B}")
+        h0 = (torch.randn(B, N, generator=g) * 4).to(torch.bfloat16).cuda()
+        h = h0.clone()
+        E.gemv_residual(Wd, sd, x.cuda(), h)
+        assert torch.equal(h, (h0.float() + y.float()).to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("rows", [1, 2, 4])
@@ -130,18 +157,19 @@ def test_gemv_w8_decode_shapes(E, N, K, B):
 
 
 @pytest.mark.parametrize("B", [1, 3, 16])
-def test_gemv_bf16_vs_oracle(E, B):
+@pytest.mark.parametrize("N,K", [(1040, 1024), (72, 576)])
+def test_gemv_bf16_vs_oracle(E, B, N, K):
     g = torch.Generator().manual_seed(B)
-    W = (torch.randn(1040, 1024, generator=g) * 0.02).to(torch.bfloat16)
-    x = torch.randn(B, 1024, generator=g).to(torch.bfloat16)
-    y = torch.empty(B, 1040, device="cuda", dtype=torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(B, K, generator=g).to(torch.bfloat16)
+    y = torch.empty(B, N, device="cuda", dtype=torch.bfloat16)
     E.gemv(W.cuda(), None, x.cuda(), y)
     ref = oracle.gemv(W.view(torch.int16).numpy().view(np.uint16), None, x.view(torch.int16).numpy().view(np.uint16))
     assert_close_bf16(host_bits(y), ref, what=f"gemv bf16 B={B}")
 
 
 # ------------------------------------------------------------------------------------------------ fused epilogues
-@pytest.mark.parametrize("B", [1, 2, 4, 16, 19])
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 19])
 @pytest.mark.parametrize("wt", ["int8", "bf16"])
 def test_swiglu_bit_identical_to_gemv_then_silu_mul(E, B, wt):
     """gemv_epi(0) == gemv + silu_mul bit for bit (tests/test_kernels.py:153-186), at the w1|w3 shape."""
@@ -163,7 +191,7 @@ def test_swiglu_bit_identical_to_gemv_then_silu_mul(E, B, wt):
     assert torch.equal(out, ref), (out.float() - ref.float()).abs().max()
 
 
-@pytest.mark.parametrize("B", [1, 4, 16])
+@pytest.mark.parametrize("B", [1, 4, 8, 16])
 def test_residual_bit_identical_to_gemv_then_add(E, B):
     N, K = 2048, 8192
     g = torch.Generator(device="cuda").manual_seed(B)
