@@ -7,7 +7,8 @@
 //   fmt 1, GPTQ-style:      Wq int32 [N, K/8], scales fp16 [N, K/group], zero points int32 [N, ceil(G/8)]
 //          (nibble j of word w = zero point of group 8 w + j).
 //
-// Dequantization costs two bit operations per weight pair: ((word >> 4p) & 0x000F000F) | 0x43004300 is the bf16 pair
+// Dequantization costs one or two bit operations per weight pair: ((word >> 4p) & 0x000F000F) | 0x43004300 (a shift
+// for p > 0 and one v_and_or_b32) is the bf16 pair
 // (128 + q[p], 128 + q[p + 4]) exactly (bf16 holds every integer in [128, 256)). A chunk's sum is then
 //     sum_k s (q_k - z) x_k = s (sum_k (128 + q_k) x_k - (128 + z) sum_k x_k),
 // with the first sum from v_dot2_f32_bf16 (batch 1) or bf16 MFMAs (batch 2..16) and the activation sums computed
@@ -20,14 +21,26 @@
 #include "status.hpp"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 namespace lfm2q {
 namespace {
 
 enum Epi { EPI_NONE = 0, EPI_SWIGLU = 1, EPI_RESIDUAL = 2 };
 
-// (128 + q[p], 128 + q[p + 4]) as a bf16 pair, p = 0..3, from one 8-weight word
-__device__ __forceinline__ uint32_t w4pair(uint32_t w, int p) { return ((w >> (4 * p)) & 0x000F000Fu) | 0x43004300u; }
+// The nibble masks as opaque register values: with the constants hidden from the optimizer, (a & m) | o selects a
+// single v_and_or_b32 (a VOP3 instruction takes no literal operand on gfx9, so with visible constants the compiler
+// emits a literal AND and a literal OR instead).
+struct NibbleMasks {
+    uint32_t m, o;  // 0x000F000F (SGPR), 0x43004300 (VGPR)
+    __device__ NibbleMasks() {
+        asm("s_mov_b32 %0, 0x000F000F" : "=s"(m));
+        asm("v_mov_b32 %0, 0x43004300" : "=v"(o));
+    }
+    // (128 + q[p], 128 + q[p + 4]) as a bf16 pair, p = 0..3, from one 8-weight word
+    __device__ uint32_t pair(uint32_t w, int p) const { return ((p ? w >> (4 * p) : w) & m) | o; }
+};
 
 // (x[p], x[p + 4]) from 8 bf16 activations x0..x7 held as 4 dwords (x0 | x1 << 16, ...)
 __device__ __forceinline__ uint32_t xpair(const v4i &d, int p) {
@@ -77,6 +90,7 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
                                                          const int32_t *__restrict__ Z, const uint16_t *__restrict__ x,
                                                          uint16_t *__restrict__ y, int N, int K, int group, int Sr) {
     using F = W4Fmt<FMT>;
+    const NibbleMasks nm;
     constexpr int NROW = EPI == EPI_SWIGLU ? 2 : 1;
     constexpr int NB = CPL * NROW <= 2 ? 4 : 2;
     const int lane = threadIdx.x & 63;
@@ -143,7 +157,7 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int p = 0; p < 4; ++p)
-                        d = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w4pair((uint32_t)it.w[u][i][j], p)),
+                        d = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nm.pair((uint32_t)it.w[u][i][j], p)),
                                                             as_bf16x2(xp[u][4 * j + p]), d, false);
                 acc[i] += it.s[u][i] * (d - (float)(128 + it.z[u][i]) * xs[u]);
             }
@@ -168,16 +182,24 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
 }
 
 // ------------------------------------------------------------------------------------------------ batch 2..16
-// WG = NWK wavefronts and 16 RT output rows (EPI_SWIGLU: plus the 16 RT matching w3 rows, NT = 2 RT tiles). K goes
-// in steps of 128 (one group when group = 128; group % 128 == 0 keeps every step inside one group); wavefront w
-// takes steps [w SPW, (w + 1) SPW), SPW = K / 128 / NWK, in stages of up to 4 steps whose loads are all issued
-// first. In a step, lane (col = l % 16, kq = l / 16) loads the 32 weights k0 + 32 kq .. + 31 of row col of every
-// tile (16 bytes) and the activations of batch row col at the same k. MFMA j (j = 0..3) takes word j of both:
-// k-slot s of lane group kq is k = k0 + 32 kq + 8 j + perm(s), the same map for both operands.
-// Activations are the A operand (batch x k), weights B (k x rows): D[batch][row] sits in lane row + 16 (batch / 4),
-// element batch % 4, so a lane's scale and zero point are those of its single row col. A fifth MFMA per j with B = 1
-// gives the step's activation sums in the same layout.
-template <int FMT, int RT, int NWK, int EPI>
+// A workgroup owns RT tiles of TR = 16 / KS output rows (EPI_SWIGLU: plus the matching w3 rows, NT = 2 RT tiles);
+// its NWK wavefronts split K into contiguous runs of 256-k blocks (one 128-byte line per row), KB blocks per stage,
+// every load of a stage issued before its MFMAs. v_mfma_f32_16x16x32_bf16 computes D[i][c] += sum_k A[i][k] B[k][c];
+// column c of B is weight row c % TR over part c / TR of the wavefront's K run (KS parts of P blocks), row i of A is
+// batch row i % TR over part i / TR, so the KS diagonal blocks D[TR s + b][TR s + r] are partial sums of output
+// (b, r) and the others are discarded (KS = 2: 8-row tiles, batches up to 8, twice the workgroups).
+// Weights: lane (c, g) (l = c + 16 g) needs 16-byte chunks g and g + 4 (k = 32 g and 128 + 32 g) of its column's
+// block. Load q reads 8 whole lines -- rows c % 8 (+ 8 q for KS = 1) of part q (KS = 2) -- lane (c, g) taking chunk
+// g + 4 ((c / 8) ^ q): each lane gets its chunk g from one load and its chunk g + 4 sits in lane l ^ 8 of the other
+// (one DPP row rotation by 8 and three selects per dword). MFMA (h, j), h = chunk half, j = word: lane group g
+// slot s holds k = 128 h + 32 g + 8 j + perm(s) with perm pairing nibbles (p, p + 4) -- the 32 k of one MFMA lie in
+// one 128-k group, so the group's scale and zero point apply to its result: per tile and half,
+//     acc += s (sum_j D_j - (128 + z) sum_j X_j),   X_j = the same MFMA against a matrix of ones.
+// Activations: load p reads bytes 64 p + 16 g of the row's 512-byte block (64 contiguous bytes per row); two 4 x 4
+// permlane transposes give lane (i, g) x[i][128 h + 32 g + 8 j .. + 7] in register 4 h + j.
+// Every load goes through a buffer resource (rows past N, batch rows past B and k past K read zeros). The partial
+// tiles (NWK wavefronts x KS parts) are summed in LDS in a fixed order, every thread taking some of the outputs.
+template <int FMT, int KS, int RT, int NWK, int EPI>
 __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *__restrict__ Wq,
                                                                 const void *__restrict__ S,
                                                                 const int32_t *__restrict__ Z,
@@ -185,101 +207,175 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
                                                                 uint16_t *__restrict__ y, int B, int N, int K,
                                                                 int group, int Sr) {
     using F = W4Fmt<FMT>;
+    const NibbleMasks nm;
+    constexpr int TR = 16 / KS;
     constexpr int NT = (EPI == EPI_SWIGLU ? 2 : 1) * RT;
-    constexpr int U = 4;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int col = lane & 15, kq = lane >> 4;
-    const int nbase = blockIdx.x * 16 * RT;
-    const int G = K / group, steps = K / 128, spw = steps / NWK;
+    constexpr int KB = NT >= 4 ? 1 : 2;     // blocks per stage (a block holds 8 activation registers per lane)
+    constexpr uint32_t OOR = 0x40000000u;   // an offset past every range below: the load returns zeros
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int nbase = blockIdx.x * TR * RT;
+    const int G = K / group;
     const uint32_t rowb = (uint32_t)K / 2;
-    int wrow[NT];
+    rsrc_t wr[NT];
+    int srow[NT];  // the weight row of this lane's column, for its scales and zero points
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-        wrow[t] = (EPI == EPI_SWIGLU && t >= RT ? Sr : 0) + min(nbase + 16 * (t % RT) + col, N - 1);
-    const bool xm = col < B;
-    const uint16_t *xrow = x + (size_t)(xm ? col : 0) * K;
+    for (int t = 0; t < NT; ++t) {
+        const int r0 = nbase + TR * (t % RT), off = EPI == EPI_SWIGLU && t >= RT ? Sr : 0;
+        const int rows = __builtin_amdgcn_readfirstlane(max(0, min(TR, N - r0)));  // keep the resource scalar
+        wr[t] = make_rsrc(Wq + (size_t)(off + min(r0, N - 1)) * rowb, (uint32_t)rows * rowb);
+        srow[t] = off + min(r0 + c % TR, N - 1);
+    }
+    const rsrc_t xr = make_rsrc(x, (uint32_t)B * K * 2u);
+    const int cpart = c / TR;  // part of this lane's B column and A row
+    const uint32_t xoff = (uint32_t)(c % TR) * K * 2u + 16 * g;
     const v8bf ones = __builtin_bit_cast(v8bf, v4u{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+
+    const int nblk = (K + 255) / 256;
+    const int per = (nblk + NWK - 1) / NWK;
+    const int kb0 = wave * per, kb1 = min(nblk, kb0 + per);
+    const int P = (per + KS - 1) / KS;
+
+    // Output elements (tile t, batch row b, row r -> y[b][nbase + TR t + r]): thread threadIdx.x + 64 NWK i takes
+    // element TR TR t + TR b + r of the summed tiles.
+    constexpr int TE = TR * TR;
+    constexpr int EL = (RT * TE + 64 * NWK - 1) / (64 * NWK);
+    struct Coord {
+        int t, b, r;
+    };
+    auto coord = [&](int i) -> Coord {
+        const int idx = (int)threadIdx.x + i * 64 * NWK;
+        return {idx / TE, (idx % TE) / TR, idx % TR};
+    };
+    // the residual values are read before the weight stream starts (their latency is not paid after the last MFMA)
+    uint32_t hr[EL];
+#pragma unroll
+    for (int i = 0; i < EL; ++i) {
+        const Coord e = coord(i);
+        const int n = min(nbase + TR * e.t + e.r, N - 1);
+        hr[i] = (EPI == EPI_RESIDUAL && e.t < RT && e.b < B) ? y[(size_t)e.b * N + n] : 0u;
+    }
 
     v4f acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    for (int s0 = wave * spw; s0 < (wave + 1) * spw; s0 += U) {
-        v4i wv[U][NT], xv[U][4];
-        float sc[U][NT];
-        int zp[U][NT];
+    for (int b0 = kb0; b0 < kb0 + P; b0 += KB) {
+        v4i wv[KB][NT][2], xv[KB][8];
+        float sc[KB][NT][2];
+        int zp[KB][NT][2];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int st = s0 + u;
-            const bool in = st < (wave + 1) * spw;
-            const int k = 128 * st + 32 * kq;
-            const int g = min(128 * st / group, G - 1);
+        for (int u = 0; u < KB; ++u) {
+            const int b = b0 + u;  // block of part 0; part s reads block b + s P
+            const bool step = b < kb0 + P;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                wv[u][t] = in ? ld_nt16(Wq + (size_t)wrow[t] * rowb + k / 2) : v4i{0, 0, 0, 0};
-                sc[u][t] = F::scale(S, Z, wrow[t], g, G);
-                zp[u][t] = F::zero(Z, wrow[t], g, G);
+            for (int q = 0; q < 2; ++q) {
+                const int bq = b + (KS == 2 ? q * P : 0);
+                const int ch = g + 4 * (((c >> 3) ^ q) & 1);
+                const bool in = step && bq < kb1 && bq * 256 + 32 * ch < K;
+                const uint32_t o = ((c & 7) + (KS == 1 ? 8 * q : 0)) * rowb + 16 * ch + bq * 128u;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) wv[u][t][q] = buf_ld16_nt(wr[t], in ? o : OOR);
             }
+            // the lane's column reads block bw; its two 128-k halves lie in groups gi(0), gi(1)
+            const int bw = min(b + cpart * P, nblk - 1);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xv[u][j] = (in && xm) ? ld16(xrow + k + 8 * j) : v4i{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (s0 + u < (wave + 1) * spw) {
-                v4f d[NT], dx = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int t = 0; t < NT; ++t) d[t] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const v8bf a = __builtin_bit_cast(
-                        v8bf, v4u{xpair(xv[u][j], 0), xpair(xv[u][j], 1), xpair(xv[u][j], 2), xpair(xv[u][j], 3)});
-                    dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, dx, 0, 0, 0);
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        const uint32_t w = (uint32_t)wv[u][t][j];
-                        const v8bf b = __builtin_bit_cast(v8bf, v4u{w4pair(w, 0), w4pair(w, 1), w4pair(w, 2), w4pair(w, 3)});
-                        d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, d[t], 0, 0, 0);
-                    }
-                }
+            for (int h = 0; h < 2; ++h) {
+                const int gi = min((bw * 256 + 128 * h) / group, G - 1);
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const float zc = (float)(128 + zp[u][t]);
+                    sc[u][t][h] = F::scale(S, Z, srow[t], gi, G);
+                    zp[u][t][h] = F::zero(Z, srow[t], gi, G);
+                }
+            }
+            const int bx = b + cpart * P;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[t][e] += sc[u][t] * (d[t][e] - zc * dx[e]);
+            for (int p = 0; p < 8; ++p) {
+                const bool in = step && bx < kb1 && bx * 256 + 32 * p < K;
+                xv[u][p] = buf_ld16(xr, xoff + (in ? bx * 512 + 64 * p : OOR));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the stage is in flight before the first wait
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            // lane (i, g) register p holds 16-byte chunk 4 p + g; MFMA (h, j) needs chunk 16 h + 4 g + j, held by
+            // lane j in register 4 h + g: two 4 x 4 transposes over (register, 16-lane row)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    v4i &r0 = xv[u][4 * h], &r1 = xv[u][4 * h + 1], &r2 = xv[u][4 * h + 2], &r3 = xv[u][4 * h + 3];
+                    const auto s02 = __builtin_amdgcn_permlane32_swap(r0[d], r2[d], false, false);
+                    const auto s13 = __builtin_amdgcn_permlane32_swap(r1[d], r3[d], false, false);
+                    const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+                    const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+                    r0[d] = s01[0];
+                    r1[d] = s01[1];
+                    r2[d] = s23[0];
+                    r3[d] = s23[1];
+                }
+            v8bf a[8];
+            v4f dx[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                dx[h] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const v4i &xr4 = xv[u][4 * h + j];
+                    a[4 * h + j] = __builtin_bit_cast(v8bf, v4u{xpair(xr4, 0), xpair(xr4, 1), xpair(xr4, 2), xpair(xr4, 3)});
+                    dx[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[4 * h + j], ones, dx[h], 0, 0, 0);
+                }
+            }
+            const bool lowc = (lane & 8) == 0;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                v4i q2[2];  // chunk g and chunk g + 4 of this lane's column
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) {
+                    const int a0 = wv[u][t][0][dd], a1 = wv[u][t][1][dd];
+                    const int recv = __builtin_amdgcn_update_dpp(0, lowc ? a1 : a0, 0x128, 0xf, 0xf, false);
+                    q2[0][dd] = lowc ? a0 : a1;
+                    q2[1][dd] = recv;
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    v4f d = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t w = (uint32_t)q2[h][j];
+                        const v8bf bw4 = __builtin_bit_cast(v8bf, v4u{nm.pair(w, 0), nm.pair(w, 1), nm.pair(w, 2), nm.pair(w, 3)});
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[4 * h + j], bw4, d, 0, 0, 0);
+                    }
+                    const float zc = (float)(128 + zp[u][t][h]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[t][e] += sc[u][t][h] * (d[e] - zc * dx[h][e]);
                 }
             }
         }
     }
 
-    if constexpr (NWK > 1) {
-        __shared__ v4f red[NWK][64];
+    // wavefront w's tile t: D[i][c] at 4 (c + 16 (i / 4)) + i % 4 (lane c + 16 (i / 4), element i % 4)
+    __shared__ __attribute__((aligned(16))) float red[NWK][NT][256];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t > 0) __syncthreads();  // wavefront 0 has read the previous tile
-            red[wave][lane] = acc[t];
-            __syncthreads();
-            if (wave == 0) {
-                v4f s = red[0][lane];
+    for (int t = 0; t < NT; ++t) *reinterpret_cast<v4f *>(&red[wave][t][4 * lane]) = acc[t];
+    __syncthreads();
 #pragma unroll
-                for (int w = 1; w < NWK; ++w) s += red[w][lane];
-                acc[t] = s;
+    for (int i = 0; i < EL; ++i) {
+        const Coord e = coord(i);
+        const int n = nbase + TR * e.t + e.r;
+        if (e.t >= RT || n >= N || e.b >= B) continue;
+        float av = 0.f, uv = 0.f;  // summed over wavefronts, then parts, in that fixed order
+#pragma unroll
+        for (int w = 0; w < NWK; ++w)
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const int ii = TR * s + e.b, cc = TR * s + e.r;
+                const int at = 4 * (cc + 16 * (ii >> 2)) + (ii & 3);
+                const float va = red[w][e.t][at], vu = EPI == EPI_SWIGLU ? red[w][NT - RT + e.t][at] : 0.f;
+                av = (w == 0 && s == 0) ? va : av + va;
+                uv = (w == 0 && s == 0) ? vu : uv + vu;
             }
-        }
-        if (wave != 0) return;
-    }
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int n = nbase + 16 * t + col;
-        if (n >= N) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * kq + i;
-            if (m >= B) continue;
-            uint16_t *yo = y + (size_t)m * N + n;
-            const float v = epi_value(EPI, acc[t][i], EPI == EPI_SWIGLU ? acc[RT + t][i] : 0.f,
-                                      EPI == EPI_RESIDUAL ? *yo : 0u);
-            *yo = (uint16_t)f2bf(v);
-        }
+        y[(size_t)e.b * N + n] = (uint16_t)f2bf(epi_value(EPI, av, uv, hr[i]));
     }
 }
 
@@ -299,47 +395,51 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
         gemv_w4_b1_kernel<FMT, 4, EPI><<<grid, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
 }
 
-// NWK: the smallest of 1, 2, 4, 8 dividing the 128-k steps with (16-row weight tiles) x NWK >= 4096, else the largest
-// that divides: 2048+ wavefronts even when a SwiGLU workgroup holds two tiles (8 per CU, the streaming optimum). RT: 16-row tiles per workgroup, 4 for outputs of 32768+ rows
-// (not with SwiGLU, whose tile pairs double the registers), else 1.
+// Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
+// [2 S, K/8] matrix) then split K alike, which keeps the fused epilogues bit-identical:
+//   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows; RT = 2 for 6144+ weight rows unless
+//   KS = 2; NWK (at most 16) from the 256-k blocks per wavefront: 2 when RT = 2, 4 when KS = RT = 1, 8 when KS = 2
+//   (at least 4 wavefronts). LFM2Q_W4_MFMA = "KS,RT,NWK" overrides the shape (read on every call).
+template <int FMT, int EPI, int KS, int RT>
+void launch_w4_shape(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int B, int N,
+                     int K, int group, int nwk, hipStream_t st) {
+    const dim3 grid((N + (16 / KS) * RT - 1) / ((16 / KS) * RT));
+#define LFM2Q_W4M(NWK_) \
+    gemv_w4_mfma_kernel<FMT, KS, RT, NWK_, EPI><<<grid, 64 * NWK_, 0, st>>>(W, S, Z, x, y, B, N, K, group, N)
+    switch (nwk) {
+        case 16: LFM2Q_W4M(16); break;
+        case 8: LFM2Q_W4M(8); break;
+        case 4: LFM2Q_W4M(4); break;
+        case 2: LFM2Q_W4M(2); break;
+        default: LFM2Q_W4M(1); break;
+    }
+#undef LFM2Q_W4M
+}
+
 template <int FMT, int EPI>
 void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int B, int N,
                     int K, int group, hipStream_t st) {
-    const int steps = K / 128;
-    const int rt = (N >= 32768 && EPI != EPI_SWIGLU) ? 4 : 1;
-    const int wgs = (N + 16 * rt - 1) / (16 * rt);
-    // the split is chosen from K and the weight-row count alone, so a fused SwiGLU call (N outputs over 2N rows)
-    // splits K like the plain GEMV of the same 2N rows, and its results are bit-identical to that GEMV + silu_mul
-    const long tiles16 = ((EPI == EPI_SWIGLU ? 2L : 1L) * N + 15) / 16;
+    const long wrows = EPI == EPI_SWIGLU ? 2L * N : N;
+    const int nblk = (K + 255) / 256;
+    int ks = (B <= 8 && wrows <= 2048) ? 2 : 1;
+    int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
+    const int bpw = ks == 2 ? 8 : rt == 2 ? 2 : 4;  // target blocks per wavefront
     int nwk = 1;
-    for (int c = 1; c <= 8; c <<= 1)
-        if (steps % c == 0) {
-            nwk = c;
-            if (tiles16 * c >= 4096) break;
+    while (nwk < 16 && (nblk >= bpw * 2 * nwk || (ks == 2 && nwk < 4))) nwk *= 2;
+    int fk = 0, fr = 0, fn = 0;
+    if (const char *e = getenv("LFM2Q_W4_MFMA"))
+        if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
+            (fr == 1 || fr == 2) && (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
+            ks = fk;
+            rt = fr;
+            nwk = fn;
         }
-    const dim3 grid(wgs);
-#define LFM2Q_W4M(RT_, NWK_)                                                                                         \
-    gemv_w4_mfma_kernel<FMT, RT_, NWK_, EPI><<<grid, 64 * NWK_, 0, st>>>(W, S, Z, x, y, B, N, K, group, N)
-    if constexpr (EPI != EPI_SWIGLU) {
-        if (rt == 4) {
-            switch (nwk) {
-                case 8: LFM2Q_W4M(4, 8); break;
-                case 4: LFM2Q_W4M(4, 4); break;
-                case 2: LFM2Q_W4M(4, 2); break;
-                default: LFM2Q_W4M(4, 1); break;
-            }
-            return;
-        }
-    }
-    {
-        switch (nwk) {
-            case 8: LFM2Q_W4M(1, 8); break;
-            case 4: LFM2Q_W4M(1, 4); break;
-            case 2: LFM2Q_W4M(1, 2); break;
-            default: LFM2Q_W4M(1, 1); break;
-        }
-    }
-#undef LFM2Q_W4M
+    if (ks == 2)
+        launch_w4_shape<FMT, EPI, 2, 1>(W, S, Z, x, y, B, N, K, group, nwk, st);
+    else if (rt == 2)
+        launch_w4_shape<FMT, EPI, 1, 2>(W, S, Z, x, y, B, N, K, group, nwk, st);
+    else
+        launch_w4_shape<FMT, EPI, 1, 1>(W, S, Z, x, y, B, N, K, group, nwk, st);
 }
 
 template <int FMT, int EPI>
@@ -349,7 +449,8 @@ void w4_run(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x
         const int bs = std::min(16, B - b0);
         const uint16_t *xb = x + (size_t)b0 * K;
         uint16_t *yb = y + (size_t)b0 * N;
-        if (bs > 1 && group % 128 == 0) {
+        static const bool b1_mfma = env_int("LFM2Q_W4_B1_MFMA", 0) != 0;
+        if ((bs > 1 || b1_mfma) && group % 128 == 0) {
             launch_w4_mfma<FMT, EPI>(W, S, Z, xb, yb, bs, N, K, group, st);
         } else {
             for (int b = 0; b < bs; ++b)

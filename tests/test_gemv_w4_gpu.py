@@ -94,10 +94,30 @@ def test_gemv_w4z_fixture(E, name, epi):
 
 # ------------------------------------------------------------------------------------------------ vs oracle
 @pytest.mark.parametrize("B", [1, 2, 5, 8, 16, 20])
-@pytest.mark.parametrize("N,K,group", [(300, 2048, 128), (257, 8192, 128), (64, 1536, 128), (72, 96, 32)])
+@pytest.mark.parametrize("N,K,group", [(300, 2048, 128), (257, 8192, 128), (64, 1536, 128), (136, 1152, 128),
+                                       (72, 96, 32)])
 def test_gemv_w4_vs_oracle(E, B, N, K, group):
     Wp, S, x = gen_ref(N + K + B, B, N, K, group)
     assert_close_bf16(run_ref(E, Wp, S, x), oracle.gemv_w4(Wp, S, x), what=f"gemv_w4 B={B} [{N}x{K}] g{group}")
+
+
+@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,2", "1,2,16", "2,1,1", "2,1,4", "2,1,16"])
+def test_gemv_w4_mfma_launch_shapes(E, monkeypatch, shape):
+    """Every batch-2..16 launch shape of the matrix-core INT4 kernel (k-parts KS, row tiles RT, wavefronts NWK,
+    forced through LFM2Q_W4_MFMA) against the oracle, in both weight formats, with a trailing half block
+    (K = 1152) and N not a multiple of the tile rows; the residual epilogue bit-identical to the plain GEMV + add."""
+    monkeypatch.setenv("LFM2Q_W4_MFMA", shape)
+    N, K, group = 300, 1152, 128
+    for B in (3, 8) if shape.startswith("2") else (3, 13):
+        Wp, S, x = gen_ref(B + 7, B, N, K, group)
+        y = run_ref(E, Wp, S, x)
+        assert_close_bf16(y, oracle.gemv_w4(Wp, S, x), what=f"gemv_w4 shape {shape} B={B}")
+        h0 = oracle.f2bf(np.random.default_rng(B).standard_normal((B, N)).astype(np.float32) * 4)
+        ref_h = oracle.f2bf(oracle.bf2f(h0) + oracle.bf2f(y))
+        assert np.array_equal(run_ref(E, Wp, S, x, 2, h0), ref_h)
+        Wq, Sz, Z, xz = gen_zp(B + 9, B, N, K, group)
+        assert_close_bf16(run_zp(E, Wq, Sz, Z, xz), oracle.gemv_w4z(Wq, Sz, Z, xz, group),
+                          what=f"gemv_w4z shape {shape} B={B}")
 
 
 @pytest.mark.parametrize("B", [1, 3, 8, 17])
