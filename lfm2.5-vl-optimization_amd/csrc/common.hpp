@@ -60,6 +60,43 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
 }
 
+// Sums of V values (V = 1, 2, 4, 8) over the 64 lanes of a wavefront in one transposed reduction: lane bits 5, 4
+// and 3 are folded first -- while several values remain, each fold pairs two of them, so that half the lanes add
+// the partner's copy of one value and the other half of the other (permlane32 / permlane16 swaps, then a DPP row
+// rotation by 8) -- then bits 0, 1 and 2 by DPP within 8 lanes. Value v ends in lanes v 64 / V .. v 64 / V + 64 / V
+// - 1. The lane pairing is the same for every V and slot, so a value's sum does not depend on how many values
+// share the call (8 values cost about as much as 2 separate wave sums).
+constexpr int DPP_ROR8 = 0x128;  // lane i <- lane i ^ 8 within each 16 lanes (row rotation by 8)
+template <int V>
+__device__ __forceinline__ float fold_sum(const float (&v)[V]) {
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "fold_sum: V in {1, 2, 4, 8}");
+    constexpr int V1 = V >= 2 ? V / 2 : 1, V2 = V1 >= 2 ? V1 / 2 : 1;
+    float b[V1], c[V2];
+#pragma unroll
+    for (int i = 0; i < V1; ++i) {  // bit 5: lanes 0-31 keep value i, lanes 32-63 value i + V1
+        const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[V >= 2 ? i + V1 : i]),
+                                                        false, false);
+        b[i] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < V2; ++i) {  // bit 4: even 16-lane rows keep b[i], odd rows b[i + V2]
+        const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[i]), __float_as_uint(b[V1 >= 2 ? i + V2 : i]),
+                                                        false, false);
+        c[i] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    }
+    float d;  // bit 3
+    if constexpr (V2 >= 2) {
+        const bool hi = (threadIdx.x & 8) != 0;
+        d = (hi ? c[1] : c[0]) + dpp<DPP_ROR8>(hi ? c[0] : c[1]);
+    } else {
+        d = c[0] + dpp<DPP_ROR8>(c[0]);
+    }
+    d += dpp<DPP_XOR1>(d);
+    d += dpp<DPP_XOR2>(d);
+    d += dpp<DPP_HALF_MIRROR>(d);
+    return d;
+}
+
 // 16-byte streaming load that does not keep the line in the caches (weights are read exactly once per call).
 __device__ __forceinline__ v4i ld_nt16(const void *p) { return __builtin_nontemporal_load((const v4i *)p); }
 // 16-byte cached load (activations: small and shared by every wave).

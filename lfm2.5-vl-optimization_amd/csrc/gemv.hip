@@ -5,7 +5,7 @@
 //   gemv_b1_kernel    batch 1. One wavefront owns R output rows; lane l streams the 16-byte chunks l, l+64, ...
 //                     of each row with non-temporal loads (a wavefront load = 1 KiB contiguous of one row), all of
 //                     a lane's chunks are in flight before the first FMA. int8 -> fp32 is one SDWA convert per
-//                     weight; the row sum is a wave64 butterfly. No LDS.
+//                     weight; the row sums of a wavefront's rows are reduced together (fold_sum). No LDS.
 //   gemv_mfma_kernel  batch 2..16. A workgroup owns 16 (or 32) output rows; its NWK wavefronts split K into
 //                     128-k blocks. A wave's two loads per block and tile row cover 16 whole 128-byte lines; the
 //                     weights are converted exactly to bf16 in registers and feed v_mfma_f32_16x16x32_bf16 with the
@@ -71,10 +71,6 @@ struct PairDot<uint16_t> {
     }
 };
 
-__device__ __forceinline__ float apply_scale(float a, const float *__restrict__ scale, int n) {
-    return scale ? a * scale[n] : a;
-}
-
 // ------------------------------------------------------------------------------------------------ batch 1
 // Persistent batch-1 GEMV: about WPC wavefronts per CU, wavefront g handles output rows g, g + nw, g + 2 nw, ...
 // (nw = wavefronts in the grid). K = 64 PER CPL: lane l owns the 16-byte chunks l, l + 64, ..., of every row, and
@@ -107,39 +103,25 @@ __global__ __launch_bounds__(256) void gemv_b1p_kernel(const WT *__restrict__ W,
     const uint32_t rowb = (uint32_t)K * sizeof(WT);
     struct Item {
         v4i w[CPL][NROW];
-        uint32_t h;  // EPI_RESIDUAL: the residual value, read together with the row's weights
+        float s[NROW];  // the rows' scales and (EPI_RESIDUAL) residual value, read together with the weights
+        uint32_t h;
     };
     auto load = [&](Item &it, int row) {
+        const int rc = min(row, N - 1);
 #pragma unroll
         for (int i = 0; i < NROW; ++i) {
             // rows past the end get an empty range: their loads return zeros without a memory access
             const rsrc_t rr = make_rsrc(wbase + (size_t)(i ? S + row : row) * rowb, row < N ? rowb : 0u);
 #pragma unroll
             for (int u = 0; u < CPL; ++u) it.w[u][i] = buf_ld16_nt(rr, loff + u * 1024);
+            it.s[i] = scale ? scale[i ? S + rc : rc] : 1.f;
         }
-        if (EPI == EPI_RESIDUAL) it.h = y[min(row, N - 1)];
+        if (EPI == EPI_RESIDUAL) it.h = y[rc];
     };
-    auto finish = [&](const Item &it, int row) {
-        float acc[NROW];
-#pragma unroll
-        for (int i = 0; i < NROW; ++i) {
-            acc[i] = 0.f;
-#pragma unroll
-            for (int u = 0; u < CPL; ++u) acc[i] = D::dot(it.w[u][i], xr[u], acc[i]);
-            acc[i] = wave_sum(acc[i]);
-        }
-        float v;
-        if (EPI == EPI_NONE) {
-            v = apply_scale(acc[0], scale, row);
-        } else if (EPI == EPI_RESIDUAL) {
-            v = bf2f(it.h) + rbf(apply_scale(acc[0], scale, row));
-        } else {
-            const float g = rbf(apply_scale(acc[0], scale, row));
-            const float u = rbf(apply_scale(acc[NROW - 1], scale, S + row));
-            v = rbf(silu_f32(g)) * u;
-        }
-        if (lane == 0) y[row] = (uint16_t)f2bf(v);
-    };
+    // NB rows (items) per round: their NROW NB per-lane partials are reduced together (fold_sum), and the lane that
+    // holds item j's sums applies its epilogue and stores it, so reduction and epilogue run once per round
+    constexpr int V = NROW * NB;
+    constexpr int LPV = 64 / V;
     // NB row buffers used in turn: while a row is reduced, the NB - 1 rows after it are in flight (about 4-6 KiB
     // per wavefront, 32-48 KiB per CU at 8 wavefronts per CU: enough to cover the loaded HBM latency). Prefetches
     // are unconditional -- past the last row they go through an empty buffer range and cost no memory traffic --
@@ -150,15 +132,54 @@ __global__ __launch_bounds__(256) void gemv_b1p_kernel(const WT *__restrict__ W,
     for (int j = 0; j < NB - 1; ++j) load(buf[j], n + j * nw);
     bool more = true;
     while (more) {
+        const int row0 = n;
+        float part[V];  // value i NB + j: weight row i (w1, w3) of item j
+        float sc[V];
+        uint32_t hres[NB];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             if (more) {
                 load(buf[(j + NB - 1) % NB], n + (NB - 1) * nw);
                 __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the current row's math
-                finish(buf[j], n);
+#pragma unroll
+                for (int i = 0; i < NROW; ++i) {
+                    float a = 0.f;
+#pragma unroll
+                    for (int u = 0; u < CPL; ++u) a = D::dot(buf[j].w[u][i], xr[u], a);
+                    part[i * NB + j] = a;
+                    sc[i * NB + j] = buf[j].s[i];
+                }
+                hres[j] = EPI == EPI_RESIDUAL ? buf[j].h : 0u;
                 n += nw;
                 more = n < N;
+            } else {
+#pragma unroll
+                for (int i = 0; i < NROW; ++i) part[i * NB + j] = 0.f, sc[i * NB + j] = 1.f;
+                hres[j] = 0u;
             }
+        }
+        const float r = fold_sum<V>(part);  // value v in lanes v 64 / V ...
+        // SwiGLU: the w3 sum of item j sits 32 lanes above its w1 sum
+        const float ru = EPI == EPI_SWIGLU ? __uint_as_float(__builtin_amdgcn_permlane32_swap(
+                                                 __float_as_uint(r), __float_as_uint(r), false, false)[1])
+                                           : 0.f;
+        const int j = lane / LPV, row = row0 + j * nw;
+        if (lane % LPV == 0 && j < NB && row < N) {
+            float sg = 1.f, su = 1.f;
+            uint32_t h = 0u;
+#pragma unroll
+            for (int jj = 0; jj < NB; ++jj)
+                if (jj == j) sg = sc[jj], su = sc[(NROW - 1) * NB + jj], h = hres[jj];
+            float v;
+            if (EPI == EPI_NONE) {
+                v = scale ? r * sg : r;
+            } else if (EPI == EPI_RESIDUAL) {
+                v = bf2f(h) + rbf(scale ? r * sg : r);
+            } else {
+                const float g = rbf(scale ? r * sg : r), u = rbf(scale ? ru * su : ru);
+                v = rbf(silu_f32(g)) * u;
+            }
+            y[row] = (uint16_t)f2bf(v);
         }
     }
 }
@@ -167,7 +188,8 @@ __global__ __launch_bounds__(256) void gemv_b1p_kernel(const WT *__restrict__ W,
 // CU in flight at once -- the better shape while a matrix is too small to give each of ~8 wavefronts per CU several
 // rows). CPL > 0: K = 64 PER CPL, all of a wavefront's weight and activation loads are issued before the first
 // dot. CPL == 0: any K % PER == 0, chunks streamed 8 per lane at a time. Per row, the arithmetic is that of the
-// persistent kernel (same chunk order, same PairDot, same reduction), so either kernel gives the same bits.
+// persistent kernel (same chunk order, same PairDot, same fold_sum lane pairing), so either kernel gives the same
+// bits.
 template <typename WT, int R, int CPL, int EPI>
 __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, const float *__restrict__ scale,
                                                       const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
@@ -185,6 +207,11 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, 
         const int wrow = (EPI == EPI_SWIGLU && i >= R) ? S + orow : orow;
         rp[i] = reinterpret_cast<const char *>(W + (size_t)wrow * K);
     }
+    // the epilogue's operands for the row this lane will store (lane i 64 / NROW stores row n0 + i), read first
+    constexpr int LPV = 64 / NROW;
+    const int ns = min(n0 + min(lane / LPV, R - 1), N - 1);
+    const float sg = scale ? scale[ns] : 1.f, su = (EPI == EPI_SWIGLU && scale) ? scale[S + ns] : 1.f;
+    const uint32_t h0 = EPI == EPI_RESIDUAL ? y[ns] : 0u;
     float acc[NROW];
 #pragma unroll
     for (int i = 0; i < NROW; ++i) acc[i] = 0.f;
@@ -223,25 +250,20 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, 
                     for (int i = 0; i < NROW; ++i) acc[i] = D::dot(w[u][i], xr[u], acc[i]);
         }
     }
-#pragma unroll
-    for (int i = 0; i < NROW; ++i) acc[i] = wave_sum(acc[i]);
-
-    if (lane >= R) return;
-    const int n = n0 + lane;
-    if (n >= N) return;
-    float a = acc[0], b = EPI == EPI_SWIGLU ? acc[R] : 0.f;
-#pragma unroll
-    for (int i = 1; i < R; ++i)
-        if (lane == i) {
-            a = acc[i];
-            if (EPI == EPI_SWIGLU) b = acc[R + i];
-        }
+    // all NROW row sums in one transposed reduction: row i's sum lands in lanes i 64 / NROW ...; SwiGLU: the w3 sum of
+    // output i sits 32 lanes above its w1 sum
+    const float r = fold_sum<NROW>(acc);
+    const float ru = EPI == EPI_SWIGLU ? __uint_as_float(__builtin_amdgcn_permlane32_swap(
+                                             __float_as_uint(r), __float_as_uint(r), false, false)[1])
+                                       : 0.f;
+    const int n = n0 + lane / LPV;
+    if (lane % LPV != 0 || lane / LPV >= R || n >= N) return;
     if (EPI == EPI_NONE) {
-        y[n] = (uint16_t)f2bf(apply_scale(a, scale, n));
+        y[n] = (uint16_t)f2bf(scale ? r * sg : r);
     } else if (EPI == EPI_RESIDUAL) {
-        y[n] = (uint16_t)f2bf(bf2f(y[n]) + rbf(apply_scale(a, scale, n)));
+        y[n] = (uint16_t)f2bf(bf2f(h0) + rbf(scale ? r * sg : r));
     } else {
-        const float g = rbf(apply_scale(a, scale, n)), u = rbf(apply_scale(b, scale, S + n));
+        const float g = rbf(scale ? r * sg : r), u = rbf(scale ? ru * su : ru);
         y[n] = (uint16_t)f2bf(rbf(silu_f32(g)) * u);
     }
 }
@@ -481,7 +503,9 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 
 // ------------------------------------------------------------------------------------------------ dispatch
 // Batch 1. Persistent kernel (LFM2Q_GEMV_WPC wavefronts per CU, default 8: the read-stream optimum measured on
-// MI355X) once every wavefront gets at least 8 rows, one-shot kernel (one wavefront per row) below that. Both need
+// MI355X) once every wavefront gets at least 8 rows, one-shot kernel below that with R output rows per wavefront:
+// R = 2 from 6144 weight rows (half the wavefronts, each with twice the loads in flight and one reduction for both
+// rows), else 1; LFM2Q_GEMV_R = 1, 2 or 4 overrides it where the registers allow (read on every call). Both need
 // K = 64 PER CPL with CPL in {1, 2, 4, 8}; other K take the one-shot kernel's generic loop, where `rows` (1, 2, 4)
 // sets the output rows per wavefront. Per-row arithmetic is the same in all of them.
 template <typename WT, int EPI>
@@ -493,13 +517,20 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
     const int cpl = C % 64 == 0 ? C / 64 : 0;
     const int blocks_p = device_cus() * (wpc < 4 ? 1 : wpc / 4);
     const bool persistent = (long)N >= 8L * 4 * blocks_p;
-    const dim3 grid1((N + 3) / 4), gridp(std::min((N + 3) / 4, blocks_p));
-#define LFM2Q_B1(C_)                                                                            \
-    do {                                                                                        \
-        if (persistent)                                                                         \
-            gemv_b1p_kernel<WT, C_, EPI><<<gridp, 256, 0, st>>>(W, scale, x, y, N, K, S);       \
-        else                                                                                    \
-            gemv_b1_kernel<WT, 1, C_, EPI><<<grid1, 256, 0, st>>>(W, scale, x, y, N, K, S);     \
+    int r1 = (EPI == EPI_SWIGLU ? 2L * N : (long)N) >= 6144 ? 2 : 1;
+    if (const char *e = getenv("LFM2Q_GEMV_R")) r1 = atoi(e);
+    auto grid = [&](int R) { return dim3((N + 4 * R - 1) / (4 * R)); };
+    const dim3 gridp(std::min((N + 3) / 4, blocks_p));
+#define LFM2Q_B1(C_)                                                                                        \
+    do {                                                                                                    \
+        if (persistent)                                                                                     \
+            gemv_b1p_kernel<WT, C_, EPI><<<gridp, 256, 0, st>>>(W, scale, x, y, N, K, S);                   \
+        else if (r1 == 4 && C_ <= 2)                                                                        \
+            gemv_b1_kernel<WT, C_ <= 2 ? 4 : 1, C_, EPI><<<grid(4), 256, 0, st>>>(W, scale, x, y, N, K, S); \
+        else if (r1 == 2 && C_ <= 4)                                                                        \
+            gemv_b1_kernel<WT, C_ <= 4 ? 2 : 1, C_, EPI><<<grid(2), 256, 0, st>>>(W, scale, x, y, N, K, S); \
+        else                                                                                                \
+            gemv_b1_kernel<WT, 1, C_, EPI><<<grid(1), 256, 0, st>>>(W, scale, x, y, N, K, S);               \
     } while (0)
     switch (cpl) {
         case 1: LFM2Q_B1(1); break;
@@ -507,7 +538,6 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
         case 4: LFM2Q_B1(4); break;
         case 8: LFM2Q_B1(8); break;
         default: {
-            auto grid = [&](int R) { return dim3((N + 4 * R - 1) / (4 * R)); };
             if (EPI == EPI_SWIGLU || rows <= 1)
                 gemv_b1_kernel<WT, 1, 0, EPI><<<grid(1), 256, 0, st>>>(W, scale, x, y, N, K, S);
             else if (rows == 2)

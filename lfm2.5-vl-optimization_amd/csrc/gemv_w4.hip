@@ -145,38 +145,59 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
             for (int e = 0; e < 4; ++e) xs[u] += bf2f_lo((uint32_t)d[e]) + bf2f_hi((uint32_t)d[e]);
         }
     }
-    auto finish = [&](const Item &it, int row) {
-        float acc[NROW];
+    // a row's per-lane partial: sum_u s_u (dot_u - (128 + z_u) xs_u)
+    auto partial = [&](const Item &it, int i) {
+        float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < NROW; ++i) {
-            acc[i] = 0.f;
+        for (int u = 0; u < CPL; ++u) {
+            float d = 0.f;
 #pragma unroll
-            for (int u = 0; u < CPL; ++u) {
-                float d = 0.f;
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int p = 0; p < 4; ++p)
-                        d = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nm.pair((uint32_t)it.w[u][i][j], p)),
-                                                            as_bf16x2(xp[u][4 * j + p]), d, false);
-                acc[i] += it.s[u][i] * (d - (float)(128 + it.z[u][i]) * xs[u]);
-            }
-            acc[i] = wave_sum(acc[i]);
+                for (int p = 0; p < 4; ++p)
+                    d = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nm.pair((uint32_t)it.w[u][i][j], p)),
+                                                        as_bf16x2(xp[u][4 * j + p]), d, false);
+            acc += it.s[u][i] * (d - (float)(128 + it.z[u][i]) * xs[u]);
         }
-        const float v = epi_value(EPI, acc[0], acc[NROW - 1], EPI == EPI_RESIDUAL ? it.h : 0u);
-        if (lane == 0) y[row] = (uint16_t)f2bf(v);
+        return acc;
     };
+    // NB rows (items) per round; their NROW NB partials are reduced together (fold_sum) and the lane holding item
+    // j's sum applies the epilogue and stores it, so the reduction and the epilogue run once per round
+    constexpr int V = NROW * NB;
     bool more = true;
     while (more) {
+        const int row0 = n;
+        float part[V];  // value i NB + j: weight row i (w1, w3) of item j
+        uint32_t hres[NB];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             if (more) {
                 load(buf[(j + NB - 1) % NB], n + (NB - 1) * nw);
                 __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the current row's math
-                finish(buf[j], n);
+#pragma unroll
+                for (int i = 0; i < NROW; ++i) part[i * NB + j] = partial(buf[j], i);
+                hres[j] = EPI == EPI_RESIDUAL ? buf[j].h : 0u;
                 n += nw;
                 more = n < N;
+            } else {
+#pragma unroll
+                for (int i = 0; i < NROW; ++i) part[i * NB + j] = 0.f;
+                hres[j] = 0u;
             }
+        }
+        const float r = fold_sum<V>(part);  // value v in lanes v 64 / V ...
+        // SwiGLU: the w3 sum of item j sits 32 lanes above its w1 sum
+        const float u = EPI == EPI_SWIGLU ? __uint_as_float(__builtin_amdgcn_permlane32_swap(
+                                                __float_as_uint(r), __float_as_uint(r), false, false)[1])
+                                          : 0.f;
+        constexpr int LPV = 64 / V;
+        const int j = lane / LPV, row = row0 + j * nw;
+        if (lane % LPV == 0 && j < NB && row < N) {
+            uint32_t h = 0u;
+#pragma unroll
+            for (int jj = 0; jj < NB; ++jj)
+                if (jj == j) h = hres[jj];
+            y[row] = (uint16_t)f2bf(epi_value(EPI, r, u, h));
         }
     }
 }
