@@ -37,7 +37,7 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 # --pmc runs of `bench.py --eager-kind 'w1|w3+swiglu'` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled
 # by what the counter reads for a 256 MiB device copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0): the run recorded in
 # profiles/hbm_traffic_counters.md. Re-measure after changing that kernel.
-W13_TRAFFIC_BYTES = 34216117
+W13_TRAFFIC_BYTES = 33947648
 # W8A8 shapes (M, K, N, bias, gelu, name): LFM2 prefill at 512 / 2048 / 4096 tokens, SigLIP2 vision at 10 tiles
 W8A8_SHAPES = ([(M, K, N, False, False, f"prefill M={M} {n}") for M in (512, 2048, 4096)
                 for K, N, n in ((2048, 3072, "qkv"), (2048, 16384, "w1|w3"), (8192, 2048, "w2"))]
@@ -525,7 +525,7 @@ def main():
                    "compute": "int8 weights x bf16 activations, fp32 accumulation, bf16 out",
                    "parallelism": "single GPU"},
         "hbm_frac": round(res1["hbm_frac"], 4),
-        "roofline": {"bound": "hbm", "kernel": "gemv_b1_kernel<int8,1,2,SWIGLU> (w1|w3 16384x2048 + SwiGLU)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_b1_kernel<int8,2,2,SWIGLU> (w1|w3 16384x2048 + SwiGLU)",
                      "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": W13_TRAFFIC_BYTES,
                      "us_per_launch": dom["us_per_launch"], "bytes_per_launch": dom["bytes_per_launch"]},
