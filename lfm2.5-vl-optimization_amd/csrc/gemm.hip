@@ -76,6 +76,22 @@ __device__ __forceinline__ void tile_of(int w, int tm_n, int tn_n, int &tm, int 
 
 constexpr int STAGES = 3;  // LDS ring depth: stage s computes while s + 1 and s + 2 are loading
 
+// s_waitcnt immediate for vmcnt(n) with the other counters at their maximum (gfx9: vmcnt bits 3:0 and 15:14)
+constexpr int vmcnt_imm(int n) { return 0x3f70 | (n & 15) | ((n >> 4) << 14); }
+// wait until at most `ahead` stages of PER loads each are outstanding (ahead <= 6)
+template <int PER>
+__device__ __forceinline__ void wait_stages(int ahead) {
+    switch (ahead) {
+        case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * PER)); break;
+        case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * PER)); break;
+        case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * PER)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * PER)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER)); break;
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    }
+}
+
 // Raw buffer descriptor in four SGPRs: base, stride 0, num_records = bytes, gfx9 word 3.
 __device__ __forceinline__ v4i make_desc(const void *base, uint32_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(base);
@@ -276,7 +292,7 @@ __device__ __forceinline__ void epilogue(const ACC (&acc)[TN][TM], const float *
 // facc = fma((float)acc, sxT[kt, m], facc), in stage order -- the reference's fold, exact per group since |acc| <=
 // 64 * 127^2 < 2^24. The group's scales for the tile's rows travel with the operands (one 4-byte direct load per
 // wavefront per stage into a 1 KiB LDS slot) and are read after the stage's barrier. YsT: OUT_Q8 scales.
-template <int BM, int BN, int OUT, bool GRP = false>
+template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES>
 __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
@@ -286,12 +302,12 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     constexpr int IX = BM / 64, IW = BN / 64;    // direct-load instructions per wavefront per stage (16 rows each)
     constexpr int IS = GRP ? 1 : 0;               // scale loads per wavefront per stage
     static_assert(IX >= 1 && IW >= 1 && TM >= 1 && TN >= 1, "tile too small");
-    static_assert(4 * stage_bytes<TN>() <= STAGES * (BM + BN) * BK, "epilogue staging exceeds the LDS ring");
+    static_assert(4 * stage_bytes<TN>() <= NSTG * (BM + BN) * BK, "epilogue staging exceeds the LDS ring");
     static_assert(!out_q8(OUT) || (GRP && WNt % 64 == 0), "INT8 output needs grouped input and 64-column blocks");
-    constexpr int RING = STAGES * (BM + BN) * BK;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + (GRP ? STAGES * 1024 : 0)];
+    constexpr int RING = NSTG * (BM + BN) * BK;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + (GRP ? NSTG * 1024 : 0)];
     uint8_t(*sX)[BM * BK] = reinterpret_cast<uint8_t(*)[BM * BK]>(smem);
-    uint8_t(*sW)[BN * BK] = reinterpret_cast<uint8_t(*)[BN * BK]>(smem + STAGES * BM * BK);
+    uint8_t(*sW)[BN * BK] = reinterpret_cast<uint8_t(*)[BN * BK]>(smem + NSTG * BM * BK);
     float(*sS)[256] = reinterpret_cast<float(*)[256]>(smem + RING);  // GRP: [stage][tile row]
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -320,7 +336,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
         ow[j] = (uint32_t)row * K + cw[j];
     }
     auto issue = [&](int kt) {
-        const int buf = kt % STAGES, k0 = kt * BK;
+        const int buf = kt % NSTG, k0 = kt * BK;
 #pragma unroll
         for (int j = 0; j < IX; ++j) {
             const uint32_t vo = k0 + cx[j] < K ? ox[j] + k0 : 0xfffffff0u;
@@ -363,20 +379,19 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
         for (int j = 0; j < TM; ++j) fx[kk][j] = swz(wm * WMt + 32 * j + lr, 2 * kk + lh, sh);
     }
 
-    issue(0);
-    if (KT > 1) issue(1);
+    static_assert((NSTG - 2) * (IX + IW + IS) <= 63 && NSTG - 2 <= 6, "vmcnt holds at most 63 loads");
+#pragma unroll
+    for (int p = 0; p < NSTG - 1; ++p)
+        if (p < KT) issue(p);
     for (int kt = 0; kt < KT; ++kt) {
-        // stage kt has landed once at most the loads of stage kt + 1 are outstanding
-        if (kt + 1 < KT)
-            __builtin_amdgcn_s_waitcnt(0x3f70 | (IX + IW + IS));  // vmcnt(one stage's loads), other counters max
-        else
-            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+        // stage kt has landed once at most the loads of the (up to NSTG - 2) stages issued after it are outstanding
+        wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
         // stage kt visible to all; everyone is done with stage kt - 1, whose buffer refills next. A bare s_barrier:
         // __syncthreads()' fences would make the compiler drain every outstanding load here, the prefetches included
         // (LDS needs no cache maintenance between the wavefronts of a workgroup).
         asm volatile("s_barrier" ::: "memory");
-        if (kt + 2 < KT) issue(kt + 2);
-        const uint8_t *x_s = sX[kt % STAGES], *w_s = sW[kt % STAGES];
+        if (kt + NSTG - 1 < KT) issue(kt + NSTG - 1);
+        const uint8_t *x_s = sX[kt % NSTG], *w_s = sW[kt % NSTG];
         // both k steps' fragments are read up front, the second set while the first set's MFMAs run
         v4i wf[2][TN], xf[2][TM];
 #pragma unroll
@@ -397,7 +412,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk][i], xf[kk][j],
                                                                      (GRP && kk == 0) ? zero : acc[i][j], 0, 0, 0);
         if (GRP) {
-            const float *s_s = sS[kt % STAGES];
+            const float *s_s = sS[kt % NSTG];
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const float sj = s_s[wm * WMt + 32 * j + lr];
@@ -703,9 +718,19 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
         }
         return;
     }
+    // LDS ring depth 6 (4 stages in flight) for a small tile whose grid leaves one workgroup per CU on a long K: a
+    // lone workgroup with 2 stages in flight is bound by the operand latency (w2 at 512 tokens: 45 -> 35 us); the
+    // deeper ring's LDS costs occupancy everywhere else. LFM2Q_GEMM_STAGES = 3 / 6 forces it.
+    const bool small = t.bm + t.bn <= 192;
+    int nst = (small && (long)grid.x <= device_cus() && K >= 4096) ? 6 : 3;
+    if (const int f = env_int("LFM2Q_GEMM_STAGES", 0)) nst = f == 6 && small ? 6 : 3;
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
-        gemm_i8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K, sh);                     \
+        if (BM_ + BN_ <= 192 && nst == 6)                                                                            \
+            gemm_i8_kernel<BM_, BN_, OUT, false, (BM_ + BN_ <= 192 ? 6 : 3)><<<grid, GT, 0, st>>>(A, B, sx, sw,      \
+                                                                                                  bias, Y, M, N, K, sh); \
+        else                                                                                                         \
+            gemm_i8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K, sh);                 \
         return;                                                                                                      \
     }
     LFM2Q_GEMM(128, 256)

@@ -145,11 +145,14 @@ def test_gemm_vision_shapes(E, M, K, N, gelu):
 TILES = [(256, 256), (128, 256), (256, 128), (128, 128), (128, 64), (64, 128), (64, 64)]
 
 
-@pytest.mark.parametrize("bm,bn", TILES)
-def test_gemm_every_tile_config(E, bm, bn, monkeypatch):
-    """Each kernel configuration (forced through LFM2Q_GEMM_BM / _BN) on a shape with M, N and K tails."""
+@pytest.mark.parametrize("bm,bn,stages", [(bm, bn, 3) for bm, bn in TILES]
+                         + [(bm, bn, 6) for bm, bn in TILES if bm + bn <= 192])
+def test_gemm_every_tile_config(E, bm, bn, stages, monkeypatch):
+    """Each kernel configuration (tile forced through LFM2Q_GEMM_BM / _BN, LDS ring depth through
+    LFM2Q_GEMM_STAGES) on a shape with M, N and K tails."""
     monkeypatch.setenv("LFM2Q_GEMM_BM", str(bm))
     monkeypatch.setenv("LFM2Q_GEMM_BN", str(bn))
+    monkeypatch.setenv("LFM2Q_GEMM_STAGES", str(stages))
     M, K, N = 300, 4304, 520
     xq, sx, wq, sw, b = _operands(bm * 7 + bn, M, K, N, True)
     acc = oracle.gemm_i8_i32(xq, wq)
