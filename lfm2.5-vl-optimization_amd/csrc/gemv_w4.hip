@@ -231,7 +231,7 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
     const NibbleMasks nm;
     constexpr int TR = 16 / KS;
     constexpr int NT = (EPI == EPI_SWIGLU ? 2 : 1) * RT;
-    constexpr int KB = NT >= 4 ? 1 : 2;     // blocks per stage (a block holds 8 activation registers per lane)
+    constexpr int KB = 2;                   // blocks per stage (a block holds 8 activation registers per lane)
     constexpr uint32_t OOR = 0x40000000u;   // an offset past every range below: the load returns zeros
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
@@ -419,8 +419,8 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
 // Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
 // [2 S, K/8] matrix) then split K alike, which keeps the fused epilogues bit-identical:
 //   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows; RT = 2 for 6144+ weight rows unless
-//   KS = 2; NWK (at most 16) from the 256-k blocks per wavefront: 2 when RT = 2, 4 when KS = RT = 1, 8 when KS = 2
-//   (at least 4 wavefronts). LFM2Q_W4_MFMA = "KS,RT,NWK" overrides the shape (read on every call).
+//   KS = 2; NWK from the 256-k blocks per wavefront: 2 when RT = 2 (at most 8 wavefronts), 4 when KS = RT = 1, 8
+//   when KS = 2 (at least 4 wavefronts; at most 16). LFM2Q_W4_MFMA = "KS,RT,NWK" overrides the shape (read on every call).
 template <int FMT, int EPI, int KS, int RT>
 void launch_w4_shape(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int B, int N,
                      int K, int group, int nwk, hipStream_t st) {
@@ -446,7 +446,8 @@ void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uin
     int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
     const int bpw = ks == 2 ? 8 : rt == 2 ? 2 : 4;  // target blocks per wavefront
     int nwk = 1;
-    while (nwk < 16 && (nblk >= bpw * 2 * nwk || (ks == 2 && nwk < 4))) nwk *= 2;
+    // at most 8 wavefronts with two tiles pairs (16 would cap the registers at 128 and spill)
+    while (nwk < (rt == 2 ? 8 : 16) && (nblk >= bpw * 2 * nwk || (ks == 2 && nwk < 4))) nwk *= 2;
     int fk = 0, fr = 0, fn = 0;
     if (const char *e = getenv("LFM2Q_W4_MFMA"))
         if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
