@@ -242,6 +242,61 @@ def cpu_baseline(budget_s=10.0):
                       f"timed region; os.cpu_count()={os.cpu_count()}, cpu='{cpu_model()}'"}
 
 
+def _median_time(fn, budget_s, max_reps=50):
+    fn()  # warm-up
+    times, t_start = [], time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baselines_extra(budget_s=4.0):
+    """The other CPU references of the path, each on a bounded sample (reported beside cpu_baseline, not used in
+    `value`): the INT8 GEMV with the weights dequantized once outside the timed region, the INT4 GEMV (GPTQ-style,
+    dequant inside, tests/test_kernels.py:150) and the W8A8 fake-quant GEMM (per-token quant + fp32 matmul of the
+    dequantized operands, profiling/int8_quality_probe.py:150-160), all restated in oracle/cpu_baseline.py."""
+    from oracle.cpu_baseline import gemv_w4_dequant_matmul, w8a8_fake_quant
+
+    g = torch.Generator().manual_seed(1)
+    cores = torch.get_num_threads()
+    out = {}
+    shapes = [(QKV, H), (H, H), (CONV_IN, H), (2 * FFN, H), (H, FFN), (VOCAB, H)]
+    mats = []
+    for N, K in shapes:
+        W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+        s = torch.rand(N, generator=g) * 0.01 + 1e-3
+        mats.append((W.float() * s[:, None], torch.randn(1, K, generator=g).to(torch.bfloat16)))
+    nbytes = sum(gemv_bytes(N, K, 1) for N, K in shapes)
+    t, n = _median_time(lambda: [F.linear(x.float(), Wd).to(torch.bfloat16) for Wd, x in mats], budget_s)
+    out["gemv_int8_dequantized_once"] = {
+        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s (INT8 algorithmic bytes)", "cores": cores, "kind": "port",
+        "sample": f"the 6 decode GEMV shapes at batch 1, fp32 weights dequantized before timing, median of {n}"}
+    w4 = []
+    for N, K in shapes:
+        G = K // W4_GROUP
+        q = torch.randint(0, 16, (N, K), generator=g, dtype=torch.uint8)
+        z = torch.randint(0, 16, (N, G), generator=g, dtype=torch.uint8)
+        sc = (torch.randn(N, G, generator=g).abs() * 0.02 + 1e-3).half()
+        w4.append((q, sc, z, torch.randn(1, K, generator=g).to(torch.bfloat16)))
+    nb4 = sum(w4_bytes(N, K, 1) for N, K in shapes)
+    t, n = _median_time(lambda: [gemv_w4_dequant_matmul(q, sc, z, x, W4_GROUP) for q, sc, z, x in w4], budget_s)
+    out["gemv_int4"] = {
+        "value": round(nb4 / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+        "sample": f"the 6 decode GEMV shapes at batch 1, GPTQ-style (group 128, zero points), dequant inside the "
+                  f"timed region, {nb4 / 1e6:.1f} MB per pass, median of {n}"}
+    M, K, N = 512, 2048, 3072
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    wq = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.rand(N, generator=g) * 0.01 + 1e-3
+    t, n = _median_time(lambda: w8a8_fake_quant(x, wq, sw), budget_s)
+    out["w8a8_fake_quant"] = {
+        "value": round(2.0 * M * N * K / t / 1e12, 4), "unit": "TOPS", "cores": cores, "kind": "port",
+        "sample": f"prefill qkv {M}x{K}x{N}, per-token quant + fp32 matmul of the dequantized operands, median of {n}"}
+    return out
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -563,6 +618,8 @@ def main():
     if not args.no_cpu:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline()
+        log("cpu baselines of the other paths")
+        out["cpu_baselines_extra"] = cpu_baselines_extra()
     print(json.dumps(out))
 
 
