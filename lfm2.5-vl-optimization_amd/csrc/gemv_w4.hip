@@ -404,7 +404,11 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
 template <int FMT, int EPI>
 void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int N, int K,
                   int group, hipStream_t st) {
-    static const int wpc = env_int("LFM2Q_W4_WPC", 8);
+    // wavefronts per CU: 4 up to 3072 rows (each wavefront amortizes its activation repack over more rows), 16 from
+    // 32768 rows (more loads in flight on a long stream), else 8; LFM2Q_W4_WPC overrides (read once)
+    static const int wpc_env = env_int("LFM2Q_W4_WPC", 0);
+    const long wrows = (EPI == EPI_SWIGLU ? 2L : 1L) * N;
+    const int wpc = wpc_env > 0 ? wpc_env : wrows <= 3072 ? 4 : wrows >= 32768 ? 16 : 8;
     const int C = K / 32;
     const int blocks = std::min((N + 3) / 4, std::max(1, device_cus() * wpc / 4));
     const dim3 grid(blocks);
