@@ -552,7 +552,8 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 // Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
 // [2 S, K] matrix) then split K alike, which keeps the fused epilogues bit-identical:
 //   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows (256+ workgroups instead of 128);
-//   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2;
+//   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2, RT = 4 above 8 batch rows
+//   for 32768+ rows without SwiGLU (the lm_head);
 //   NWK (at most 16) from the 128-k blocks per wavefront: 2 when RT = 2, 4 when KS = RT = 1, 8 when KS = 2
 //   (at least 4 wavefronts). Measured on MI355X over the LFM2 decode shapes at batches 4, 8 and 16.
 // LFM2Q_GEMV_MFMA = "KS,RT,NWK" overrides the shape (read on every call; the last bits of the sums change with it).
@@ -579,19 +580,23 @@ void launch_mfma(const WT *W, const float *scale, const uint16_t *x, uint16_t *y
     const int nblk = (K + 127) / 128;
     int ks = (B <= 8 && wrows <= 2048) ? 2 : 1;
     int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
-    const int bpw = ks == 2 ? 8 : rt == 2 ? 2 : 4;  // target blocks per wavefront
+    if (EPI != EPI_SWIGLU && B > 8 && wrows >= 32768) rt = 4;  // halves the activation reads per weight byte again
+    const int bpw = ks == 2 ? 8 : rt >= 2 ? 2 : 4;  // target blocks per wavefront
     int nwk = 1;
     while (nwk < 16 && (nblk >= bpw * 2 * nwk || (ks == 2 && nwk < 4))) nwk *= 2;
     int fk = 0, fr = 0, fn = 0;
     if (const char *e = getenv("LFM2Q_GEMV_MFMA"))
         if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
-            (fr == 1 || fr == 2) && (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
+            (fr == 1 || fr == 2 || (fr == 4 && fk == 1 && EPI != EPI_SWIGLU)) &&
+            (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
             ks = fk;
             rt = fr;
             nwk = fn;
         }
     if (ks == 2)
         launch_mfma_shape<WT, EPI, 2, 1>(W, scale, x, y, B, N, K, S, nwk, st);
+    else if (EPI != EPI_SWIGLU && rt == 4)
+        launch_mfma_shape<WT, EPI, 1, EPI == EPI_SWIGLU ? 1 : 4>(W, scale, x, y, B, N, K, S, nwk, st);
     else if (rt == 2)
         launch_mfma_shape<WT, EPI, 1, 2>(W, scale, x, y, B, N, K, S, nwk, st);
     else

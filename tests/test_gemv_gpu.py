@@ -99,7 +99,7 @@ def test_gemv_w8_vs_oracle(E, B, N, K):
     assert_close_bf16(host_bits(y), ref, what=f"gemv int8 B={B} [{N}x{K}]")
 
 
-@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,8", "1,2,1", "2,1,1", "2,1,2", "2,1,16"])
+@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,8", "1,2,1", "1,4,8", "1,4,1", "2,1,1", "2,1,2", "2,1,16"])
 @pytest.mark.parametrize("wt", ["int8", "bf16"])
 def test_gemv_mfma_launch_shapes(E, monkeypatch, shape, wt):
     """Every batch-2..16 launch shape (k-parts KS, row tiles RT, wavefronts NWK, forced through LFM2Q_GEMV_MFMA)
