@@ -6,12 +6,12 @@
 //                     of each row with non-temporal loads (a wavefront load = 1 KiB contiguous of one row), all of
 //                     a lane's chunks are in flight before the first FMA. int8 -> fp32 is one SDWA convert per
 //                     weight; the row sums of a wavefront's rows are reduced together (fold_sum). No LDS.
-//   gemv_mfma_kernel  batch 2..16. A workgroup owns 16 (or 32) output rows; its NWK wavefronts split K into
-//                     128-k blocks. A wave's two loads per block and tile row cover 16 whole 128-byte lines; the
-//                     weights are converted exactly to bf16 in registers and feed v_mfma_f32_16x16x32_bf16 with the
-//                     activations as the A operand (16 batch rows x 32 k) and the weights as B (32 k x 16 output
-//                     rows). The NWK partial 16x16 tiles meet in LDS. The matrix cores take the batch FMAs off the
-//                     VALU (1.5 VALU ops per weight at any batch), so the kernel stays HBM-bound up to B = 16.
+//   gemv_mfma_kernel  batch 2..16. A workgroup owns RT tiles of 16 output rows (8 when the K run is split in two
+//                     inside the MFMA, batches <= 8); its NWK wavefronts split K into 128-k blocks. A tile block is
+//                     read by two wave loads of 8 whole 128-byte lines; the weights are converted exactly to bf16 in
+//                     registers and feed v_mfma_f32_16x16x32_bf16 with the activations as the A operand (batch rows
+//                     x 32 k) and the weights as B (32 k x output rows). The partial tiles meet in LDS. The matrix
+//                     cores take the batch FMAs off the VALU (about 1.5 VALU ops per weight at any batch).
 // The per-row accumulation order of each kernel does not depend on which epilogue runs or on how many rows a
 // wavefront owns, so the fused epilogues are bit-identical to the plain GEMV followed by the separate op.
 //
