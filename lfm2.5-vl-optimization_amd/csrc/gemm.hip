@@ -720,14 +720,15 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
     }
     // LDS ring depth 6 (4 stages in flight) for a small tile whose grid leaves one workgroup per CU on a long K: a
     // lone workgroup with 2 stages in flight is bound by the operand latency (w2 at 512 tokens: 45 -> 35 us); the
-    // deeper ring's LDS costs occupancy everywhere else. LFM2Q_GEMM_STAGES = 3 / 6 forces it.
+    // deeper ring's LDS costs occupancy everywhere else. LFM2Q_GEMM_STAGES = 3 / 6 forces it (6 for any tile but
+    // 256 x 256, which has its own ring).
     const bool small = t.bm + t.bn <= 192;
     int nst = (small && (long)grid.x <= device_cus() && K >= 4096) ? 6 : 3;
-    if (const int f = env_int("LFM2Q_GEMM_STAGES", 0)) nst = f == 6 && small ? 6 : 3;
+    if (const int f = env_int("LFM2Q_GEMM_STAGES", 0)) nst = f == 6 && t.bm + t.bn <= 384 ? 6 : 3;
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
-        if (BM_ + BN_ <= 192 && nst == 6)                                                                            \
-            gemm_i8_kernel<BM_, BN_, OUT, false, (BM_ + BN_ <= 192 ? 6 : 3)><<<grid, GT, 0, st>>>(A, B, sx, sw,      \
+        if (BM_ + BN_ <= 384 && nst == 6)                                                                            \
+            gemm_i8_kernel<BM_, BN_, OUT, false, (BM_ + BN_ <= 384 ? 6 : 3)><<<grid, GT, 0, st>>>(A, B, sx, sw,      \
                                                                                                   bias, Y, M, N, K, sh); \
         else                                                                                                         \
             gemm_i8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K, sh);                 \

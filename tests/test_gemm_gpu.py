@@ -146,7 +146,7 @@ TILES = [(256, 256), (128, 256), (256, 128), (128, 128), (128, 64), (64, 128), (
 
 
 @pytest.mark.parametrize("bm,bn,stages", [(bm, bn, 3) for bm, bn in TILES]
-                         + [(bm, bn, 6) for bm, bn in TILES if bm + bn <= 192])
+                         + [(bm, bn, 6) for bm, bn in TILES if bm + bn <= 384])
 def test_gemm_every_tile_config(E, bm, bn, stages, monkeypatch):
     """Each kernel configuration (tile forced through LFM2Q_GEMM_BM / _BN, LDS ring depth through
     LFM2Q_GEMM_STAGES) on a shape with M, N and K tails."""
