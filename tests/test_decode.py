@@ -1,0 +1,64 @@
+"""The decode dispatch's path choice (lfm2opt.decode.linear_path) on the CPU: the reference's rules where they carry
+over (src/lfm2opt/runtime.py:223-244: "cublas" always takes F.linear, quantized weights without a BF16 copy never
+do) and the MI355X thresholds at the LFM2 decode shapes."""
+
+import pytest
+
+from lfm2opt.decode import linear_path
+
+QKV, IN, W13, W2, HEAD, OUT = (3072, 2048), (6144, 2048), (16384, 2048), (2048, 8192), (65536, 2048), (2048, 2048)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int4"])
+@pytest.mark.parametrize("B", [1, 4, 16, 17, 64, 256])
+def test_cublas_mode_is_always_linear(fmt, B):
+    assert linear_path("cublas", fmt, B, *QKV, True) == "linear"
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("shape", [QKV, IN, W13, W2, HEAD, OUT])
+@pytest.mark.parametrize("B", [1, 2, 3, 8, 9, 16])
+def test_quantized_gemv_up_to_16(fmt, shape, B):
+    for kept in (True, False):
+        assert linear_path(fmt, fmt, B, *shape, kept) == "gemv"
+
+
+def test_int8_above_16():
+    # wide weights: W8A16 whether or not a BF16 copy is kept
+    for shape in (W13, HEAD):
+        for B in (17, 24, 64, 128):
+            assert linear_path("int8", "int8", B, *shape, True) == "w8a16"
+            assert linear_path("int8", "int8", B, *shape, False) == "w8a16"
+    # narrow weights: the BF16 copy when kept
+    for shape in (QKV, IN, W2, OUT):
+        assert linear_path("int8", "int8", 17, *shape, True) == "linear"
+        assert linear_path("int8", "int8", 300, *shape, True) == "linear"
+    # narrow weights without a copy: the GEMV up to 32 rows (64 at K = 8192), W8A16 beyond
+    assert [linear_path("int8", "int8", B, *QKV, False) for B in (17, 32, 33, 64)] == ["gemv", "gemv", "w8a16", "w8a16"]
+    assert [linear_path("int8", "int8", B, *W2, False) for B in (17, 64, 65, 128)] == ["gemv", "gemv", "w8a16", "w8a16"]
+
+
+def test_int4_above_16():
+    for shape in (QKV, W13, W2, HEAD):
+        for B in (17, 64, 1000):
+            assert linear_path("int4", "int4", B, *shape, True) == "linear"
+            assert linear_path("int4", "int4", B, *shape, False) == "gemv"  # no INT4 GEMM: the GEMV in 16-row chunks
+
+
+def test_int8_weights_in_int4_mode():
+    """w4_keep_int8 kinds are stored in INT8 under mode "int4" and follow the INT8 rules."""
+    assert linear_path("int4", "int8", 24, *HEAD, True) == "w8a16"
+    assert linear_path("int4", "int8", 24, *QKV, True) == "linear"
+
+
+def test_bf16_weights():
+    assert [linear_path("bf16", "bf16", B, *QKV, False) for B in (1, 8, 9, 16, 17)] == \
+        ["gemv", "gemv", "gemv", "gemv", "linear"]
+    assert [linear_path("bf16", "bf16", B, *W2, False) for B in (1, 8, 9, 16)] == ["gemv", "gemv", "linear", "linear"]
+
+
+def test_bad_arguments():
+    with pytest.raises(ValueError):
+        linear_path("fp8", "int8", 1, *QKV, True)
+    with pytest.raises(ValueError):
+        linear_path("int8", "fp4", 1, *QKV, True)
