@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <type_traits>
 
 namespace lfm2q {
 namespace {
@@ -302,15 +303,17 @@ __device__ __forceinline__ v8bf as_bf16x8(v4i v) { return __builtin_bit_cast(v8b
 // Every load goes through a buffer resource: rows past N, batch rows past B and k past K (a trailing half block)
 // read zeros without a memory access. The partial tiles (NWK wavefronts x KS parts) are summed in LDS in a fixed
 // order, every thread of the workgroup taking some of the outputs.
-template <typename WT, int KS, int RT, int NWK, int EPI>
+template <typename WT, int KS, int RT, int NWK, int EPI, int BT>
 __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restrict__ W, const float *__restrict__ scale,
                                                              const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
                                                              int B, int N, int K, int S) {
     constexpr bool I8 = sizeof(WT) == 1;
-    constexpr int TR = 16 / KS;             // weight rows per tile, batch rows per part
+    constexpr int TR = 16 / KS;             // weight rows per tile, batch rows per part of a batch tile
     constexpr int NT = (EPI == EPI_SWIGLU ? 2 : 1) * RT;
     constexpr int WL = I8 ? 2 : 4;          // 16-byte weight loads per lane per tile per block
-    constexpr int KB = NT * WL >= 8 ? 1 : 8 / (NT * WL);  // blocks per stage
+    // blocks per stage: at least 8 weight loads per lane in flight with one batch tile; with several, their
+    // activation loads are in flight too and the registers run out first
+    constexpr int KB = BT == 1 ? (NT * WL >= 8 ? 1 : 8 / (NT * WL)) : (NT * WL >= 4 || BT >= 4 ? 1 : 2);
     constexpr uint32_t BB = 128 * sizeof(WT);  // bytes of one row's block
     constexpr uint32_t OOR = 0x40000000u;   // an offset past every range below: the load returns zeros
     // the k range is wavefront-uniform: block conditions and offsets stay scalar where the lane does not matter
@@ -330,7 +333,7 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
     const int c8 = lane >> 3;  // int8: the lane's 16-byte chunk of a 128-byte row block
     const uint32_t woff = I8 ? (lane & 7) * rowb + 16 * c8 : (c % TR) * rowb + 16 * g;
     const int cpart = c / TR;  // part of this lane's B column (bf16) and A row
-    const uint32_t xoff = (uint32_t)(c % TR) * K * 2u + 16 * g;
+    const uint32_t xoff = (uint32_t)(c % TR) * K * 2u + 16 * g;  // batch tile j adds j TR rows
 
     // this wavefront's blocks [kb0, kb1): part s is kb0 + s P .. kb0 + s P + P - 1
     const int nblk = (K + 127) / 128;
@@ -338,21 +341,21 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
     const int kb0 = wave * per, kb1 = min(nblk, kb0 + per);
     const int P = (per + KS - 1) / KS;
 
-    // Output elements (tile t, batch row b, row r -> y[b][nbase + TR t + r]). Through LDS (NWK > 1 or KS > 1):
-    // thread threadIdx.x + 64 NWK i takes element TR TR t + TR b + r; otherwise each lane keeps the 4 RT elements
-    // its MFMA accumulators hold (r = c, b = 4 g + e).
+    // Output elements (tile t, batch tile j, batch row b of the tile, row r -> y[TR j + b][nbase + TR t + r]).
+    // Through LDS (NWK > 1 or KS > 1): thread threadIdx.x + 64 NWK i takes element TE (BT t + j) + TR b + r;
+    // otherwise each lane keeps the 4 RT BT elements its MFMA accumulators hold (r = c, b = 4 g + e).
     constexpr bool VIA_LDS = NWK > 1 || KS > 1;
     constexpr int TE = TR * TR;
-    constexpr int EL = VIA_LDS ? (RT * TE + 64 * NWK - 1) / (64 * NWK) : 4 * RT;
+    constexpr int EL = VIA_LDS ? (RT * BT * TE + 64 * NWK - 1) / (64 * NWK) : 4 * RT * BT;
     struct Coord {
-        int t, b, r;
+        int t, j, b, r;
     };
     auto coord = [&](int i) -> Coord {
         if constexpr (VIA_LDS) {
             const int idx = (int)threadIdx.x + i * 64 * NWK;
-            return {idx / TE, (idx % TE) / TR, idx % TR};
+            return {idx / (BT * TE), (idx / TE) % BT, (idx % TE) / TR, idx % TR};
         } else {
-            return {i >> 2, 4 * g + (i & 3), c};
+            return {i / (4 * BT), (i >> 2) % BT, 4 * g + (i & 3), c};
         }
     };
     // the epilogue's operands (scales, residual values) are read before the weight stream starts, so their
@@ -363,17 +366,20 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
     for (int i = 0; i < EL; ++i) {
         const Coord e = coord(i);
         const int n = min(nbase + TR * e.t + e.r, N - 1);  // rows past N are never stored
+        const int bb = TR * e.j + e.b;
         sg[i] = scale ? scale[n] : 1.f;
         su[i] = (EPI == EPI_SWIGLU && scale) ? scale[S + n] : 1.f;
-        hr[i] = (EPI == EPI_RESIDUAL && e.t < RT && e.b < B) ? y[(size_t)e.b * N + n] : 0u;
+        hr[i] = (EPI == EPI_RESIDUAL && e.t < RT && bb < B) ? y[(size_t)bb * N + n] : 0u;
     }
 
-    v4f acc[NT];
+    v4f acc[NT][BT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < BT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
     for (int b0 = kb0; b0 < kb0 + P; b0 += KB) {
-        v4i wv[KB][NT][WL], xv[KB][4];
+        v4i wv[KB][NT][WL], xv[KB][BT][4];
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
             const int b = b0 + u;  // block of part 0; part s reads block b + s P
@@ -399,7 +405,9 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const bool in = step && bx < kb1 && bx * 128 + 32 * p < K;
-                xv[u][p] = buf_ld16(xr, xoff + (in ? bx * 256 + 64 * p : OOR));
+#pragma unroll
+                for (int j = 0; j < BT; ++j)
+                    xv[u][j][p] = buf_ld16(xr, xoff + (in ? j * TR * K * 2u + bx * 256 + 64 * p : OOR));
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // every load of the stage is in flight before the first wait
@@ -410,16 +418,18 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
                 // (k = 32 g + 8 m). A 4 x 4 transpose over (register, 16-lane row): swap the upper 32 lanes of
                 // registers 0, 1 with the lower 32 lanes of 2, 3, then the odd rows of 0, 2 with the even rows of 1, 3.
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const auto s02 = __builtin_amdgcn_permlane32_swap(xv[u][0][d], xv[u][2][d], false, false);
-                    const auto s13 = __builtin_amdgcn_permlane32_swap(xv[u][1][d], xv[u][3][d], false, false);
-                    const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
-                    const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
-                    xv[u][0][d] = s01[0];
-                    xv[u][1][d] = s01[1];
-                    xv[u][2][d] = s23[0];
-                    xv[u][3][d] = s23[1];
-                }
+                for (int j = 0; j < BT; ++j)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const auto s02 = __builtin_amdgcn_permlane32_swap(xv[u][j][0][d], xv[u][j][2][d], false, false);
+                        const auto s13 = __builtin_amdgcn_permlane32_swap(xv[u][j][1][d], xv[u][j][3][d], false, false);
+                        const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+                        const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+                        xv[u][j][0][d] = s01[0];
+                        xv[u][j][1][d] = s01[1];
+                        xv[u][j][2][d] = s23[0];
+                        xv[u][j][3][d] = s23[1];
+                    }
             }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -443,7 +453,10 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
                         wb = i8x8_to_bf16(q[m >> 1][2 * (m & 1)], q[m >> 1][2 * (m & 1) + 1]);
                     else
                         wb = as_bf16x8(wv[u][t][m]);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[u][m]), wb, acc[t], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < BT; ++j)
+                        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[u][j][m]), wb, acc[t][j], 0,
+                                                                            0, 0);
                 }
             }
         }
@@ -451,10 +464,10 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
 
     auto store = [&](int i, float a, float u) {
         const Coord e = coord(i);
-        const int n = nbase + TR * e.t + e.r;
-        if (e.t >= RT || n >= N || e.b >= B) return;
+        const int n = nbase + TR * e.t + e.r, bb = TR * e.j + e.b;
+        if (e.t >= RT || n >= N || bb >= B) return;
         const float av = scale ? a * sg[i] : a;
-        uint16_t *yp = y + (size_t)e.b * N + n;
+        uint16_t *yp = y + (size_t)bb * N + n;
         if (EPI == EPI_NONE) {
             *yp = (uint16_t)f2bf(av);
         } else if (EPI == EPI_RESIDUAL) {
@@ -465,15 +478,18 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
         }
     };
     if constexpr (VIA_LDS) {
-        // wavefront w's tile t: D[i][c] at 4 (c + 16 (i / 4)) + i % 4 (lane c + 16 (i / 4), element i % 4)
-        __shared__ __attribute__((aligned(16))) float red[NWK][NT][256];
+        // wavefront w's tile t, batch tile j: D[i][c] at 4 (c + 16 (i / 4)) + i % 4 (lane c + 16 (i / 4), element
+        // i % 4)
+        __shared__ __attribute__((aligned(16))) float red[NWK][NT][BT][256];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) *reinterpret_cast<v4f *>(&red[wave][t][4 * lane]) = acc[t];
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int j = 0; j < BT; ++j) *reinterpret_cast<v4f *>(&red[wave][t][j][4 * lane]) = acc[t][j];
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < EL; ++i) {
             const Coord e = coord(i);
-            if (e.t >= RT || nbase + TR * e.t + e.r >= N || e.b >= B) continue;
+            if (e.t >= RT || nbase + TR * e.t + e.r >= N || TR * e.j + e.b >= B) continue;
             float a = 0.f, u = 0.f;  // summed over wavefronts, then parts, in that fixed order
 #pragma unroll
             for (int w = 0; w < NWK; ++w)
@@ -481,7 +497,8 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
                 for (int s = 0; s < KS; ++s) {
                     const int ii = TR * s + e.b, cc = TR * s + e.r;
                     const int at = 4 * (cc + 16 * (ii >> 2)) + (ii & 3);
-                    const float va = red[w][e.t][at], vu = EPI == EPI_SWIGLU ? red[w][NT - RT + e.t][at] : 0.f;
+                    const float va = red[w][e.t][e.j][at];
+                    const float vu = EPI == EPI_SWIGLU ? red[w][NT - RT + e.t][e.j][at] : 0.f;
                     a = (w == 0 && s == 0) ? va : a + va;
                     u = (w == 0 && s == 0) ? vu : u + vu;
                 }
@@ -489,7 +506,10 @@ __global__ __launch_bounds__(64 * NWK) void gemv_mfma_kernel(const WT *__restric
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < EL; ++i) store(i, acc[i >> 2][i & 3], acc[NT - RT + (i >> 2)][i & 3]);
+        for (int i = 0; i < EL; ++i) {
+            const int t = i / (4 * BT), j = (i >> 2) % BT;
+            store(i, acc[t][j][i & 3], acc[NT - RT + t][j][i & 3]);
+        }
     }
 }
 
@@ -551,59 +571,107 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 
 // Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
 // [2 S, K] matrix) then split K alike, which keeps the fused epilogues bit-identical:
-//   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows (256+ workgroups instead of 128);
-//   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2, RT = 4 above 8 batch rows
-//   for 32768+ rows without SwiGLU (the lm_head);
-//   NWK (at most 16) from the 128-k blocks per wavefront: 2 when RT = 2, 4 when KS = RT = 1, 8 when KS = 2
-//   (at least 4 wavefronts). Measured on MI355X over the LFM2 decode shapes at batches 4, 8 and 16.
-// LFM2Q_GEMV_MFMA = "KS,RT,NWK" overrides the shape (read on every call; the last bits of the sums change with it).
-template <typename WT, int EPI, int KS, int RT>
+//   BT (batch tiles per wavefront, sharing every weight load): 16-row batch tiles, BT = 1, 2 or 4 for up to 16, 32
+//   or 64 batch rows;
+//   KS = 2 (8-row tiles, 256+ workgroups instead of 128) for at most 2048 weight rows: batch tiles of 8 rows, BT = 1
+//   up to batch 8 and 2 up to batch 16;
+//   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2, RT = 4 for 32768+ rows above
+//   8 batch rows with one batch tile and no SwiGLU (the lm_head), RT = 1 with SwiGLU and four batch tiles
+//   (registers);
+//   NWK (at most 16, at most 16 / BT with several batch tiles: LDS) from the 128-k blocks per wavefront: 2 when
+//   RT = 2, 4 when KS = RT = 1, 8 when KS = 2 (at least 4 wavefronts). Measured on MI355X over the LFM2 decode
+//   shapes at batches 4 to 64.
+// LFM2Q_GEMV_MFMA = "KS,RT,NWK[,BT]" overrides the shape (read on every call; the last bits of the sums change with
+// it).
+template <typename WT, int EPI, int KS, int RT, int BT>
 void launch_mfma_shape(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int N, int K, int S,
                        int nwk, hipStream_t st) {
     const dim3 grid((N + (16 / KS) * RT - 1) / ((16 / KS) * RT));
 #define LFM2Q_MF(NWK_) \
-    gemv_mfma_kernel<WT, KS, RT, NWK_, EPI><<<grid, 64 * NWK_, 0, st>>>(W, scale, x, y, B, N, K, S)
-    switch (nwk) {
-        case 16: LFM2Q_MF(16); break;
-        case 8: LFM2Q_MF(8); break;
-        case 4: LFM2Q_MF(4); break;
-        case 2: LFM2Q_MF(2); break;
-        default: LFM2Q_MF(1); break;
-    }
+    gemv_mfma_kernel<WT, KS, RT, NWK_, EPI, BT><<<grid, 64 * NWK_, 0, st>>>(W, scale, x, y, B, N, K, S)
+    constexpr int NWK_MAX = 16 / BT;  // LDS: NWK NT BT KiB of partial tiles with NT <= 4
+    if constexpr (NWK_MAX >= 16)
+        if (nwk >= 16) {
+            LFM2Q_MF(16);
+            return;
+        }
+    if constexpr (NWK_MAX >= 8)
+        if (nwk >= 8) {
+            LFM2Q_MF(8);
+            return;
+        }
+    if (nwk >= 4)
+        LFM2Q_MF(4);
+    else if (nwk >= 2)
+        LFM2Q_MF(2);
+    else
+        LFM2Q_MF(1);
 #undef LFM2Q_MF
+}
+
+struct MfmaShape {
+    int ks, rt, nwk, bt;
+};
+
+// B <= 64 (B <= 16 at KS = 2)
+inline MfmaShape mfma_shape(int epi, long wrows, int B, int K) {
+    const int nblk = (K + 127) / 128;
+    MfmaShape m;
+    m.ks = (B <= 16 && wrows <= 2048) ? 2 : 1;
+    m.bt = m.ks == 2 ? (B <= 8 ? 1 : 2) : (B <= 16 ? 1 : B <= 32 ? 2 : 4);
+    m.rt = (m.ks == 1 && wrows >= 6144) ? 2 : 1;
+    if (epi != EPI_SWIGLU && B > 8 && m.bt == 1 && wrows >= 32768) m.rt = 4;  // halves the activation reads again
+    if (epi == EPI_SWIGLU && m.bt == 4) m.rt = 1;
+    const int bpw = m.ks == 2 ? 8 : m.rt >= 2 ? 2 : 4;  // target blocks per wavefront
+    m.nwk = 1;
+    while (m.nwk < 16 && (nblk >= bpw * 2 * m.nwk || (m.ks == 2 && m.nwk < 4))) m.nwk *= 2;
+    m.nwk = std::min(m.nwk, 16 / m.bt);
+    int fk = 0, fr = 0, fn = 0, fb = 1;
+    if (const char *e = getenv("LFM2Q_GEMV_MFMA")) {
+        const int got = sscanf(e, "%d,%d,%d,%d", &fk, &fr, &fn, &fb);
+        const bool bt_ok = (fb == 1 || fb == 2 || (fb == 4 && fk == 1)) && B <= (16 / fk) * fb;
+        const bool rt_ok = fr == 1 || (fr == 2 && fk == 1 && !(fb == 4 && epi == EPI_SWIGLU)) ||
+                           (fr == 4 && fk == 1 && fb == 1 && epi != EPI_SWIGLU);
+        if (got >= 3 && (fk == 1 || (fk == 2 && fr == 1)) && bt_ok && rt_ok &&
+            (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16) && fn <= 16 / fb)
+            m = MfmaShape{fk, fr, fn, fb};
+    }
+    return m;
 }
 
 template <typename WT, int EPI>
 void launch_mfma(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int N, int K, int S,
                  hipStream_t st) {
-    const long wrows = EPI == EPI_SWIGLU ? 2L * S : N;
-    const int nblk = (K + 127) / 128;
-    int ks = (B <= 8 && wrows <= 2048) ? 2 : 1;
-    int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
-    if (EPI != EPI_SWIGLU && B > 8 && wrows >= 32768) rt = 4;  // halves the activation reads per weight byte again
-    const int bpw = ks == 2 ? 8 : rt >= 2 ? 2 : 4;  // target blocks per wavefront
-    int nwk = 1;
-    while (nwk < 16 && (nblk >= bpw * 2 * nwk || (ks == 2 && nwk < 4))) nwk *= 2;
-    int fk = 0, fr = 0, fn = 0;
-    if (const char *e = getenv("LFM2Q_GEMV_MFMA"))
-        if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
-            (fr == 1 || fr == 2 || (fr == 4 && fk == 1 && EPI != EPI_SWIGLU)) &&
-            (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
-            ks = fk;
-            rt = fr;
-            nwk = fn;
-        }
-    if (ks == 2)
-        launch_mfma_shape<WT, EPI, 2, 1>(W, scale, x, y, B, N, K, S, nwk, st);
-    else if (EPI != EPI_SWIGLU && rt == 4)
-        launch_mfma_shape<WT, EPI, 1, EPI == EPI_SWIGLU ? 1 : 4>(W, scale, x, y, B, N, K, S, nwk, st);
-    else if (rt == 2)
-        launch_mfma_shape<WT, EPI, 1, 2>(W, scale, x, y, B, N, K, S, nwk, st);
-    else
-        launch_mfma_shape<WT, EPI, 1, 1>(W, scale, x, y, B, N, K, S, nwk, st);
+    const MfmaShape m = mfma_shape(EPI, EPI == EPI_SWIGLU ? 2L * S : N, B, K);
+    auto go = [&](auto ks, auto rt, auto bt) {
+        launch_mfma_shape<WT, EPI, decltype(ks)::value, decltype(rt)::value, decltype(bt)::value>(W, scale, x, y, B,
+                                                                                                   N, K, S, m.nwk, st);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    if (m.ks == 2) {
+        if (m.bt == 2) go(I2{}, I1{}, I2{});
+        else go(I2{}, I1{}, I1{});
+    } else if (m.bt == 4) {
+        if constexpr (EPI != EPI_SWIGLU)
+            if (m.rt == 2) return go(I1{}, I2{}, I4{});
+        go(I1{}, I1{}, I4{});
+    } else if (m.bt == 2) {
+        if (m.rt == 2) go(I1{}, I2{}, I2{});
+        else go(I1{}, I1{}, I2{});
+    } else if (m.rt == 4) {
+        if constexpr (EPI != EPI_SWIGLU) go(I1{}, I4{}, I1{});
+    } else if (m.rt == 2) {
+        go(I1{}, I2{}, I1{});
+    } else {
+        go(I1{}, I1{}, I1{});
+    }
 }
 
-// y: [B, Nout] (Nout = S for SwiGLU). Batches above 16 run as consecutive chunks of at most 16 rows.
+// y: [B, Nout] (Nout = S for SwiGLU). Batches run as consecutive chunks of at most 64 rows (16 when the activations
+// of 64 rows reach 1 GiB, or with LFM2Q_GEMV_CHUNK=16, read on every call); a chunk of one row takes the batch-1
+// kernels.
 template <typename WT, int EPI>
 int gemv_run(const char *name, const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int Nout,
              int K, int rows, hipStream_t st) {
@@ -615,8 +683,12 @@ int gemv_run(const char *name, const WT *W, const float *scale, const uint16_t *
     LFM2Q_REQUIRE(K <= (1 << 24), LFM2Q_ERR_SHAPE, "%s: K above 16777216 (K=%d)", name, K);
     LFM2Q_REQUIRE(aligned16(W) && aligned16(x), LFM2Q_ERR_ALIGN, "%s: W and x must be 16-byte aligned", name);
     const int S = Nout;  // SwiGLU: w3 rows start at S
-    for (int b0 = 0; b0 < B; b0 += 16) {
-        const int bs = B - b0 < 16 ? B - b0 : 16;
+    // the activation resource of a chunk must stay below the out-of-range offset (1 GiB) the kernel uses
+    int chunk = 64L * K * 2 < (1L << 30) ? 64 : 16;
+    if (const char *e = getenv("LFM2Q_GEMV_CHUNK"))
+        if (atoi(e) == 16) chunk = 16;
+    for (int b0 = 0; b0 < B; b0 += chunk) {
+        const int bs = B - b0 < chunk ? B - b0 : chunk;
         const uint16_t *xb = x + (size_t)b0 * K;
         uint16_t *yb = y + (size_t)b0 * Nout;
         if (bs == 1)

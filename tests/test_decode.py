@@ -24,18 +24,21 @@ def test_quantized_gemv_up_to_16(fmt, shape, B):
 
 
 def test_int8_above_16():
-    # wide weights: W8A16 whether or not a BF16 copy is kept
-    for shape in (W13, HEAD):
-        for B in (17, 24, 64, 128):
-            assert linear_path("int8", "int8", B, *shape, True) == "w8a16"
-            assert linear_path("int8", "int8", B, *shape, False) == "w8a16"
-    # narrow weights: the BF16 copy when kept
-    for shape in (QKV, IN, W2, OUT):
-        assert linear_path("int8", "int8", 17, *shape, True) == "linear"
-        assert linear_path("int8", "int8", 300, *shape, True) == "linear"
-    # narrow weights without a copy: the GEMV up to 32 rows (64 at K = 8192), W8A16 beyond
-    assert [linear_path("int8", "int8", B, *QKV, False) for B in (17, 32, 33, 64)] == ["gemv", "gemv", "w8a16", "w8a16"]
-    assert [linear_path("int8", "int8", B, *W2, False) for B in (17, 64, 65, 128)] == ["gemv", "gemv", "w8a16", "w8a16"]
+    # the lm_head: W8A16 whether or not a BF16 copy is kept
+    for B in (17, 24, 64, 128):
+        assert linear_path("int8", "int8", B, *HEAD, True) == "w8a16"
+        assert linear_path("int8", "int8", B, *HEAD, False) == "w8a16"
+    # w1|w3-sized: the GEMV up to 32 rows, then W8A16
+    for kept in (True, False):
+        assert [linear_path("int8", "int8", B, *W13, kept) for B in (17, 32, 33, 64)] == \
+            ["gemv", "gemv", "w8a16", "w8a16"]
+    # narrow: the GEMV; a kept BF16 copy at K = 8192 and above 32 rows; W8A16 above 64 rows without a copy
+    assert [linear_path("int8", "int8", B, *QKV, True) for B in (17, 32, 33, 300)] == \
+        ["gemv", "gemv", "linear", "linear"]
+    assert [linear_path("int8", "int8", B, *QKV, False) for B in (17, 64, 65)] == ["gemv", "gemv", "w8a16"]
+    assert [linear_path("int8", "int8", B, *W2, True) for B in (17, 64)] == ["linear", "linear"]
+    assert [linear_path("int8", "int8", B, *W2, False) for B in (17, 64, 65, 128)] == \
+        ["gemv", "gemv", "w8a16", "w8a16"]
 
 
 def test_int4_above_16():
@@ -48,7 +51,7 @@ def test_int4_above_16():
 def test_int8_weights_in_int4_mode():
     """w4_keep_int8 kinds are stored in INT8 under mode "int4" and follow the INT8 rules."""
     assert linear_path("int4", "int8", 24, *HEAD, True) == "w8a16"
-    assert linear_path("int4", "int8", 24, *QKV, True) == "linear"
+    assert linear_path("int4", "int8", 40, *QKV, True) == "linear"
 
 
 def test_bf16_weights():

@@ -17,8 +17,10 @@ from gpu_util import assert_close_bf16, dev_bf16, host_bits
 
 pytestmark = pytest.mark.gpu
 
-# (N, K): narrow, the stacked w1|w3, K = 8192 (the w2 rule) and 8192 output rows (the W8A16 rule)
-SHAPES = {("qkv", 0): (384, 512), ("w13", 0): (640, 512), ("w2", 0): (128, 8192), ("head", 0): (8192, 256)}
+# (N, K): narrow, the stacked w1|w3, K = 8192 (the w2 rule), 8192 rows (the w1|w3-sized rule) and 32768 rows (the
+# lm_head rule)
+SHAPES = {("qkv", 0): (384, 512), ("w13", 0): (640, 512), ("w2", 0): (128, 8192), ("w13", 1): (8192, 256),
+          ("head", 0): (32768, 256)}
 
 
 @pytest.fixture(scope="module")
@@ -97,9 +99,10 @@ def test_linear_drop_bf16(weights):
     D = make(weights, "int8", drop_bf16=True)
     assert not D.lin_bf16
     paths = {(key, B): check_linear(D, key, B, B + 3) for key in SHAPES for B in (24, 40, 72)}
-    assert paths[(("qkv", 0), 24)] == "gemv" and paths[(("qkv", 0), 40)] == "w8a16"
+    assert paths[(("qkv", 0), 40)] == "gemv" and paths[(("qkv", 0), 72)] == "w8a16"
     assert paths[(("w2", 0), 40)] == "gemv" and paths[(("w2", 0), 72)] == "w8a16"
     assert paths[(("head", 0), 24)] == "w8a16"
+    assert paths[(("w13", 1), 24)] == "gemv" and paths[(("w13", 1), 40)] == "w8a16"
 
 
 def test_keep_int8_kinds(weights):

@@ -89,7 +89,7 @@ def _gen(seed, B, N, K):
     return W, scale, x
 
 
-@pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 17])
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 12, 16, 17, 24, 40, 64, 65])
 @pytest.mark.parametrize("N,K", [(3072, 2048), (2048, 8192), (200, 1152), (96, 576), (40, 64)])
 def test_gemv_w8_vs_oracle(E, B, N, K):
     W, scale, x = _gen(100 + B, B, N, K)
@@ -99,15 +99,29 @@ def test_gemv_w8_vs_oracle(E, B, N, K):
     assert_close_bf16(host_bits(y), ref, what=f"gemv int8 B={B} [{N}x{K}]")
 
 
-@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,8", "1,2,1", "1,4,8", "1,4,1", "2,1,1", "2,1,2", "2,1,16"])
+MFMA_SHAPES = ["1,1,1", "1,1,4", "1,2,8", "1,2,1", "1,4,8", "1,4,1", "2,1,1", "2,1,2", "2,1,16",
+               "2,1,1,2", "2,1,8,2", "1,1,1,2", "1,1,8,2", "1,2,2,2", "1,2,8,2", "1,1,1,4", "1,1,4,4", "1,2,2,4"]
+
+
+def _launch_batches(shape):
+    """Two batch sizes the forced shape accepts (KS = 2 takes 8 rows per batch tile, KS = 1 16)."""
+    ks, bt = int(shape.split(",")[0]), int((shape.split(",") + ["1"])[3])
+    if bt == 1:
+        return (3, 8) if ks == 2 else (3, 13)
+    top = (16 // ks) * bt
+    return top // 2 + 3, top
+
+
+@pytest.mark.parametrize("shape", MFMA_SHAPES)
 @pytest.mark.parametrize("wt", ["int8", "bf16"])
 def test_gemv_mfma_launch_shapes(E, monkeypatch, shape, wt):
-    """Every batch-2..16 launch shape (k-parts KS, row tiles RT, wavefronts NWK, forced through LFM2Q_GEMV_MFMA)
-    against the oracle, with a trailing half block (K = 1088) and N not a multiple of the tile rows."""
+    """Every matrix-core launch shape (k-parts KS, row tiles RT, wavefronts NWK, batch tiles BT, forced through
+    LFM2Q_GEMV_MFMA) against the oracle, with a trailing half block (K = 1088), N not a multiple of the tile rows and
+    a partial last batch tile; the residual epilogue bit-identical to the plain GEMV + add."""
     monkeypatch.setenv("LFM2Q_GEMV_MFMA", shape)
     N, K = 300, 1088
     g = torch.Generator().manual_seed(len(shape))
-    for B in (3, 8) if shape.startswith("2") else (3, 13):
+    for B in _launch_batches(shape):
         if wt == "int8":
             W, scale, x = _gen(B, B, N, K)
             ref = oracle.gemv(W.numpy(), scale.numpy(), host_bits(x))
@@ -156,7 +170,7 @@ def test_gemv_w8_decode_shapes(E, N, K, B):
     assert_close_bf16(host_bits(y[:, rows.cuda()]), ro, what=f"gemv int8 B={B} [{N}x{K}] sampled rows vs oracle")
 
 
-@pytest.mark.parametrize("B", [1, 3, 16])
+@pytest.mark.parametrize("B", [1, 3, 16, 20, 64])
 @pytest.mark.parametrize("N,K", [(1040, 1024), (72, 576)])
 def test_gemv_bf16_vs_oracle(E, B, N, K):
     g = torch.Generator().manual_seed(B)
@@ -169,7 +183,7 @@ def test_gemv_bf16_vs_oracle(E, B, N, K):
 
 
 # ------------------------------------------------------------------------------------------------ fused epilogues
-@pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 19])
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 19, 40, 64])
 @pytest.mark.parametrize("wt", ["int8", "bf16"])
 def test_swiglu_bit_identical_to_gemv_then_silu_mul(E, B, wt):
     """gemv_epi(0) == gemv + silu_mul bit for bit (tests/test_kernels.py:153-186), at the w1|w3 shape."""
@@ -191,7 +205,7 @@ def test_swiglu_bit_identical_to_gemv_then_silu_mul(E, B, wt):
     assert torch.equal(out, ref), (out.float() - ref.float()).abs().max()
 
 
-@pytest.mark.parametrize("B", [1, 4, 8, 16])
+@pytest.mark.parametrize("B", [1, 4, 8, 12, 16, 24, 64])
 def test_residual_bit_identical_to_gemv_then_add(E, B):
     N, K = 2048, 8192
     g = torch.Generator(device="cuda").manual_seed(B)
