@@ -576,11 +576,10 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 //   KS = 2 (8-row tiles, 256+ workgroups instead of 128) for at most 2048 weight rows: batch tiles of 8 rows, BT = 1
 //   up to batch 8 and 2 up to batch 16;
 //   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2, RT = 4 for 32768+ rows above
-//   8 batch rows with one batch tile and no SwiGLU (the lm_head), RT = 1 with SwiGLU and four batch tiles
-//   (registers);
-//   NWK (at most 16, at most 16 / BT with several batch tiles: LDS) from the 128-k blocks per wavefront: 2 when
-//   RT = 2, 4 when KS = RT = 1, 8 when KS = 2 (at least 4 wavefronts). Measured on MI355X over the LFM2 decode
-//   shapes at batches 4 to 64.
+//   8 batch rows without SwiGLU (the lm_head);
+//   NWK from the 128-k blocks per wavefront: 2 when RT = 2 or BT > 1, 4 when KS = RT = BT = 1, 8 when KS = 2 (at
+//   least 4 wavefronts); at most 16 / BT (LDS), 8 / BT for 32768+ rows with several batch tiles. Measured on MI355X
+//   over the LFM2 decode shapes at batches 4 to 64.
 // LFM2Q_GEMV_MFMA = "KS,RT,NWK[,BT]" overrides the shape (read on every call; the last bits of the sums change with
 // it).
 template <typename WT, int EPI, int KS, int RT, int BT>
@@ -620,18 +619,17 @@ inline MfmaShape mfma_shape(int epi, long wrows, int B, int K) {
     m.ks = (B <= 16 && wrows <= 2048) ? 2 : 1;
     m.bt = m.ks == 2 ? (B <= 8 ? 1 : 2) : (B <= 16 ? 1 : B <= 32 ? 2 : 4);
     m.rt = (m.ks == 1 && wrows >= 6144) ? 2 : 1;
-    if (epi != EPI_SWIGLU && B > 8 && m.bt == 1 && wrows >= 32768) m.rt = 4;  // halves the activation reads again
-    if (epi == EPI_SWIGLU && m.bt == 4) m.rt = 1;
-    const int bpw = m.ks == 2 ? 8 : m.rt >= 2 ? 2 : 4;  // target blocks per wavefront
+    const bool head = B > 8 && wrows >= 32768;
+    if (epi != EPI_SWIGLU && head) m.rt = 4;  // halves the activation reads per weight byte again
+    const int bpw = m.ks == 2 ? 8 : (m.rt >= 2 || m.bt > 1) ? 2 : 4;  // target blocks per wavefront
     m.nwk = 1;
     while (m.nwk < 16 && (nblk >= bpw * 2 * m.nwk || (m.ks == 2 && m.nwk < 4))) m.nwk *= 2;
-    m.nwk = std::min(m.nwk, 16 / m.bt);
+    m.nwk = std::min(m.nwk, (head && m.bt > 1 ? 8 : 16) / m.bt);
     int fk = 0, fr = 0, fn = 0, fb = 1;
     if (const char *e = getenv("LFM2Q_GEMV_MFMA")) {
         const int got = sscanf(e, "%d,%d,%d,%d", &fk, &fr, &fn, &fb);
         const bool bt_ok = (fb == 1 || fb == 2 || (fb == 4 && fk == 1)) && B <= (16 / fk) * fb;
-        const bool rt_ok = fr == 1 || (fr == 2 && fk == 1 && !(fb == 4 && epi == EPI_SWIGLU)) ||
-                           (fr == 4 && fk == 1 && fb == 1 && epi != EPI_SWIGLU);
+        const bool rt_ok = fr == 1 || (fr == 2 && fk == 1) || (fr == 4 && fk == 1 && epi != EPI_SWIGLU);
         if (got >= 3 && (fk == 1 || (fk == 2 && fr == 1)) && bt_ok && rt_ok &&
             (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16) && fn <= 16 / fb)
             m = MfmaShape{fk, fr, fn, fb};
@@ -650,22 +648,25 @@ void launch_mfma(const WT *W, const float *scale, const uint16_t *x, uint16_t *y
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I4 = std::integral_constant<int, 4>;
+    auto with_bt = [&](auto ks, auto rt) {
+        if (m.bt == 4)
+            go(ks, rt, I4{});
+        else if (m.bt == 2)
+            go(ks, rt, I2{});
+        else
+            go(ks, rt, I1{});
+    };
     if (m.ks == 2) {
-        if (m.bt == 2) go(I2{}, I1{}, I2{});
-        else go(I2{}, I1{}, I1{});
-    } else if (m.bt == 4) {
-        if constexpr (EPI != EPI_SWIGLU)
-            if (m.rt == 2) return go(I1{}, I2{}, I4{});
-        go(I1{}, I1{}, I4{});
-    } else if (m.bt == 2) {
-        if (m.rt == 2) go(I1{}, I2{}, I2{});
-        else go(I1{}, I1{}, I2{});
+        if (m.bt == 2)
+            go(I2{}, I1{}, I2{});
+        else
+            go(I2{}, I1{}, I1{});
     } else if (m.rt == 4) {
-        if constexpr (EPI != EPI_SWIGLU) go(I1{}, I4{}, I1{});
+        if constexpr (EPI != EPI_SWIGLU) with_bt(I1{}, I4{});
     } else if (m.rt == 2) {
-        go(I1{}, I2{}, I1{});
+        with_bt(I1{}, I2{});
     } else {
-        go(I1{}, I1{}, I1{});
+        with_bt(I1{}, I1{});
     }
 }
 

@@ -100,7 +100,8 @@ def test_gemv_w8_vs_oracle(E, B, N, K):
 
 
 MFMA_SHAPES = ["1,1,1", "1,1,4", "1,2,8", "1,2,1", "1,4,8", "1,4,1", "2,1,1", "2,1,2", "2,1,16",
-               "2,1,1,2", "2,1,8,2", "1,1,1,2", "1,1,8,2", "1,2,2,2", "1,2,8,2", "1,1,1,4", "1,1,4,4", "1,2,2,4"]
+               "2,1,1,2", "2,1,8,2", "1,1,1,2", "1,1,8,2", "1,2,2,2", "1,2,8,2", "1,4,1,2", "1,4,8,2", "1,1,1,4",
+               "1,1,4,4", "1,2,2,4", "1,4,1,4", "1,4,4,4"]
 
 
 def _launch_batches(shape):
