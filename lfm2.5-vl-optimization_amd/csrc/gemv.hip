@@ -6,12 +6,13 @@
 //                     of each row with non-temporal loads (a wavefront load = 1 KiB contiguous of one row), all of
 //                     a lane's chunks are in flight before the first FMA. int8 -> fp32 is one SDWA convert per
 //                     weight; the row sums of a wavefront's rows are reduced together (fold_sum). No LDS.
-//   gemv_mfma_kernel  batch 2..16. A workgroup owns RT tiles of 16 output rows (8 when the K run is split in two
-//                     inside the MFMA, batches <= 8); its NWK wavefronts split K into 128-k blocks. A tile block is
-//                     read by two wave loads of 8 whole 128-byte lines; the weights are converted exactly to bf16 in
-//                     registers and feed v_mfma_f32_16x16x32_bf16 with the activations as the A operand (batch rows
-//                     x 32 k) and the weights as B (32 k x output rows). The partial tiles meet in LDS. The matrix
-//                     cores take the batch FMAs off the VALU (about 1.5 VALU ops per weight at any batch).
+//   gemv_mfma_kernel  batch 2..64. A workgroup owns RT tiles of 16 output rows (8 when the K run is split in two
+//                     inside the MFMA, batches <= 16) and BT batch tiles of 16 (8) rows that share every weight
+//                     load; its NWK wavefronts split K into 128-k blocks. A tile block is read by two wave loads of
+//                     8 whole 128-byte lines; the weights are converted exactly to bf16 in registers and feed
+//                     v_mfma_f32_16x16x32_bf16 with the activations as the A operand (batch rows x 32 k) and the
+//                     weights as B (32 k x output rows). The partial tiles meet in LDS. The matrix cores take the
+//                     batch FMAs off the VALU (about 1.5 VALU ops per weight at any batch).
 // The per-row accumulation order of each kernel does not depend on which epilogue runs or on how many rows a
 // wavefront owns, so the fused epilogues are bit-identical to the plain GEMV followed by the separate op.
 //
@@ -577,7 +578,7 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 //   up to batch 8 and 2 up to batch 16;
 //   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2, RT = 4 for 32768+ rows above
 //   8 batch rows without SwiGLU (the lm_head);
-//   NWK from the 128-k blocks per wavefront: 2 when RT = 2 or BT > 1, 4 when KS = RT = BT = 1, 8 when KS = 2 (at
+//   NWK from the 128-k blocks per wavefront: 2 when RT = 2 or BT > 1, 4 when KS = RT = BT = 1, 8 BT when KS = 2 (at
 //   least 4 wavefronts); at most 16 / BT (LDS), 8 / BT for 32768+ rows with several batch tiles. Measured on MI355X
 //   over the LFM2 decode shapes at batches 4 to 64.
 // LFM2Q_GEMV_MFMA = "KS,RT,NWK[,BT]" overrides the shape (read on every call; the last bits of the sums change with
@@ -621,7 +622,7 @@ inline MfmaShape mfma_shape(int epi, long wrows, int B, int K) {
     m.rt = (m.ks == 1 && wrows >= 6144) ? 2 : 1;
     const bool head = B > 8 && wrows >= 32768;
     if (epi != EPI_SWIGLU && head) m.rt = 4;  // halves the activation reads per weight byte again
-    const int bpw = m.ks == 2 ? 8 : (m.rt >= 2 || m.bt > 1) ? 2 : 4;  // target blocks per wavefront
+    const int bpw = m.ks == 2 ? 8 * m.bt : (m.rt >= 2 || m.bt > 1) ? 2 : 4;  // target blocks per wavefront
     m.nwk = 1;
     while (m.nwk < 16 && (nblk >= bpw * 2 * m.nwk || (m.ks == 2 && m.nwk < 4))) m.nwk *= 2;
     m.nwk = std::min(m.nwk, (head && m.bt > 1 ? 8 : 16) / m.bt);
