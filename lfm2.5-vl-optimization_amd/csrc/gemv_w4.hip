@@ -52,24 +52,29 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ v2bf as_bf16x2(uint32_t v) { return __builtin_bit_cast(v2bf, v); }
 __device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
-// group scale and zero point of weight row `row`, group g
+// Group scale and zero point of weight row `row`, group g: scale_raw / zero_raw are the loaded words, decoded by
+// scale_of / zero_of where they are used, so that a load issued ahead of time is not waited for at its issue point
 template <int FMT>
 struct W4Fmt;
 template <>
 struct W4Fmt<0> {
-    __device__ static float scale(const void *S, const int32_t *, int row, int g, int G) {
-        return reinterpret_cast<const float *>(S)[(size_t)row * G + g];
+    __device__ static uint32_t scale_raw(const void *S, int row, int g, int G) {
+        return reinterpret_cast<const uint32_t *>(S)[(size_t)row * G + g];
     }
-    __device__ static int zero(const int32_t *, int, int, int) { return 8; }
+    __device__ static float scale_of(uint32_t r) { return __uint_as_float(r); }
+    __device__ static uint32_t zero_raw(const int32_t *, int, int, int) { return 0u; }
+    __device__ static int zero_of(uint32_t, int) { return 8; }
 };
 template <>
 struct W4Fmt<1> {
-    __device__ static float scale(const void *S, const int32_t *, int row, int g, int G) {
-        return h2f(reinterpret_cast<const uint16_t *>(S)[(size_t)row * G + g]);
+    __device__ static uint32_t scale_raw(const void *S, int row, int g, int G) {
+        return reinterpret_cast<const uint16_t *>(S)[(size_t)row * G + g];
     }
-    __device__ static int zero(const int32_t *Z, int row, int g, int G) {
-        return ((uint32_t)Z[(size_t)row * ((G + 7) >> 3) + (g >> 3)] >> (4 * (g & 7))) & 15;
+    __device__ static float scale_of(uint32_t r) { return h2f(r); }
+    __device__ static uint32_t zero_raw(const int32_t *Z, int row, int g, int G) {
+        return (uint32_t)Z[(size_t)row * ((G + 7) >> 3) + (g >> 3)];
     }
+    __device__ static int zero_of(uint32_t r, int g) { return (r >> (4 * (g & 7))) & 15; }
 };
 
 __device__ __forceinline__ float epi_value(int epi, float a, float b, uint32_t h) {
@@ -95,9 +100,10 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
     constexpr int NB = CPL * NROW <= 2 ? 4 : 2;
     const int lane = threadIdx.x & 63;
     const int nw = gridDim.x * 4;
-    const int G = K / group, C = K / 32;
+    const int G = K / group;
+    // A wavefront without rows (n >= N, the tail of the last workgroup) still takes its part of the shared activation
+    // repack below, then runs one round of empty rows (zero-range loads, no stores).
     int n = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    if (n >= N) return;  // no block-level synchronization in this kernel
 
     int gl[CPL];  // group of the lane's chunk u (clamped for chunks past K)
 #pragma unroll
@@ -105,8 +111,7 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
     const uint32_t rowb = (uint32_t)K / 2;
     struct Item {
         v4i w[CPL][NROW];
-        float s[CPL][NROW];
-        int z[CPL][NROW];
+        uint32_t s[CPL][NROW], z[CPL][NROW];  // raw scale and zero-point words
         uint32_t h;
     };
     auto load = [&](Item &it, int row) {
@@ -118,32 +123,47 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
 #pragma unroll
             for (int u = 0; u < CPL; ++u) {
                 it.w[u][i] = buf_ld16_nt(rr, (lane + 64 * u) * 16);
-                it.s[u][i] = F::scale(S, Z, wc, gl[u], G);
-                it.z[u][i] = F::zero(Z, wc, gl[u], G);
+                it.s[u][i] = F::scale_raw(S, wc, gl[u], G);
+                it.z[u][i] = F::zero_raw(Z, wc, gl[u], G);
             }
         }
         if (EPI == EPI_RESIDUAL) it.h = y[rc];
     };
-    // the first rows' weights are requested before the activations are repacked, so the two memory latencies
-    // overlap instead of adding up
+    // The activation pairs of chunk c = lane + 64 u are the same for every wavefront, so the workgroup converts them
+    // once: wavefront j converts piece j (8 activations) of every chunk into LDS, then each lane reads its chunks'
+    // 16 pairs and 4 piece sums back. xp[u][4 j + p] = (x[8 j + p], x[8 j + p + 4]), word-major. The activation
+    // loads go first and the first rows' weights right after them, so the repack waits only for the activations
+    // while the weights stay in flight.
+    __shared__ uint32_t xq[CPL][16][64];
+    __shared__ float xsq[CPL][4][64];
+    const int jx = threadIdx.x >> 6;
+    const rsrc_t xr = make_rsrc(x, (uint32_t)K * 2u);  // chunks past K read zeros (no branch around the loads)
+    v4i xd[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) xd[u] = buf_ld16(xr, (uint32_t)(lane + 64 * u) * 64u + 16u * jx);
     Item buf[NB];
 #pragma unroll
     for (int j = 0; j < NB - 1; ++j) load(buf[j], n + j * nw);
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t xp[CPL][16];  // activation pairs, word-major: xp[u][4 j + p] = (x[8 j + p], x[8 j + p + 4])
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) xq[u][4 * jx + p][lane] = xpair(xd[u], p);
+        float t = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t += bf2f_lo((uint32_t)xd[u][e]) + bf2f_hi((uint32_t)xd[u][e]);
+        xsq[u][jx][lane] = t;
+    }
+    // LDS writes done, then the workgroup barrier; a bare s_barrier, because __syncthreads()' fence would also wait
+    // for the weight loads in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    uint32_t xp[CPL][16];
     float xs[CPL];
 #pragma unroll
     for (int u = 0; u < CPL; ++u) {
-        const int c = lane + 64 * u;
-        xs[u] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const v4i d = c < C ? ld16(x + (size_t)c * 32 + 8 * j) : v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int p = 0; p < 4; ++p) xp[u][4 * j + p] = xpair(d, p);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) xs[u] += bf2f_lo((uint32_t)d[e]) + bf2f_hi((uint32_t)d[e]);
-        }
+        for (int q = 0; q < 16; ++q) xp[u][q] = xq[u][q][lane];
+        xs[u] = ((xsq[u][0][lane] + xsq[u][1][lane]) + xsq[u][2][lane]) + xsq[u][3][lane];
     }
     // a row's per-lane partial: sum_u s_u (dot_u - (128 + z_u) xs_u)
     auto partial = [&](const Item &it, int i) {
@@ -157,7 +177,7 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
                 for (int p = 0; p < 4; ++p)
                     d = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nm.pair((uint32_t)it.w[u][i][j], p)),
                                                         as_bf16x2(xp[u][4 * j + p]), d, false);
-            acc += it.s[u][i] * (d - (float)(128 + it.z[u][i]) * xs[u]);
+            acc += F::scale_of(it.s[u][i]) * (d - (float)(128 + F::zero_of(it.z[u][i], gl[u])) * xs[u]);
         }
         return acc;
     };
@@ -283,8 +303,7 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
 
     for (int b0 = kb0; b0 < kb0 + P; b0 += KB) {
         v4i wv[KB][NT][2], xv[KB][8];
-        float sc[KB][NT][2];
-        int zp[KB][NT][2];
+        uint32_t sc[KB][NT][2], zp[KB][NT][2];  // raw scale / zero-point words, decoded at their use
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
             const int b = b0 + u;  // block of part 0; part s reads block b + s P
@@ -305,8 +324,8 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
                 const int gi = min((bw * 256 + 128 * h) / group, G - 1);
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    sc[u][t][h] = F::scale(S, Z, srow[t], gi, G);
-                    zp[u][t][h] = F::zero(Z, srow[t], gi, G);
+                    sc[u][t][h] = F::scale_raw(S, srow[t], gi, G);
+                    zp[u][t][h] = F::zero_raw(Z, srow[t], gi, G);
                 }
             }
             const int bx = b + cpart * P;
@@ -367,9 +386,11 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
                         const v8bf bw4 = __builtin_bit_cast(v8bf, v4u{nm.pair(w, 0), nm.pair(w, 1), nm.pair(w, 2), nm.pair(w, 3)});
                         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[4 * h + j], bw4, d, 0, 0, 0);
                     }
-                    const float zc = (float)(128 + zp[u][t][h]);
+                    const int gi = min((min(b0 + u + cpart * P, nblk - 1) * 256 + 128 * h) / group, G - 1);
+                    const float zc = (float)(128 + F::zero_of(zp[u][t][h], gi));
+                    const float sv = F::scale_of(sc[u][t][h]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[t][e] += sc[u][t][h] * (d[e] - zc * dx[h][e]);
+                    for (int e = 0; e < 4; ++e) acc[t][e] += sv * (d[e] - zc * dx[h][e]);
                 }
             }
         }
