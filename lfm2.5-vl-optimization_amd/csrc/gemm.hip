@@ -292,8 +292,8 @@ __device__ __forceinline__ void epilogue(const ACC (&acc)[TN][TM], const float *
 // facc = fma((float)acc, sxT[kt, m], facc), in stage order -- the reference's fold, exact per group since |acc| <=
 // 64 * 127^2 < 2^24. The group's scales for the tile's rows travel with the operands (one 4-byte direct load per
 // wavefront per stage into a 1 KiB LDS slot) and are read after the stage's barrier. YsT: OUT_Q8 scales.
-template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES>
-__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_kernel(
+template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES, int KSP = 1>
+__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
     int sh, float *__restrict__ YsT = nullptr) {
@@ -304,18 +304,28 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     static_assert(IX >= 1 && IW >= 1 && TM >= 1 && TN >= 1, "tile too small");
     static_assert(4 * stage_bytes<TN>() <= NSTG * (BM + BN) * BK, "epilogue staging exceeds the LDS ring");
     static_assert(!out_q8(OUT) || (GRP && WNt % 64 == 0), "INT8 output needs grouped input and 64-column blocks");
+    // KSP > 1: KSP groups of 4 wavefronts split the K stages of one tile, each with its own operand ring; their
+    // int32 accumulators meet in LDS at the end (exact, so the result does not depend on KSP). Per-token only: the
+    // grouped path folds fp32 scales stage by stage, in order.
+    static_assert(KSP == 1 || (!GRP && !out_q8(OUT)), "split K needs the int32 accumulators of the per-token path");
+    static_assert(KSP == 1 || (KSP - 1) * BM * BN * 4 <= KSP * NSTG * (BM + BN) * BK, "partials exceed the rings");
     constexpr int RING = NSTG * (BM + BN) * BK;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[RING + (GRP ? NSTG * 1024 : 0)];
-    uint8_t(*sX)[BM * BK] = reinterpret_cast<uint8_t(*)[BM * BK]>(smem);
-    uint8_t(*sW)[BN * BK] = reinterpret_cast<uint8_t(*)[BN * BK]>(smem + NSTG * BM * BK);
-    float(*sS)[256] = reinterpret_cast<float(*)[256]>(smem + RING);  // GRP: [stage][tile row]
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[KSP * RING + (GRP ? NSTG * 1024 : 0)];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int grp = KSP == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 8);  // K group of this wavefront
+    const int wave = (tid >> 6) & 3;                                        // wavefront within its group
     const int wm = wave >> 1, wn = wave & 1;
+    uint8_t(*sX)[BM * BK] = reinterpret_cast<uint8_t(*)[BM * BK]>(smem + grp * RING);
+    uint8_t(*sW)[BN * BK] = reinterpret_cast<uint8_t(*)[BN * BK]>(smem + grp * RING + NSTG * BM * BK);
+    float(*sS)[256] = reinterpret_cast<float(*)[256]>(smem + KSP * RING);  // GRP: [stage][tile row]
     int tm, tn;
     tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int KT = (K + BK - 1) / BK;
+    // this group's stages [kt0, kt0 + KT); every group runs KTg iterations (the barriers are workgroup-wide), the
+    // ones past its own stages issue and compute nothing
+    const int KTall = (K + BK - 1) / BK, KTg = (KTall + KSP - 1) / KSP;
+    const int kt0 = grp * KTg, KT = max(0, min(KTall, kt0 + KTg) - kt0);
 
     // this lane's share of the direct loads: instruction j of wavefront w covers tile rows 16 (4 j + w) + lane / 4
     const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
@@ -335,8 +345,8 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
         cw[j] = 16 * ((lane & 3) ^ ((row >> sh) & 3));
         ow[j] = (uint32_t)row * K + cw[j];
     }
-    auto issue = [&](int kt) {
-        const int buf = kt % NSTG, k0 = kt * BK;
+    auto issue = [&](int kt) {  // kt: this group's stage index
+        const int buf = kt % NSTG, k0 = (kt0 + kt) * BK;
 #pragma unroll
         for (int j = 0; j < IX; ++j) {
             const uint32_t vo = k0 + cx[j] < K ? ox[j] + k0 : 0xfffffff0u;
@@ -348,7 +358,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
             lds_dma16(rw, vo, lds_addr(sW[buf] + 1024 * (4 * j + wave)));
         }
         if (GRP)  // scales sxT[kt, m0 + 64 wave + lane] (rows past the tile are loaded and not used)
-            lds_dma4(rs, (uint32_t)(((long)kt * M + m0 + 64 * wave + lane) * 4),
+            lds_dma4(rs, (uint32_t)(((long)(kt0 + kt) * M + m0 + 64 * wave + lane) * 4),
                      lds_addr(reinterpret_cast<uint8_t *>(sS[buf]) + 256 * wave));
     };
 
@@ -383,13 +393,14 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
 #pragma unroll
     for (int p = 0; p < NSTG - 1; ++p)
         if (p < KT) issue(p);
-    for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
         // stage kt has landed once at most the loads of the (up to NSTG - 2) stages issued after it are outstanding
         wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
         // stage kt visible to all; everyone is done with stage kt - 1, whose buffer refills next. A bare s_barrier:
         // __syncthreads()' fences would make the compiler drain every outstanding load here, the prefetches included
         // (LDS needs no cache maintenance between the wavefronts of a workgroup).
         asm volatile("s_barrier" ::: "memory");
+        if (KSP > 1 && kt >= KT) continue;  // this group's stages are done; it keeps meeting the barriers
         if (kt + NSTG - 1 < KT) issue(kt + NSTG - 1);
         const uint8_t *x_s = sX[kt % NSTG], *w_s = sW[kt % NSTG];
         // both k steps' fragments are read up front, the second set while the first set's MFMAs run
@@ -427,6 +438,36 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     }
 
     __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
+    if constexpr (KSP > 1) {
+        // groups 1.. store their accumulators (16-byte pieces, lane-contiguous), group 0 adds them in group order
+        v4i *part = reinterpret_cast<v4i *>(smem);
+        auto slot = [&](int g, int i, int j, int q) { return (((((g - 1) * 4 + wave) * TN + i) * TM + j) * 4 + q) * 64 + lane; };
+        if (grp > 0)
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        part[slot(grp, i, j, q)] =
+                            v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        __syncthreads();
+        if (grp == 0)
+#pragma unroll
+            for (int g = 1; g < KSP; ++g)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const v4i v = part[slot(g, i, j, q)];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+                        }
+        __syncthreads();  // the partials are read before group 0's epilogue slices overwrite them
+        if (grp > 0) return;
+    }
     if constexpr (GRP)
         epilogue<TM, TN, OUT>(facc, nullptr, sw, bias, Y, YsT, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
                               smem + wave * stage_bytes<TN>());
@@ -666,6 +707,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 struct TileCfg {
     int bm, bn, resident;
     double a, b;
+    int ksp = 1;  // wavefront groups splitting K inside the workgroup (per-token path)
 };
 
 // Tile sets: per-token (all seven), grouped (the four tiles whose fp32 accumulators fit beside the int32 ones), and
@@ -703,10 +745,47 @@ inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
     return bestc;
 }
 
+// Per-token path: the seven tiles, each also with K split over 2 (and, for the small tiles, 4) wavefront groups,
+// fitted like the table above to MI355X timings of every (tile, split) on the 13 LFM2 prefill / SigLIP2 shapes
+// (`resident` = workgroups one CU holds at that split). LFM2Q_GEMM_BM / _BN force a tile, LFM2Q_GEMM_KSPLIT its
+// split (default 1 when a tile is forced).
+inline TileCfg pick_tile_pt(int M, int N, int K) {
+    const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
+    const int force_ks = env_int("LFM2Q_GEMM_KSPLIT", 0);
+    static const TileCfg opts[] = {
+        {256, 256, 1, 0.1602, 13.18, 1}, {128, 256, 2, 0.2905, 7.561, 1}, {128, 256, 1, 0.2700, 10.24, 2},
+        {256, 128, 2, 0.2911, 7.385, 1}, {256, 128, 1, 0.2551, 11.07, 2}, {128, 128, 3, 0.3480, 5.025, 1},
+        {128, 128, 1, 0.3443, 5.495, 2}, {128, 64, 4, 0.4521, 3.957, 1},  {128, 64, 2, 0.4711, 2.457, 2},
+        {128, 64, 1, 0.5112, 3.716, 4},  {64, 128, 4, 0.4512, 3.989, 1},  {64, 128, 2, 0.4826, 2.524, 2},
+        {64, 128, 1, 0.5485, 3.476, 4},  {64, 64, 6, 0.5646, 2.981, 1},   {64, 64, 3, 0.6092, 0.771, 2},
+        {64, 64, 1, 0.6973, 2.274, 4}};
+    if (force_bm && force_bn) {
+        const int ks = force_ks == 4 ? 4 : force_ks == 2 ? 2 : 1;
+        for (const TileCfg &o : opts)
+            if (o.bm == force_bm && o.bn == force_bn && o.ksp == ks) return o;
+        for (const TileCfg &o : opts)
+            if (o.bm == force_bm && o.bn == force_bn && o.ksp == 1) return o;
+    }
+    const long cus = device_cus();
+    double best = 1e300;
+    TileCfg bestc = opts[5];
+    for (const TileCfg &o : opts) {
+        if (force_ks && o.ksp != force_ks) continue;
+        const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
+        const long per = (tiles + cus - 1) / cus;
+        const double t = o.a * (double)per * o.bm * o.bn * (double)K * 1e-6 + o.b * (double)((per + o.resident - 1) / o.resident);
+        if (t < best) {
+            best = t;
+            bestc = o;
+        }
+    }
+    return bestc;
+}
+
 template <int OUT>
 void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float *sw, const uint16_t *bias, void *Y,
                  int M, int N, int K, hipStream_t st) {
-    const TileCfg t = pick_tile(M, N, K);
+    const TileCfg t = pick_tile_pt(M, N, K);
     static const int sh = env_int("LFM2Q_GEMM_SWZ", 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
     if (t.bm == 256 && t.bn == 256) {
@@ -725,9 +804,20 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
     const bool small = t.bm + t.bn <= 192;
     int nst = (small && (long)grid.x <= device_cus() && K >= 4096) ? 6 : 3;
     if (const int f = env_int("LFM2Q_GEMM_STAGES", 0)) nst = f == 6 && t.bm + t.bn <= 384 ? 6 : 3;
+    // K split inside the workgroup (t.ksp groups of 4 wavefronts, int32 partials summed in LDS): where the tiles
+    // leave one workgroup per CU, a lone workgroup's stage is bound by its LDS -> MFMA dependency chain and a second
+    // or fourth group of wavefronts on other K stages fills the CU (w2 at 512 tokens: 36 -> 27 us).
+    const int ksp = t.ksp;
+    if (ksp > 1) nst = 3;
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
-        if (BM_ + BN_ <= 384 && nst == 6)                                                                            \
+        if (ksp == 4 && BM_ + BN_ <= 192)                                                                            \
+            gemm_i8_kernel<BM_, BN_, OUT, false, STAGES, (BM_ + BN_ <= 192 ? 4 : 1)><<<grid, 4 * GT, 0, st>>>(       \
+                A, B, sx, sw, bias, Y, M, N, K, sh);                                                                 \
+        else if (ksp == 2)                                                                                           \
+            gemm_i8_kernel<BM_, BN_, OUT, false, STAGES, 2><<<grid, 2 * GT, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K, \
+                                                                                      sh);                           \
+        else if (BM_ + BN_ <= 384 && nst == 6)                                                                       \
             gemm_i8_kernel<BM_, BN_, OUT, false, (BM_ + BN_ <= 384 ? 6 : 3)><<<grid, GT, 0, st>>>(A, B, sx, sw,      \
                                                                                                   bias, Y, M, N, K, sh); \
         else                                                                                                         \

@@ -145,23 +145,29 @@ def test_gemm_vision_shapes(E, M, K, N, gelu):
 TILES = [(256, 256), (128, 256), (256, 128), (128, 128), (128, 64), (64, 128), (64, 64)]
 
 
-@pytest.mark.parametrize("bm,bn,stages", [(bm, bn, 3) for bm, bn in TILES]
-                         + [(bm, bn, 6) for bm, bn in TILES if bm + bn <= 384])
-def test_gemm_every_tile_config(E, bm, bn, stages, monkeypatch):
+@pytest.mark.parametrize("bm,bn,stages,ksplit", [(bm, bn, 3, 1) for bm, bn in TILES]
+                         + [(bm, bn, 6, 1) for bm, bn in TILES if bm + bn <= 384]
+                         + [(bm, bn, 3, 2) for bm, bn in TILES if bm + bn <= 384]
+                         + [(bm, bn, 3, 4) for bm, bn in TILES if bm + bn <= 192])
+def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, monkeypatch):
     """Each kernel configuration (tile forced through LFM2Q_GEMM_BM / _BN, LDS ring depth through
-    LFM2Q_GEMM_STAGES) on a shape with M, N and K tails."""
+    LFM2Q_GEMM_STAGES, K split over 1, 2 or 4 wavefront groups through LFM2Q_GEMM_KSPLIT) on shapes with M, N and K
+    tails; with a K split also K whose stages divide unevenly (1104: 18 stages) and K with fewer stages than groups
+    (96: 2 stages), where some groups have nothing to add. int32 accumulators exact, bf16 epilogue bit-exact."""
     monkeypatch.setenv("LFM2Q_GEMM_BM", str(bm))
     monkeypatch.setenv("LFM2Q_GEMM_BN", str(bn))
     monkeypatch.setenv("LFM2Q_GEMM_STAGES", str(stages))
-    M, K, N = 300, 4304, 520
-    xq, sx, wq, sw, b = _operands(bm * 7 + bn, M, K, N, True)
-    acc = oracle.gemm_i8_i32(xq, wq)
-    c = torch.empty(M, N, device="cuda", dtype=torch.int32)
-    E.gemm_i8_i32(dev(xq), dev(wq), c)
-    assert np.array_equal(c.cpu().numpy(), acc)
-    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
-    E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), dev_bf16(b), y, False)
-    assert int(ulp_dist(host_bits(y), oracle.gemm_i8_epilogue(acc, sx, sw, b)).max()) == 0
+    monkeypatch.setenv("LFM2Q_GEMM_KSPLIT", str(ksplit))
+    M, N = 300, 520
+    for K in (4304, 1104, 96) if ksplit > 1 else (4304,):
+        xq, sx, wq, sw, b = _operands(bm * 7 + bn + K, M, K, N, True)
+        acc = oracle.gemm_i8_i32(xq, wq)
+        c = torch.empty(M, N, device="cuda", dtype=torch.int32)
+        E.gemm_i8_i32(dev(xq), dev(wq), c)
+        assert np.array_equal(c.cpu().numpy(), acc), f"int32 K={K}"
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), dev_bf16(b), y, False)
+        assert int(ulp_dist(host_bits(y), oracle.gemm_i8_epilogue(acc, sx, sw, b)).max()) == 0, f"bf16 K={K}"
 
 
 # ------------------------------------------------------------------------------------------------ errors
