@@ -504,8 +504,8 @@ __device__ __forceinline__ v8bf w8x8_to_bf16(uint32_t d0, uint32_t d1) {
     return __builtin_bit_cast(v8bf, r);
 }
 
-template <int BM, int BN, int OUT>
-__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_w8_kernel(
+template <int BM, int BN, int OUT, int KSP = 1>
+__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(2))) void gemm_w8_kernel(
     const uint16_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sw,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ Y, int M, int N, int K) {
     constexpr int BKE = 64;                       // k per stage
@@ -514,16 +514,23 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     constexpr int XS = BM * 2 * BKE, WS = BN * BKE;
     static_assert(IX >= 1 && IW >= 1 && TM >= 1 && TN >= 1, "tile too small");
     static_assert(4 * stage_bytes<TN>() <= STAGES * (XS + WS), "epilogue staging exceeds the LDS ring");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * (XS + WS)];
-    uint8_t(*sX)[XS] = reinterpret_cast<uint8_t(*)[XS]>(smem);
-    uint8_t(*sW)[WS] = reinterpret_cast<uint8_t(*)[WS]>(smem + STAGES * XS);
+    // KSP > 1: KSP groups of 4 wavefronts split the K stages, each with its own ring; the fp32 partial tiles of
+    // groups 1.. are added into group 0's through LDS, in group order, before the epilogue
+    static_assert(KSP == 1 || (KSP - 1) * BM * BN * 4 <= KSP * STAGES * (XS + WS), "partials exceed the rings");
+    constexpr int RING = STAGES * (XS + WS);
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[KSP * RING];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int grp = KSP == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 8);
+    const int wave = (tid >> 6) & 3;
     const int wm = wave >> 1, wn = wave & 1;
+    uint8_t(*sX)[XS] = reinterpret_cast<uint8_t(*)[XS]>(smem + grp * RING);
+    uint8_t(*sW)[WS] = reinterpret_cast<uint8_t(*)[WS]>(smem + grp * RING + STAGES * XS);
     int tm, tn;
     tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int KT = (K + BKE - 1) / BKE;
+    const int KTall = (K + BKE - 1) / BKE, KTg = (KTall + KSP - 1) / KSP;
+    const int kt0 = grp * KTg, KT = max(0, min(KTall, kt0 + KTg) - kt0);  // this group's stages kt0 .. kt0 + KT - 1
     const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K * 2, 0x7fffffffL));
     const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
     // X: instruction j of wavefront w fills rows 8 (4 j + w) .. + 7; lane i -> row + i / 8, slot i % 8
@@ -541,8 +548,8 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
         cw[j] = 16 * ((lane & 3) ^ ((row >> 2) & 3));
         ow[j] = (uint32_t)row * K + cw[j];
     }
-    auto issue = [&](int kt) {
-        const int buf = kt % STAGES, k0 = kt * BKE;
+    auto issue = [&](int kt) {  // kt: this group's stage index
+        const int buf = kt % STAGES, k0 = (kt0 + kt) * BKE;
 #pragma unroll
         for (int j = 0; j < IX; ++j) {
             const uint32_t vo = 2 * k0 + cx[j] < 2 * K ? ox[j] + 2 * k0 : 0xfffffff0u;
@@ -564,14 +571,15 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
     const int lr = lane & 31, lh = lane >> 5;
 
-    issue(0);
+    if (KT > 0) issue(0);
     if (KT > 1) issue(1);
-    for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
         if (kt + 1 < KT)
             __builtin_amdgcn_s_waitcnt(0x3f70 | (IX + IW));
         else
             __builtin_amdgcn_s_waitcnt(0x3f70);
         asm volatile("s_barrier" ::: "memory");
+        if (KSP > 1 && kt >= KT) continue;  // this group's stages are done; it keeps meeting the barriers
         if (kt + 2 < KT) issue(kt + 2);
         const uint8_t *x_s = sX[kt % STAGES], *w_s = sW[kt % STAGES];
 #pragma unroll
@@ -593,6 +601,35 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2))) void ge
         }
     }
     __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
+    if constexpr (KSP > 1) {
+        v4f *part = reinterpret_cast<v4f *>(smem);
+        auto slot = [&](int g, int i, int j, int q) { return (((((g - 1) * 4 + wave) * TN + i) * TM + j) * 4 + q) * 64 + lane; };
+        if (grp > 0)
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        part[slot(grp, i, j, q)] =
+                            v4f{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        __syncthreads();
+        if (grp == 0)
+#pragma unroll
+            for (int g = 1; g < KSP; ++g)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const v4f v = part[slot(g, i, j, q)];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+                        }
+        __syncthreads();  // the partials are read before group 0's epilogue slices overwrite them
+        if (grp > 0) return;
+    }
     epilogue<TM, TN, OUT>(acc, nullptr, sw, bias, Y, nullptr, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
                           smem + wave * stage_bytes<TN>());
 }
@@ -859,9 +896,22 @@ void launch_gemm_w8(const uint16_t *X, const int8_t *W, const float *sw, const u
                     int N, int K, hipStream_t st) {
     const TileCfg t = pick_tile(M, N, K, TILES_GROUPED);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
+    // K split inside the workgroup where the tiles leave at most one workgroup per CU (a lone workgroup of 4
+    // wavefronts is bound by its LDS -> convert -> MFMA chain): 4 groups for 64 x 64 tiles, 2 for the others (LDS).
+    // LFM2Q_GEMM_KSPLIT = 1 / 2 / 4 forces it (4 only for 64 x 64).
+    const int KT = (K + 63) / 64;
+    const bool s64 = t.bm == 64 && t.bn == 64;
+    int ksp = ((long)grid.x <= device_cus() && KT >= 8) ? (s64 ? 4 : 2) : 1;
+    if (const int f = env_int("LFM2Q_GEMM_KSPLIT", 0)) ksp = f == 4 && s64 ? 4 : f == 2 ? 2 : 1;
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
-        gemm_w8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(X, W, sw, bias, Y, M, N, K);                             \
+        if (ksp == 4 && BM_ == 64 && BN_ == 64)                                                                      \
+            gemm_w8_kernel<BM_, BN_, OUT, (BM_ == 64 && BN_ == 64 ? 4 : 1)><<<grid, 4 * GT, 0, st>>>(X, W, sw, bias, \
+                                                                                                  Y, M, N, K);       \
+        else if (ksp == 2)                                                                                           \
+            gemm_w8_kernel<BM_, BN_, OUT, 2><<<grid, 2 * GT, 0, st>>>(X, W, sw, bias, Y, M, N, K);                  \
+        else                                                                                                         \
+            gemm_w8_kernel<BM_, BN_, OUT><<<grid, GT, 0, st>>>(X, W, sw, bias, Y, M, N, K);                         \
         return;                                                                                                      \
     }
     LFM2Q_GEMM(128, 128)

@@ -16,11 +16,13 @@ w1|w3 16384 x 2048, w2 2048 x 8192, lm_head 65536 x 2048):
   INT8 and INT4 weights, batch <= 16: the GEMV (e.g. INT8 w1|w3 9.8 us at batch 16 against 18 us for W8A16 and for
                BF16 F.linear); its fused SwiGLU and residual epilogues run at every batch size, where the reference
                fuses at batch 1 only (_epi_ok);
-  INT8, batch > 16: the GEMV reads each weight once for up to 64 batch rows. The lm_head (32768+ rows) takes W8A16
-               (35 us, flat up to 64 rows, against 49 us for the GEMV at 24 rows); w1|w3-sized weights (8192+ rows)
-               the GEMV up to 32 rows (14.3 us) and W8A16 beyond; narrower weights the GEMV (qkv 7.8 us at 24 rows
-               against 11.7 us for BF16 F.linear), except that a kept BF16 copy takes over at K >= 8192 (w2 13.9 us
-               against 19.0) and above 32 rows; without a copy, W8A16 above 64 rows;
+  INT8, batch > 16: the GEMV reads each weight once for up to 64 batch rows, W8A16 splits K inside its workgroups
+               when the tiles are few. The lm_head (32768+ rows) takes W8A16 (35 us against 43 us for the GEMV at 24
+               rows); w1|w3-sized weights (8192+ rows) the GEMV up to 24 rows (11.9 us against 13.4) and W8A16
+               beyond (14.3 us at 64 rows against 22.3); narrow weights with K = 2048 the GEMV up to 32 rows, then the
+               kept BF16 copy or W8A16 (qkv ~11-12 us either way, GEMV 12.9 at 64 rows); w2 (K = 8192) the kept BF16
+               copy (13.9 us at 24 rows against 19.0), or without one the GEMV up to 48 rows and W8A16 beyond (33.7
+               us at 64 rows against 37.7);
   INT4, batch > 16: the kept BF16 copy through F.linear, or without one the GEMV in 16-row chunks (no INT4 GEMM);
   BF16 weights: the GEMV up to batch 8, and up to 16 for K < 8192 (qkv 6.6 us against 11.3 us for F.linear at
                batch 16; w2 18.5 against 13.1), F.linear beyond.
@@ -42,7 +44,7 @@ from .quant import GROUP, quantize_int4, quantize_int8
 MODES = ("cublas", "bf16", "int8", "int4")
 GEMV_MAX_BATCH = 16      # quantized weights: the GEMV beat F.linear and W8A16 at every LFM2 shape up to this batch
 BF16_GEMV_MAX_BATCH = 8  # BF16 weights (16 when K < 8192)
-W8A16_MIN_ROWS = 8192    # INT8 weights with this many output rows go to W8A16 above batch 32
+W8A16_MIN_ROWS = 8192    # INT8 weights with this many output rows go to W8A16 above batch 24
 HEAD_ROWS = 32768        # ... and above batch 16 with this many
 
 
@@ -63,10 +65,10 @@ def linear_path(mode, fmt, B, N, K, has_bf16):
         if N >= HEAD_ROWS:
             return "w8a16"
         if N >= W8A16_MIN_ROWS:
-            return "gemv" if B <= 32 else "w8a16"
-        if has_bf16 and (K >= 8192 or B > 32):
-            return "linear"
-        return "gemv" if B <= 64 else ("linear" if has_bf16 else "w8a16")
+            return "gemv" if B <= 24 else "w8a16"
+        if K >= 8192:
+            return "linear" if has_bf16 else ("gemv" if B <= 48 else "w8a16")
+        return "gemv" if B <= 32 else ("linear" if has_bf16 else "w8a16")
     return "linear" if has_bf16 else "gemv"
 
 

@@ -28,16 +28,17 @@ def test_int8_above_16():
     for B in (17, 24, 64, 128):
         assert linear_path("int8", "int8", B, *HEAD, True) == "w8a16"
         assert linear_path("int8", "int8", B, *HEAD, False) == "w8a16"
-    # w1|w3-sized: the GEMV up to 32 rows, then W8A16
+    # w1|w3-sized: the GEMV up to 24 rows, then W8A16
     for kept in (True, False):
-        assert [linear_path("int8", "int8", B, *W13, kept) for B in (17, 32, 33, 64)] == \
+        assert [linear_path("int8", "int8", B, *W13, kept) for B in (17, 24, 25, 64)] == \
             ["gemv", "gemv", "w8a16", "w8a16"]
-    # narrow: the GEMV; a kept BF16 copy at K = 8192 and above 32 rows; W8A16 above 64 rows without a copy
+    # narrow, K = 2048: the GEMV up to 32 rows, then the kept BF16 copy or W8A16
     assert [linear_path("int8", "int8", B, *QKV, True) for B in (17, 32, 33, 300)] == \
         ["gemv", "gemv", "linear", "linear"]
-    assert [linear_path("int8", "int8", B, *QKV, False) for B in (17, 64, 65)] == ["gemv", "gemv", "w8a16"]
+    assert [linear_path("int8", "int8", B, *QKV, False) for B in (17, 32, 33)] == ["gemv", "gemv", "w8a16"]
+    # w2 (K = 8192): the kept BF16 copy, or the GEMV up to 48 rows and W8A16 beyond
     assert [linear_path("int8", "int8", B, *W2, True) for B in (17, 64)] == ["linear", "linear"]
-    assert [linear_path("int8", "int8", B, *W2, False) for B in (17, 64, 65, 128)] == \
+    assert [linear_path("int8", "int8", B, *W2, False) for B in (17, 48, 49, 128)] == \
         ["gemv", "gemv", "w8a16", "w8a16"]
 
 

@@ -99,7 +99,7 @@ def test_linear_drop_bf16(weights):
     D = make(weights, "int8", drop_bf16=True)
     assert not D.lin_bf16
     paths = {(key, B): check_linear(D, key, B, B + 3) for key in SHAPES for B in (24, 40, 72)}
-    assert paths[(("qkv", 0), 40)] == "gemv" and paths[(("qkv", 0), 72)] == "w8a16"
+    assert paths[(("qkv", 0), 24)] == "gemv" and paths[(("qkv", 0), 40)] == "w8a16"
     assert paths[(("w2", 0), 40)] == "gemv" and paths[(("w2", 0), 72)] == "w8a16"
     assert paths[(("head", 0), 24)] == "w8a16"
     assert paths[(("w13", 1), 24)] == "gemv" and paths[(("w13", 1), 40)] == "w8a16"

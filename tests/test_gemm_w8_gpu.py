@@ -48,13 +48,19 @@ def test_gemm_w8_vs_oracle(E, M, K, N, bias, gelu):
                       what=f"gemm_w8 {M}x{K}x{N}{' bias' if bias else ''}{' gelu' if gelu else ''}")
 
 
-@pytest.mark.parametrize("tile", ["128x128", "128x64", "64x128", "64x64"])
-def test_gemm_w8_every_tile(E, tile, monkeypatch):
+@pytest.mark.parametrize("tile,ksplit", [(t, k) for t in ("128x128", "128x64", "64x128", "64x64") for k in (1, 2)]
+                         + [("64x64", 4)])
+def test_gemm_w8_every_tile(E, tile, ksplit, monkeypatch):
+    """Every tile with K split over 1, 2 or 4 wavefront groups (LFM2Q_GEMM_KSPLIT), with K = 576 (9 stages), 1104
+    (18 stages, uneven split) and 128 (2 stages: some groups have nothing to add)."""
     bm, bn = tile.split("x")
     monkeypatch.setenv("LFM2Q_GEMM_BM", bm)
     monkeypatch.setenv("LFM2Q_GEMM_BN", bn)
-    x, W, sw, b = operands(3, 200, 576, 264, True)
-    assert_close_bf16(run(E, x, W, sw, b, False), oracle.gemm_w8(x, W, sw, b), what=f"gemm_w8 tile {tile}")
+    monkeypatch.setenv("LFM2Q_GEMM_KSPLIT", str(ksplit))
+    for K in (576, 1104, 128):
+        x, W, sw, b = operands(3 + K, 200, K, 264, True)
+        assert_close_bf16(run(E, x, W, sw, b, False), oracle.gemm_w8(x, W, sw, b),
+                          what=f"gemm_w8 tile {tile} ksplit {ksplit} K={K}")
 
 
 @pytest.mark.parametrize("M,K,N,bias,gelu", [(64, 2048, 16384, False, False), (256, 8192, 2048, False, False),
