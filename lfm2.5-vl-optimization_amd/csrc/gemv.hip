@@ -1,11 +1,13 @@
 // Decode GEMVs for gfx950: y[b, n] = (sum_k W[n, k] x[b, k]) * scale[n] with int8 (weight-only) or bf16 weights,
 // bf16 activations, fp32 accumulation, and optional fused SwiGLU / residual-add epilogues.
 //
-// Two kernels, both pure HBM streams over W (every weight byte is read exactly once per call):
+// The kernels are pure HBM streams over W (every weight byte is read exactly once per call):
 //   gemv_b1_kernel    batch 1. One wavefront owns R output rows; lane l streams the 16-byte chunks l, l+64, ...
 //                     of each row with non-temporal loads (a wavefront load = 1 KiB contiguous of one row), all of
 //                     a lane's chunks are in flight before the first FMA. int8 -> fp32 is one SDWA convert per
 //                     weight; the row sums of a wavefront's rows are reduced together (fold_sum). No LDS.
+//   gemv_bn_kernel    batch 2 with rows of at most 128 chunks: the batch-1 kernel over both batch rows, each weight
+//                     chunk converted once.
 //   gemv_mfma_kernel  batch 2..64. A workgroup owns RT tiles of 16 output rows (8 when the K run is split in two
 //                     inside the MFMA, batches <= 16) and BT batch tiles of 16 (8) rows that share every weight
 //                     load; its NWK wavefronts split K into 128-k blocks. A tile block is read by two wave loads of
@@ -267,6 +269,81 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, 
     } else {
         const float g = rbf(scale ? r * sg : r), u = rbf(scale ? ru * su : ru);
         y[n] = (uint16_t)f2bf(rbf(silu_f32(g)) * u);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ batch 2, VALU
+// The one-shot batch-1 kernel over NB batch rows at once: each weight chunk is converted once and dotted with the NB
+// rows' activations (all loads in flight before the first dot). Per batch row the arithmetic is the batch-1
+// kernel's (same chunk order, PairDot and fold_sum), so each row of the result is bit-identical to a batch-1 call.
+// For short rows only (K = 64 PER CPL, CPL <= 2): the activations of NB rows live in registers.
+template <typename WT, int R, int CPL, int EPI, int NB>
+__global__ __launch_bounds__(256) void gemv_bn_kernel(const WT *__restrict__ W, const float *__restrict__ scale,
+                                                      const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
+                                                      int N, int K, int S, int B) {
+    using D = PairDot<WT>;
+    constexpr int PER = D::PER, XL = D::XL;
+    constexpr int NROW = EPI == EPI_SWIGLU ? 2 * R : R;
+    static_assert(CPL >= 1, "K = 64 PER CPL");
+    const int lane = threadIdx.x & 63;
+    const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * R);
+    if (n0 >= N) return;  // no block-level synchronization in this kernel
+    const char *rp[NROW];
+#pragma unroll
+    for (int i = 0; i < NROW; ++i) {
+        const int orow = min(n0 + (i % R), N - 1);
+        const int wrow = (EPI == EPI_SWIGLU && i >= R) ? S + orow : orow;
+        rp[i] = reinterpret_cast<const char *>(W + (size_t)wrow * K);
+    }
+    constexpr int LPV = 64 / NROW;
+    const int ns = min(n0 + min(lane / LPV, R - 1), N - 1);
+    const float sg = scale ? scale[ns] : 1.f, su = (EPI == EPI_SWIGLU && scale) ? scale[S + ns] : 1.f;
+    uint32_t h0[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) h0[b] = (EPI == EPI_RESIDUAL && b < B) ? y[(size_t)b * N + ns] : 0u;
+    // batch rows past B read zeros through an empty range
+    const rsrc_t xr = make_rsrc(x, (uint32_t)B * K * 2u);
+    v4i w[CPL][NROW], xv[NB][CPL][XL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u)
+#pragma unroll
+        for (int i = 0; i < NROW; ++i) w[u][i] = ld_nt16(rp[i] + (size_t)(lane + 64 * u) * 16);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+#pragma unroll
+            for (int q = 0; q < XL; ++q)
+                xv[b][u][q] = buf_ld16(xr, (uint32_t)(((size_t)b * K + (size_t)(lane + 64 * u) * PER + 8 * q) * 2));
+    float acc[NB][NROW];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < NROW; ++i) acc[b][i] = 0.f;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u)
+#pragma unroll
+        for (int i = 0; i < NROW; ++i)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b][i] = D::dot(w[u][i], xv[b][u], acc[b][i]);
+    const int n = n0 + lane / LPV;
+    const bool st = lane % LPV == 0 && lane / LPV < R && n < N;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const float r = fold_sum<NROW>(acc[b]);
+        const float ru = EPI == EPI_SWIGLU ? __uint_as_float(__builtin_amdgcn_permlane32_swap(
+                                                 __float_as_uint(r), __float_as_uint(r), false, false)[1])
+                                           : 0.f;
+        if (!st || b >= B) continue;
+        uint16_t *yp = y + (size_t)b * N + n;
+        if (EPI == EPI_NONE) {
+            *yp = (uint16_t)f2bf(scale ? r * sg : r);
+        } else if (EPI == EPI_RESIDUAL) {
+            *yp = (uint16_t)f2bf(bf2f(h0[b]) + rbf(scale ? r * sg : r));
+        } else {
+            const float g = rbf(scale ? r * sg : r), u = rbf(scale ? ru * su : ru);
+            *yp = (uint16_t)f2bf(rbf(silu_f32(g)) * u);
+        }
     }
 }
 
@@ -570,6 +647,29 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 #undef LFM2Q_B1
 }
 
+// Batch 2 on the VALU kernel when a row is at most 128 chunks (K <= 2048 int8, 1024 bf16), R as for batch 1
+// (measured on MI355X: 4 % off the batch-2 decode step; at batch 3-4 the matrix-core kernel is faster). Returns
+// false where it does not apply. LFM2Q_GEMV_VALU = 0 turns it off (read on every call).
+template <typename WT, int EPI>
+bool launch_bn(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int N, int K, int S,
+               hipStream_t st) {
+    constexpr int PER = PairDot<WT>::PER;
+    if (B != 2 || K % (64 * PER) || K / (64 * PER) > 2) return false;
+    if (const char *e = getenv("LFM2Q_GEMV_VALU"))
+        if (atoi(e) == 0) return false;
+    const int cpl = K / (64 * PER);
+    const int r = (EPI == EPI_SWIGLU ? 2L * N : (long)N) >= 6144 ? 2 : 1;
+    const dim3 grid((N + 4 * r - 1) / (4 * r));
+#define LFM2Q_BN(R_, C_) gemv_bn_kernel<WT, R_, C_, EPI, 2><<<grid, 256, 0, st>>>(W, scale, x, y, N, K, S, B)
+    if (r == 2) {
+        if (cpl == 1) LFM2Q_BN(2, 1); else LFM2Q_BN(2, 2);
+    } else {
+        if (cpl == 1) LFM2Q_BN(1, 1); else LFM2Q_BN(1, 2);
+    }
+#undef LFM2Q_BN
+    return true;
+}
+
 // Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
 // [2 S, K] matrix) then split K alike, which keeps the fused epilogues bit-identical:
 //   BT (batch tiles per wavefront, sharing every weight load): 16-row batch tiles, BT = 1, 2 or 4 for up to 16, 32
@@ -695,7 +795,7 @@ int gemv_run(const char *name, const WT *W, const float *scale, const uint16_t *
         uint16_t *yb = y + (size_t)b0 * Nout;
         if (bs == 1)
             launch_b1<WT, EPI>(W, scale, xb, yb, Nout, K, S, rows, st);
-        else
+        else if (!launch_bn<WT, EPI>(W, scale, xb, yb, bs, Nout, K, S, st))
             launch_mfma<WT, EPI>(W, scale, xb, yb, bs, Nout, K, S, st);
     }
     return launch_status(name);

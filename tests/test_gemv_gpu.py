@@ -183,6 +183,42 @@ def test_gemv_bf16_vs_oracle(E, B, N, K):
     assert_close_bf16(host_bits(y), ref, what=f"gemv bf16 B={B}")
 
 
+@pytest.mark.parametrize("B", [2])
+@pytest.mark.parametrize("wt,N,K", [("int8", 300, 2048), ("int8", 7000, 1024), ("bf16", 300, 1024),
+                                    ("bf16", 6200, 512)])
+def test_gemv_valu_batch_rows_match_batch_1(E, B, wt, N, K):
+    """Batch 2 with short rows runs the VALU kernel over both batch rows at once: each row of the result equals a
+    batch-1 call on that row bit for bit (plain, SwiGLU and residual), and the whole stays within the bar of the
+    oracle."""
+    g = torch.Generator(device="cuda").manual_seed(B * 100 + K)
+    if wt == "int8":
+        W = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+        scale = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    else:
+        W = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        scale = None
+    x = torch.randn(B, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty(B, N, device="cuda", dtype=torch.bfloat16)
+    E.gemv(W, scale, x, y)
+    for b in range(B):
+        y1 = torch.empty(1, N, device="cuda", dtype=torch.bfloat16)
+        E.gemv(W, scale, x[b:b + 1].contiguous(), y1)
+        assert torch.equal(y[b], y1[0]), f"row {b}"
+    Wn = W.cpu().numpy() if wt == "int8" else host_bits(W)
+    assert_close_bf16(host_bits(y), oracle.gemv(Wn, None if scale is None else scale.cpu().numpy(), host_bits(x)),
+                      what=f"gemv {wt} B={B} [{N}x{K}] VALU batch")
+    S = N // 2
+    act = torch.empty(B, S, device="cuda", dtype=torch.bfloat16)
+    E.gemv_epi(0, W[:2 * S].contiguous(), None if scale is None else scale[:2 * S].contiguous(), x, act)
+    ref = torch.empty_like(act)
+    E.silu_mul(y[:, :2 * S].contiguous(), ref)
+    assert torch.equal(act, ref)
+    h0 = (torch.randn(B, N, device="cuda", generator=g) * 4).to(torch.bfloat16)
+    h = h0.clone()
+    E.gemv_residual(W, scale, x, h)
+    assert torch.equal(h, (h0.float() + y.float()).to(torch.bfloat16))
+
+
 # ------------------------------------------------------------------------------------------------ fused epilogues
 @pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 19, 40, 64])
 @pytest.mark.parametrize("wt", ["int8", "bf16"])
