@@ -303,7 +303,19 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
 
     for (int b0 = kb0; b0 < kb0 + P; b0 += KB) {
         v4i wv[KB][NT][2], xv[KB][8];
-        uint32_t sc[KB][NT][2], zp[KB][NT][2];  // raw scale / zero-point words, decoded at their use
+        // The stage's scales and zero points: 2 blocks x 2 halves = 4 groups per column. Lane (c, j) loads group
+        // gi(u = j / 2, h = j % 2) of its column's row, one load per tile instead of one per (block, half); lane
+        // (c, g) later takes group (u, h) from lane c + 16 (2 u + h). Raw words, decoded at their use.
+        static_assert(KB == 2, "one lane group per (block, half) of the stage");
+        uint32_t scr[NT], zpr[NT];
+        {
+            const int gj = min((min(b0 + (g >> 1) + cpart * P, nblk - 1) * 256 + 128 * (g & 1)) / group, G - 1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                scr[t] = F::scale_raw(S, srow[t], gj, G);
+                zpr[t] = F::zero_raw(Z, srow[t], gj, G);
+            }
+        }
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
             const int b = b0 + u;  // block of part 0; part s reads block b + s P
@@ -316,17 +328,6 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
                 const uint32_t o = ((c & 7) + (KS == 1 ? 8 * q : 0)) * rowb + 16 * ch + bq * 128u;
 #pragma unroll
                 for (int t = 0; t < NT; ++t) wv[u][t][q] = buf_ld16_nt(wr[t], in ? o : OOR);
-            }
-            // the lane's column reads block bw; its two 128-k halves lie in groups gi(0), gi(1)
-            const int bw = min(b + cpart * P, nblk - 1);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int gi = min((bw * 256 + 128 * h) / group, G - 1);
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    sc[u][t][h] = F::scale_raw(S, srow[t], gi, G);
-                    zp[u][t][h] = F::zero_raw(Z, srow[t], gi, G);
-                }
             }
             const int bx = b + cpart * P;
 #pragma unroll
@@ -387,8 +388,10 @@ __global__ __launch_bounds__(64 * NWK) void gemv_w4_mfma_kernel(const uint8_t *_
                         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[4 * h + j], bw4, d, 0, 0, 0);
                     }
                     const int gi = min((min(b0 + u + cpart * P, nblk - 1) * 256 + 128 * h) / group, G - 1);
-                    const float zc = (float)(128 + F::zero_of(zp[u][t][h], gi));
-                    const float sv = F::scale_of(sc[u][t][h]);
+                    const int src = (c + 16 * (2 * u + h)) << 2;  // the lane that loaded group (u, h)
+                    const uint32_t zw = FMT == 0 ? 0u : (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)zpr[t]);
+                    const float zc = (float)(128 + F::zero_of(zw, gi));
+                    const float sv = F::scale_of((uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)scr[t]));
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[t][e] += sv * (d[e] - zc * dx[h][e]);
                 }
