@@ -601,7 +601,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 
 // ------------------------------------------------------------------------------------------------ dispatch
 // Batch 1. Persistent kernel (LFM2Q_GEMV_WPC wavefronts per CU, default 8: the read-stream optimum measured on
-// MI355X) once every wavefront gets at least 8 rows, one-shot kernel below that with R output rows per wavefront:
+// MI355X) once every wavefront gets at least 64 rows (the 65536-row lm_head is 2.2 us faster one-shot), one-shot
+// kernel below that with R output rows per wavefront:
 // R = 2 from 6144 weight rows (half the wavefronts, each with twice the loads in flight and one reduction for both
 // rows), else 1; LFM2Q_GEMV_R = 1, 2 or 4 overrides it where the registers allow (read on every call). Both need
 // K = 64 PER CPL with CPL in {1, 2, 4, 8}; other K take the one-shot kernel's generic loop, where `rows` (1, 2, 4)
@@ -614,7 +615,8 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
     const int C = K / PER;
     const int cpl = C % 64 == 0 ? C / 64 : 0;
     const int blocks_p = device_cus() * (wpc < 4 ? 1 : wpc / 4);
-    const bool persistent = (long)N >= 8L * 4 * blocks_p;
+    bool persistent = (long)N >= 64L * 4 * blocks_p;
+    if (const char *e = getenv("LFM2Q_GEMV_PERSIST")) persistent = atoi(e) != 0 && cpl > 0;  // forced (tests)
     int r1 = (EPI == EPI_SWIGLU ? 2L * N : (long)N) >= 6144 ? 2 : 1;
     if (const char *e = getenv("LFM2Q_GEMV_R")) r1 = atoi(e);
     auto grid = [&](int R) { return dim3((N + 4 * R - 1) / (4 * R)); };

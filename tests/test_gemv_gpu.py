@@ -153,6 +153,39 @@ def test_gemv_w8_rows_hint_same_result(E, rows):
     assert torch.equal(y0, y1)
 
 
+@pytest.mark.parametrize("wt,N,K", [("int8", 5000, 2048), ("int8", 3001, 8192), ("int8", 4000, 1024),
+                                    ("bf16", 5000, 1024)])
+def test_gemv_persistent_matches_one_shot(E, monkeypatch, wt, N, K):
+    """Batch 1: the persistent kernel (forced with LFM2Q_GEMV_PERSIST=1; by default only for 131072+ rows at 8 wavefronts per CU) and the
+    one-shot kernel give the same bits, plain, SwiGLU and residual, and match the oracle."""
+    g = torch.Generator(device="cuda").manual_seed(N + K)
+    if wt == "int8":
+        W = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+        scale = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    else:
+        W = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        scale = None
+    x = torch.randn(1, K, device="cuda", generator=g).to(torch.bfloat16)
+    h0 = (torch.randn(1, N, device="cuda", generator=g) * 4).to(torch.bfloat16)
+    S = N // 2
+    W2, s2 = W[:2 * S].contiguous(), None if scale is None else scale[:2 * S].contiguous()
+    res = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("LFM2Q_GEMV_PERSIST", mode)
+        y = torch.empty(1, N, device="cuda", dtype=torch.bfloat16)
+        E.gemv(W, scale, x, y)
+        a = torch.empty(1, S, device="cuda", dtype=torch.bfloat16)
+        E.gemv_epi(0, W2, s2, x, a)
+        h = h0.clone()
+        E.gemv_residual(W, scale, x, h)
+        res[mode] = (y, a, h)
+    for u, v in zip(res["1"], res["0"]):
+        assert torch.equal(u, v)
+    Wn = W.cpu().numpy() if wt == "int8" else host_bits(W)
+    assert_close_bf16(host_bits(res["1"][0]), oracle.gemv(Wn, None if scale is None else scale.cpu().numpy(),
+                                                          host_bits(x)), what=f"persistent gemv {wt} [{N}x{K}]")
+
+
 @pytest.mark.parametrize("N,K", DECODE_SHAPES)
 @pytest.mark.parametrize("B", [1, 4, 16])
 def test_gemv_w8_decode_shapes(E, N, K, B):
