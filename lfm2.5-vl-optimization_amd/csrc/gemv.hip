@@ -678,11 +678,11 @@ bool launch_bn(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 //   or 64 batch rows;
 //   KS = 2 (8-row tiles, 256+ workgroups instead of 128) for at most 2048 weight rows: batch tiles of 8 rows, BT = 1
 //   up to batch 8 and 2 up to batch 16;
-//   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2, RT = 4 for 32768+ rows above
-//   8 batch rows without SwiGLU (the lm_head);
+//   RT = 2 for 6144+ weight rows (two tiles share each activation load) unless KS = 2, RT = 4 for 32768+ rows
+//   without SwiGLU (the lm_head);
 //   NWK from the 128-k blocks per wavefront: 2 when RT = 2 or BT > 1, 4 when KS = RT = BT = 1, 8 BT when KS = 2 (at
-//   least 4 wavefronts); at most 16 / BT (LDS), 8 / BT for 32768+ rows with several batch tiles. Measured on MI355X
-//   over the LFM2 decode shapes at batches 4 to 64.
+//   least 4 wavefronts with two batch tiles); at most 16 / BT (LDS), 8 / BT for 32768+ rows with several batch
+//   tiles. Measured on MI355X over the LFM2 decode shapes at batches 4 to 64.
 // LFM2Q_GEMV_MFMA = "KS,RT,NWK[,BT]" overrides the shape (read on every call; the last bits of the sums change with
 // it).
 template <typename WT, int EPI, int KS, int RT, int BT>
@@ -722,11 +722,11 @@ inline MfmaShape mfma_shape(int epi, long wrows, int B, int K) {
     m.ks = (B <= 16 && wrows <= 2048) ? 2 : 1;
     m.bt = m.ks == 2 ? (B <= 8 ? 1 : 2) : (B <= 16 ? 1 : B <= 32 ? 2 : 4);
     m.rt = (m.ks == 1 && wrows >= 6144) ? 2 : 1;
-    const bool head = B > 8 && wrows >= 32768;
+    const bool head = wrows >= 32768;
     if (epi != EPI_SWIGLU && head) m.rt = 4;  // halves the activation reads per weight byte again
     const int bpw = m.ks == 2 ? 8 * m.bt : (m.rt >= 2 || m.bt > 1) ? 2 : 4;  // target blocks per wavefront
     m.nwk = 1;
-    while (m.nwk < 16 && (nblk >= bpw * 2 * m.nwk || (m.ks == 2 && m.nwk < 4))) m.nwk *= 2;
+    while (m.nwk < 16 && (nblk >= bpw * 2 * m.nwk || (m.ks == 2 && m.bt > 1 && m.nwk < 4))) m.nwk *= 2;
     m.nwk = std::min(m.nwk, (head && m.bt > 1 ? 8 : 16) / m.bt);
     int fk = 0, fr = 0, fn = 0, fb = 1;
     if (const char *e = getenv("LFM2Q_GEMV_MFMA")) {
