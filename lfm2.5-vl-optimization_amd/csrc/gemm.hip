@@ -636,9 +636,11 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(2))) v
 
 // ------------------------------------------------------------------------------------------------ big tiles
 // 256 x 256 tiles for the large GEMMs: 512 threads (8 wavefronts as 4 token blocks x 2 weight blocks, each 64 tokens x
-// 128 weight rows = 2 x 4 MFMA tiles, two wavefronts per SIMD). Per MAC this moves 2/3 of the L2 -> LDS operand
-// bytes of the 128 x 256 kernel, which is what bounds the large shapes (the L2 runs near saturation there). K
-// advances in BKT-byte stages through an NST-deep LDS ring filled by direct loads (NST - 1 stages in flight).
+// 128 weight rows = 2 x 4 MFMA tiles, two wavefronts per SIMD; one wavefront per SIMD with 128 x 128 blocks, which
+// reads a third less LDS per MFMA, measured 10-25 % slower on every LFM2 / SigLIP2 shape). Per MAC this moves 2/3 of
+// the L2 -> LDS operand bytes of the 128 x 256 kernel, which is what bounds the large shapes (the L2 runs near
+// saturation there). K advances in BKT-byte stages through an NST-deep LDS ring filled by direct loads (NST - 1
+// stages in flight).
 // LDS rows are BKT bytes = CPR 16-byte chunks; chunk c of row r sits at slot c ^ ((r / (8 / CPR * 2)) % CPR), so
 // the 16 rows a 16-lane phase of ds_read_b128 reads at one logical chunk hit 16 distinct 16-byte bank groups of the
 // 64-bank LDS.
@@ -647,13 +649,14 @@ template <int OUT, int BKT, int NST>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_big_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K) {
+    constexpr int WV = 8;
     constexpr int BM = 256, BN = 256, WMt = 64, WNt = 128, TM = 2, TN = 4;
     constexpr int CPR = BKT / 16;        // 16-byte chunks per LDS row
     constexpr int RPI = 64 / CPR;        // rows one direct-load instruction fills (1 KiB)
-    constexpr int IL = BM / RPI / 8;     // direct-load instructions per wavefront per operand per stage
+    constexpr int IL = BM / RPI / WV;    // direct-load instructions per wavefront per operand per stage
     constexpr int KS = BKT / 32;         // 32-byte MFMA k steps per stage
     static_assert(2 * NST * BM * BKT <= 160 * 1024, "LDS ring too large");
-    static_assert(8 * stage_bytes<TN>() <= 2 * NST * BM * BKT, "epilogue staging exceeds the LDS ring");
+    static_assert(WV * stage_bytes<TN>() <= 2 * NST * BM * BKT, "epilogue staging exceeds the LDS ring");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * BM * BKT];
     uint8_t(*sX)[BM * BKT] = reinterpret_cast<uint8_t(*)[BM * BKT]>(smem);
     uint8_t(*sW)[BN * BKT] = reinterpret_cast<uint8_t(*)[BN * BKT]>(smem + NST * BM * BKT);
@@ -667,12 +670,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
     const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
-    // instruction j of wavefront w fills LDS rows RPI (8 j + w) .. + RPI - 1; lane i -> row + i / CPR, slot i % CPR
+    // instruction j of wavefront w fills LDS rows RPI (WV j + w) .. + RPI - 1; lane i -> row + i / CPR, slot i % CPR
     uint32_t off[IL];
     int cb[IL];
 #pragma unroll
     for (int j = 0; j < IL; ++j) {
-        const int row = RPI * (8 * j + wave) + lane / CPR;
+        const int row = RPI * (WV * j + wave) + lane / CPR;
         cb[j] = swzb<CPR>(row, lane % CPR) - row * BKT;  // byte offset of the logical chunk stored in this slot
         off[j] = (uint32_t)row * K + cb[j];
     }
@@ -681,8 +684,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
         for (int j = 0; j < IL; ++j) {
             const bool in = k0 + cb[j] < K;
-            lds_dma16(rx, in ? off[j] + k0 : 0xfffffff0u, lds_addr(sX[buf] + 1024 * (8 * j + wave)));
-            lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, lds_addr(sW[buf] + 1024 * (8 * j + wave)));
+            lds_dma16(rx, in ? off[j] + k0 : 0xfffffff0u, lds_addr(sX[buf] + 1024 * (WV * j + wave)));
+            lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, lds_addr(sW[buf] + 1024 * (WV * j + wave)));
         }
     };
 
@@ -700,10 +703,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         if (p < KT) issue(p);
     for (int kt = 0; kt < KT; ++kt) {
         // stage kt has landed once at most the loads of the stages after it that are in flight remain outstanding
+        static_assert((NST - 2) * 2 * IL < 64, "vmcnt holds 6 bits");
         if (kt + NST - 2 < KT)
-            __builtin_amdgcn_s_waitcnt(0x3f70 | ((NST - 2) * 2 * IL));  // vmcnt((NST - 2) * 2 IL)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * 2 * IL));
         else
-            __builtin_amdgcn_s_waitcnt(0x3f70);                          // vmcnt(0)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         asm volatile("s_barrier" ::: "memory");  // everyone's loads of stage kt landed; stage kt - 1 is free
         if (kt + NST - 1 < KT) issue(kt + NST - 1);
         const uint8_t *x_s = sX[kt % NST], *w_s = sW[kt % NST];
@@ -734,6 +738,190 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
     epilogue<TM, TN, OUT>(acc, sx, sw, bias, Y, nullptr, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
                           smem + wave * stage_bytes<TN>());
+}
+
+// Persistent form of the 256 x 256 kernel (128-byte stages, two ring slots): one workgroup per CU walks the tiles
+// w, w + grid, ... (same XCD bands as tile_of). When a tile's K loop ends, the next tile's first stage and its
+// epilogue operands (the 256 token scales, 256 weight scales and 256 bias values, by direct loads into a second
+// small LDS buffer) are issued before the epilogue runs, so their latency hides behind the dequant and the stores,
+// and the stores drain while the next tile's first stage computes: the stage-0 wait leaves exactly the wavefront's
+// SST staged stores outstanding. Staged stores are buffer stores whose out-of-range lanes get an offset past the
+// buffer (dropped by the range check), so every wavefront issues the same number; the staging area is the ring
+// slot the last stage used, 32 rows x 256 bytes per wavefront with 16-byte granule g of row r at g ^ (r % 16).
+// bf16 output only, with N % 8 == 0, 16-byte aligned Y and M N 2 < 2^31 (the launcher checks): the epilogue then
+// issues no vector memory loads, so nothing but the staged stores is outstanding when the next tile's first stage
+// is waited for.
+template <int OUT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_bigp_kernel(
+    const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
+    const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K) {
+    static_assert(OUT == OUT_BF16 || OUT == OUT_BF16_GELU, "bf16 output only");
+    constexpr int BM = 256, BN = 256, BKT = 128, WMt = 64, WNt = 128, TM = 2, TN = 4;
+    constexpr int CPR = BKT / 16, RPI = 64 / CPR, IL = BM / RPI / 8, KS = BKT / 32;
+    constexpr int SLOT = 2 * BM * BKT;             // one stage of both operands (64 KiB)
+    constexpr int EOP = 4 * BM + 4 * BN + 2 * BN;  // one tile's epilogue operands: sx, sw, bias (2.5 KiB)
+    constexpr int SST = TM * 32 / 4;               // staged stores per wavefront per tile (4 rows per store)
+    static_assert(8 * 32 * 2 * WNt <= SLOT, "epilogue staging exceeds a ring slot");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SLOT + 2 * EOP];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tm_n = (M + BM - 1) / BM, tn_n = (N + BN - 1) / BN, T = tm_n * tn_n;
+    const int KT = (K + BKT - 1) / BKT;
+    int t = blockIdx.x;
+    if (t >= T) return;  // the launch sizes the grid to at most T; uniform per workgroup
+
+    uint32_t off[IL];
+    int cb[IL];
+#pragma unroll
+    for (int j = 0; j < IL; ++j) {
+        const int row = RPI * (8 * j + wave) + lane / CPR;
+        cb[j] = swzb<CPR>(row, lane % CPR) - row * BKT;
+        off[j] = (uint32_t)row * K + cb[j];
+    }
+    int m0 = 0, n0 = 0;
+    v4i rx, rw;
+    auto at_tile = [&](int tt) {
+        int tm, tn;
+        tile_of(tt, tm_n, tn_n, tm, tn);
+        m0 = tm * BM;
+        n0 = tn * BN;
+        rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
+        rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
+    };
+    // LDS addresses as 32-bit wavefront-uniform offsets from the array's base (scalar arithmetic only)
+    const uint32_t lbase = lds_addr(smem), wbase = __builtin_amdgcn_readfirstlane(wave);
+    auto issue = [&](int kt, int slot) {
+        const uint32_t sX = lbase + slot * SLOT, sW = sX + BM * BKT;
+        const int k0 = kt * BKT;
+#pragma unroll
+        for (int j = 0; j < IL; ++j) {
+            const bool in = k0 + cb[j] < K;
+            lds_dma16(rx, in ? off[j] + k0 : 0xfffffff0u, sX + 1024 * (8 * j + wbase));
+            lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, sW + 1024 * (8 * j + wbase));
+        }
+    };
+    // the tile's token scales (waves 0-3, 64 each), weight scales (waves 4-7) and bias (waves 0-1) into LDS
+    const v4i rsx = make_desc(sx, (uint32_t)M * 4), rsw = make_desc(sw, (uint32_t)N * 4);
+    const v4i rb = make_desc(bias, bias ? (uint32_t)N * 2 : 0u);
+    auto issue_eop = [&](int e) {
+        const uint32_t eb = lbase + 2 * SLOT + e * EOP;
+        // recomputed here rather than kept live across the K loop (register pressure)
+        int l = lane;
+        asm volatile("" : "+v"(l));
+        if (wbase < 4) {
+            lds_dma4(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
+            if (wbase < 2 && bias) lds_dma4(rb, (uint32_t)(n0 + 128 * wbase + 2 * l) * 2, eb + 2048 + 256 * wbase);
+        } else {
+            lds_dma4(rsw, (uint32_t)(n0 + 64 * (wbase - 4) + l) * 4, eb + 1024 + 256 * (wbase - 4));
+        }
+    };
+    const rsrc_t ry = make_rsrc(Y, (uint32_t)((size_t)M * N * 2));
+
+    at_tile(t);
+    issue(0, 0);
+    issue_eop(0);
+    const int lr = lane & 31, lh = lane >> 5;
+    int g = 0;  // ring stage counter across tiles: stage g sits in slot g & 1
+    for (int it = 0;; ++it) {
+        v16i acc[TN][TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+        for (int kt = 0; kt < KT; ++kt, ++g) {
+            // stage kt has landed once this wavefront's loads are done; at a tile's first stage the previous
+            // epilogue's staged stores, issued after those loads, may still be in flight
+            if (kt == 0 && it > 0)
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(SST));
+            else
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            asm volatile("s_barrier" ::: "memory");  // every wavefront's loads of stage kt landed; slot g + 1 is free
+            if (kt + 1 < KT) issue(kt + 1, (g + 1) & 1);
+            const uint8_t *x_s = smem + (g & 1) * SLOT, *w_s = x_s + BM * BKT;
+            v4i wf[2][TN], xf[2][TM];
+            auto rd = [&](int set, int kk) {
+                const int c = 2 * kk + lh;
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+                    wf[set][i] = *reinterpret_cast<const v4i *>(w_s + swzb<CPR>(wn * WNt + 32 * i + lr, c));
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    xf[set][j] = *reinterpret_cast<const v4i *>(x_s + swzb<CPR>(wm * WMt + 32 * j + lr, c));
+            };
+            rd(0, 0);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                if (kk + 1 < KS) rd((kk + 1) & 1, kk + 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk & 1][i], xf[kk & 1][j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // the next tile's first stage (slot g & 1, free since the barrier of this tile's last stage) and epilogue
+        // operands go out before this tile's epilogue
+        const int tnext = t + (int)gridDim.x;
+        const int pm0 = m0, pn0 = n0;
+        if (tnext < T) {
+            at_tile(tnext);
+            issue(0, g & 1);
+            issue_eop((it + 1) & 1);
+        }
+        asm volatile("s_barrier" ::: "memory");  // every wavefront is done with the last stage's slot
+        const int mb = pm0 + wm * WMt, nb = pn0 + wn * WNt;
+        {
+            const uint8_t *eb = smem + 2 * SLOT + (it & 1) * EOP;
+            const float *sxs = reinterpret_cast<const float *>(eb);
+            const float *sws = reinterpret_cast<const float *>(eb + 1024);
+            const uint16_t *bs = reinterpret_cast<const uint16_t *>(eb + 2048);
+            uint8_t *stage = smem + ((g - 1) & 1) * SLOT + wave * 8192;
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const float s_m = sxs[wm * WMt + 32 * j + lr];
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int nl = wn * WNt + 32 * i + 8 * q + 4 * lh;
+                        const v4f w4 = *reinterpret_cast<const v4f *>(sws + nl);
+                        uint32_t b01 = 0, b23 = 0;
+                        if (bias) {
+                            const uint2 bb = *reinterpret_cast<const uint2 *>(bs + nl);
+                            b01 = bb.x;
+                            b23 = bb.y;
+                        }
+                        float v[4];
+                        v[0] = dequant(acc[i][j][4 * q], s_m, w4[0], bf2f_lo(b01));
+                        v[1] = dequant(acc[i][j][4 * q + 1], s_m, w4[1], bf2f_hi(b01));
+                        v[2] = dequant(acc[i][j][4 * q + 2], s_m, w4[2], bf2f_lo(b23));
+                        v[3] = dequant(acc[i][j][4 * q + 3], s_m, w4[3], bf2f_hi(b23));
+                        if (out_gelu(OUT))
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f32(v[e]);
+                        *reinterpret_cast<uint2 *>(stage + lr * 256 + (((4 * i + q) ^ (lr & 15)) << 4) + 8 * lh) =
+                            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    }
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int rr = 0; rr < 32; rr += 4) {
+                    const int r = rr + (lane >> 4), c = lane & 15;
+                    const v4i v = *reinterpret_cast<const v4i *>(stage + r * 256 + ((c ^ (r & 15)) << 4));
+                    const int mo = mb + 32 * j + r, no = nb + 8 * c;
+                    const uint32_t o = (mo < M && no < N) ? (uint32_t)(((size_t)mo * N + no) * 2) : 0xfffffff0u;
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), ry, (int)o, 0, 0);
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+        if (tnext >= T) break;
+        t = tnext;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
@@ -790,12 +978,12 @@ inline TileCfg pick_tile_pt(int M, int N, int K) {
     const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
     const int force_ks = env_int("LFM2Q_GEMM_KSPLIT", 0);
     static const TileCfg opts[] = {
-        {256, 256, 1, 0.1602, 13.18, 1}, {128, 256, 2, 0.2905, 7.561, 1}, {128, 256, 1, 0.2700, 10.24, 2},
-        {256, 128, 2, 0.2911, 7.385, 1}, {256, 128, 1, 0.2551, 11.07, 2}, {128, 128, 3, 0.3480, 5.025, 1},
-        {128, 128, 1, 0.3443, 5.495, 2}, {128, 64, 4, 0.4521, 3.957, 1},  {128, 64, 2, 0.4711, 2.457, 2},
-        {128, 64, 1, 0.5112, 3.716, 4},  {64, 128, 4, 0.4512, 3.989, 1},  {64, 128, 2, 0.4826, 2.524, 2},
-        {64, 128, 1, 0.5485, 3.476, 4},  {64, 64, 6, 0.5646, 2.981, 1},   {64, 64, 3, 0.6092, 0.771, 2},
-        {64, 64, 1, 0.6973, 2.274, 4}};
+        {256, 256, 1, 0.1582, 10.87, 1}, {128, 256, 2, 0.2912, 7.604, 1}, {128, 256, 1, 0.2721, 10.14, 2},
+        {256, 128, 2, 0.2911, 7.455, 1}, {256, 128, 1, 0.2572, 10.95, 2}, {128, 128, 3, 0.3494, 5.003, 1},
+        {128, 128, 1, 0.3449, 5.533, 2}, {128, 64, 4, 0.4546, 3.930, 1},  {128, 64, 2, 0.4729, 2.456, 2},
+        {128, 64, 1, 0.5114, 3.760, 4},  {64, 128, 4, 0.4555, 3.970, 1},  {64, 128, 2, 0.4864, 2.494, 2},
+        {64, 128, 1, 0.5502, 3.505, 4},  {64, 64, 6, 0.5660, 3.086, 1},   {64, 64, 3, 0.6101, 0.836, 2},
+        {64, 64, 1, 0.7027, 2.256, 4}};
     if (force_bm && force_bn) {
         const int ks = force_ks == 4 ? 4 : force_ks == 2 ? 2 : 1;
         for (const TileCfg &o : opts)
@@ -826,6 +1014,15 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
     static const int sh = env_int("LFM2Q_GEMM_SWZ", 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
     if (t.bm == 256 && t.bn == 256) {
+        if constexpr (OUT == OUT_BF16 || OUT == OUT_BF16_GELU) {
+            // persistent form: one workgroup per CU (its LDS allows no second), at most one per tile
+            if (env_int("LFM2Q_GEMM_BIGP", 1) && K > 0 && (N & 7) == 0 && ((uintptr_t)Y & 15) == 0 &&
+                (size_t)M * N * 2 < 0x80000000ull) {
+                const int pgrid = (int)std::min<long>((long)grid.x, device_cus());
+                gemm_i8_bigp_kernel<OUT><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                return;
+            }
+        }
         // ring shape (K bytes per stage x stages); LFM2Q_GEMM_RING = 1282 / 644 / 645 forces one
         switch (env_int("LFM2Q_GEMM_RING", 1282)) {
         case 644: gemm_i8_big_kernel<OUT, 64, 4><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;

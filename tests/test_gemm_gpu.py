@@ -170,6 +170,28 @@ def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, monkeypatch):
         assert int(ulp_dist(host_bits(y), oracle.gemm_i8_epilogue(acc, sx, sw, b)).max()) == 0, f"bf16 K={K}"
 
 
+@pytest.mark.parametrize("bias,gelu", [(False, False), (True, True)])
+def test_gemm_persistent_big_tiles(E, bias, gelu, monkeypatch):
+    """The persistent 256 x 256 kernel with more tiles than workgroups (17 x 17 tiles on one workgroup per CU, so
+    workgroups take a second tile whose first stage and epilogue operands load during the first tile's epilogue),
+    with M, N and K tails: bf16 output against the oracle's epilogue of the exact int32 product (bit-exact, <= 1 ulp
+    with GELU) and bit-identical to the one-tile-per-workgroup kernel (LFM2Q_GEMM_BIGP=0)."""
+    monkeypatch.setenv("LFM2Q_GEMM_BM", "256")
+    monkeypatch.setenv("LFM2Q_GEMM_BN", "256")
+    M, K, N = 4100, 272, 4104
+    xq, sx, wq, sw, b = _operands(M + N + int(gelu), M, K, N, bias)
+    acc = oracle.gemm_i8_i32(xq, wq)
+    ref = oracle.gemm_i8_epilogue(acc, sx, sw, b, gelu)
+    outs = []
+    for persistent in ("1", "0"):
+        monkeypatch.setenv("LFM2Q_GEMM_BIGP", persistent)
+        y = torch.full((M, N), 3.0, device="cuda", dtype=torch.bfloat16)
+        E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), None if b is None else dev_bf16(b), y, gelu)
+        outs.append(host_bits(y))
+    assert int(ulp_dist(outs[0], ref).max()) <= (1 if gelu else 0)
+    assert np.array_equal(outs[0], outs[1])
+
+
 # ------------------------------------------------------------------------------------------------ errors
 def test_gemm_argument_errors(E):
     xq = torch.zeros(4, 64, device="cuda", dtype=torch.int8)
