@@ -621,7 +621,8 @@ def main():
         t_lib = sum(r["us_hipblaslt_int_mm_i32"] for r in shapes)
         big = next(r for r in shapes if r["M"] == 4096 and r["N"] == 16384)
         out["w8a8"] = {"unit": "TOPS", "peak": INT8_PEAK_TOPS,
-                       "roofline": {"bound": "mfma", "kernel": "gemm_i8_big_kernel<0,128,2> (4096 x 2048 x 16384)",
+                       "roofline": {"bound": "mfma",
+                                    "kernel": "gemm_i8_bigp_kernel<0> (4096 x 2048 x 16384, persistent 256 x 256 tiles)",
                                     "achieved": big["tops_gemm"], "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                                     "frac": round(big["tops_gemm"] / INT8_PEAK_TOPS, 4)},
                        "all_shapes_tops_hipblaslt_int_mm_i32": round(ops / t_lib / 1e6, 1),
