@@ -97,18 +97,16 @@ __device__ __forceinline__ v4i make_desc(const void *base, uint32_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(base);
     return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
 }
-// 16 bytes per lane from buffer offset `voff` straight into LDS at lds_base + 16 * lane (M0 holds lds_base). Written
-// as inline asm so the compiler, which cannot see which LDS bytes the load writes, does not drain every
-// outstanding load before each LDS read or barrier; the kernel orders it with explicit s_waitcnt + barrier.
+// 16 bytes per lane from buffer offset `voff` straight into LDS at lds_base + 16 * lane (lds_base is passed in M0,
+// which the compiler loads for the asm). Written as inline asm so the compiler, which cannot see which LDS bytes
+// the load writes, does not drain every outstanding load before each LDS read or barrier; the kernel orders it with
+// explicit s_waitcnt + barrier.
 __device__ __forceinline__ void lds_dma16(v4i desc, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(desc),
-                 "s"(lds_base)
-                 : "memory", "m0");
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base) : "memory");
 }
 // 4 bytes per lane from buffer offset `voff` into LDS at lds_base + 4 * lane
 __device__ __forceinline__ void lds_dma4(v4i desc, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "s"(lds_base)
-                 : "memory", "m0");
+    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base) : "memory");
 }
 // LDS address of p as a wavefront-uniform (SGPR) value for M0
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -292,8 +290,12 @@ __device__ __forceinline__ void epilogue(const ACC (&acc)[TN][TM], const float *
 // facc = fma((float)acc, sxT[kt, m], facc), in stage order -- the reference's fold, exact per group since |acc| <=
 // 64 * 127^2 < 2^24. The group's scales for the tile's rows travel with the operands (one 4-byte direct load per
 // wavefront per stage into a 1 KiB LDS slot) and are read after the stage's barrier. YsT: OUT_Q8 scales.
+// Occupancy hint: two wavefronts per SIMD, except where the 6-stage ring of a large tile leaves room for one workgroup
+template <int BM, int BN, int NSTG>
+constexpr int gemm_waves_per_eu() { return NSTG == 6 && BM + BN > 192 ? 1 : 2; }
+
 template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES, int KSP = 1>
-__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_kernel(
+__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu<BM, BN, NSTG>()))) void gemm_i8_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
     int sh, float *__restrict__ YsT = nullptr) {
