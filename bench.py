@@ -378,23 +378,27 @@ def w8a8_results(reps):
 
 def eager_kind(kind, B, reps, wfmt="int8"):
     """Counter-collection mode: the launches of one decode kind (of the `wfmt` decode step), one W8A8 GEMM shape
-    ("gemm:M,K,N", gemm kernel only, on one weight matrix) or a plain 256 MiB device copy (kind "copy", the
-    calibration of the HBM byte counters) run eagerly, one kernel per dispatch, `reps` times over."""
+    ("gemm:M,K,N", or "gemmg:M,K,N" with grouped-64 activation scales; gemm kernel only, on one weight matrix) or a
+    plain 256 MiB device copy (kind "copy", the calibration of the HBM byte counters) run eagerly, one kernel per
+    dispatch, `reps` times over."""
     if kind == "copy":
         src = torch.randint(-127, 128, (256 << 20,), device="cuda", dtype=torch.int8)
         dst = torch.empty_like(src)
         fns, nbytes = [lambda: dst.copy_(src)], 2 * src.numel()
-    elif kind.startswith("gemm:"):
+    elif kind.startswith(("gemm:", "gemmg:")):
         from lfm2opt.kernels import int8_ext
 
         E8 = int8_ext()
-        M, K, N = (int(v) for v in kind[5:].split(","))
+        M, K, N = (int(v) for v in kind.split(":")[1].split(","))
         g = torch.Generator(device="cuda").manual_seed(M + K + N)
         w = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
         xq = torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8, generator=g)
         sx, sw = torch.rand(M, device="cuda", generator=g), torch.rand(N, device="cuda", generator=g) * 0.01
+        if kind.startswith("gemmg:"):  # grouped-64 activation scales [K/64, M]
+            sx = torch.rand(K // 64, M, device="cuda", generator=g)
         y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
-        fns, nbytes = [lambda: E8.gemm_i8(xq, sx, w, sw, None, y, False)], M * K + N * K + 4 * (M + N) + 2 * M * N
+        fns = [lambda: E8.gemm_i8(xq, sx, w, sw, None, y, False)]
+        nbytes = M * K + N * K + 4 * sx.numel() + 4 * N + 2 * M * N
     else:
         step = DecodeStep(B, "cuda", wfmt=wfmt)
         sel = [(fn, b) for k, fn, b in step.ops if k == kind]
@@ -564,8 +568,8 @@ def main():
     ap.add_argument("--w4-batches", default="1,8", help="INT4 decode batch sizes ('' to skip)")
     ap.add_argument("--only-w8a8", action="store_true", help="W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--eager-kind", default=None,
-                    help="run one decode kind (e.g. 'w1|w3+swiglu'), 'gemm:M,K,N' or 'copy' eagerly, for counter "
-                         "collection")
+                    help="run one decode kind (e.g. 'w1|w3+swiglu'), 'gemm:M,K,N', 'gemmg:M,K,N' (grouped scales) or 'copy' "
+                         "eagerly, for counter collection")
     ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
