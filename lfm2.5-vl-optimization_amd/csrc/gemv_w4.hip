@@ -447,9 +447,10 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
 // Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
 // [2 S, K/8] matrix) then split K alike, which keeps the fused epilogues bit-identical:
 //   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows; RT = 2 for 6144+ weight rows unless
-//   KS = 2; NWK from the 256-k blocks per wavefront: 2 (4 when KS = 2, with at least 4 wavefronts), at most 8
-//   wavefronts for two-tile workgroups and 16 otherwise. INT4 costs twice the VALU work per weight byte of INT8, so
-//   its wavefronts take half the blocks (measured on MI355X at batches 2, 4 and 8). LFM2Q_W4_MFMA = "KS,RT,NWK" overrides the shape (read on every call).
+//   KS = 2; NWK from the 256-k blocks per wavefront: 2 (4 when KS = 2, with at least 4 wavefronts past K = 2048),
+//   at most 8 wavefronts for two-tile workgroups and 16 otherwise. INT4 costs twice the VALU work per weight byte
+//   of INT8, so its wavefronts take half the blocks (measured on MI355X at batches 2, 4 and 8). LFM2Q_W4_MFMA =
+//   "KS,RT,NWK" overrides the shape (read on every call).
 template <int FMT, int EPI, int KS, int RT>
 void launch_w4_shape(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int B, int N,
                      int K, int group, int nwk, hipStream_t st) {
@@ -475,8 +476,9 @@ void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uin
     int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
     const int bpw = ks == 2 ? 4 : 2;  // target blocks per wavefront
     int nwk = 1;
-    // at most 8 wavefronts with two tiles pairs (16 would cap the registers at 128 and spill)
-    while (nwk < (rt == 2 ? 8 : 16) && (nblk >= bpw * 2 * nwk || (ks == 2 && nwk < 4))) nwk *= 2;
+    // at most 8 wavefronts with two tiles pairs (16 would cap the registers at 128 and spill); 8-row tiles keep at
+    // least 4 wavefronts past 2048 k (2 for K = 2048: the narrow o / out_proj kernels, measured at batch 8)
+    while (nwk < (rt == 2 ? 8 : 16) && (nblk >= bpw * 2 * nwk || (ks == 2 && nblk > 8 && nwk < 4))) nwk *= 2;
     int fk = 0, fr = 0, fn = 0;
     if (const char *e = getenv("LFM2Q_W4_MFMA"))
         if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
