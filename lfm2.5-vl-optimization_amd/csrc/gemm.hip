@@ -750,9 +750,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 // SST staged stores outstanding. Staged stores are buffer stores whose out-of-range lanes get an offset past the
 // buffer (dropped by the range check), so every wavefront issues the same number; the staging area is the ring
 // slot the last stage used, 32 rows x 256 bytes per wavefront with 16-byte granule g of row r at g ^ (r % 16).
-// bf16 output only, with N % 8 == 0, 16-byte aligned Y and M N 2 < 2^31 (the launcher checks): the epilogue then
-// issues no vector memory loads, so nothing but the staged stores is outstanding when the next tile's first stage
-// is waited for.
+// bf16 output only, with N % 8 == 0, 16-byte aligned Y, 4-byte aligned bias (its dword loads) and M N 2 < 2^31
+// (the launcher checks): the epilogue then issues no vector memory loads, so nothing but the staged stores is
+// outstanding when the next tile's first stage is waited for.
 template <int OUT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_bigp_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
@@ -1019,7 +1019,7 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
         if constexpr (OUT == OUT_BF16 || OUT == OUT_BF16_GELU) {
             // persistent form: one workgroup per CU (its LDS allows no second), at most one per tile
             if (env_int("LFM2Q_GEMM_BIGP", 1) && K > 0 && (N & 7) == 0 && ((uintptr_t)Y & 15) == 0 &&
-                (size_t)M * N * 2 < 0x80000000ull) {
+                ((uintptr_t)bias & 3) == 0 && (size_t)M * N * 2 < 0x80000000ull) {
                 const int pgrid = (int)std::min<long>((long)grid.x, device_cus());
                 gemm_i8_bigp_kernel<OUT><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 return;
