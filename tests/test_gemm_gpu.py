@@ -192,6 +192,24 @@ def test_gemm_persistent_big_tiles(E, bias, gelu, monkeypatch):
     assert np.array_equal(outs[0], outs[1])
 
 
+def test_gemm_big_tiles_unaligned_operands(E, monkeypatch):
+    """256 x 256 tiles with a bias view 2 bytes off a 4-byte boundary and an output view 8 bytes off a 16-byte one:
+    the launcher leaves the persistent kernel (dword bias loads, 16-byte staged stores) for the one-tile-per-workgroup
+    kernel's predicated path; bf16 output still bit-exact against the oracle."""
+    monkeypatch.setenv("LFM2Q_GEMM_BM", "256")
+    monkeypatch.setenv("LFM2Q_GEMM_BN", "256")
+    M, K, N = 520, 128, 520
+    xq, sx, wq, sw, b = _operands(11, M, K, N, True)
+    ref = oracle.gemm_i8_epilogue(oracle.gemm_i8_i32(xq, wq), sx, sw, b, False)
+    bfull = dev_bf16(np.concatenate([[0], b]).astype(np.uint16))
+    yfull = torch.zeros(M * N + 4, device="cuda", dtype=torch.bfloat16)
+    for bias, y in ((bfull[1:], yfull[:M * N].view(M, N)), (bfull[1:], yfull[4:].view(M, N)),
+                    (dev_bf16(b), yfull[4:].view(M, N))):
+        y.fill_(5.0)
+        E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), bias, y, False)
+        assert int(ulp_dist(host_bits(y), ref).max()) == 0
+
+
 # ------------------------------------------------------------------------------------------------ errors
 def test_gemm_argument_errors(E):
     xq = torch.zeros(4, 64, device="cuda", dtype=torch.int8)
