@@ -222,6 +222,99 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
     }
 }
 
+// One-shot batch 1: wavefront w of workgroup b owns output rows (4 b + w) R .. + R - 1, issues all their weight,
+// scale and zero-point loads after its activation loads, and exits after them (many short wavefronts streaming
+// through the CUs, so one's dequantization overlaps the loads of those dispatched after it; the persistent kernel
+// issues every wavefront's rows up front and dequantizes them all at the end). Each wavefront converts its own
+// chunks' activations in registers (no LDS, no barrier) with the persistent kernel's arithmetic, so each row's bits
+// are the same as gemv_w4_b1_kernel's. Used below 32768 weight rows (measured: the decode step's w1|w3 6.5 -> 5.5
+// us, in_proj 4.1 -> 3.8 us; the 65536-row lm_head stays faster persistent).
+template <int FMT, int CPL, int EPI, int R>
+__global__ __launch_bounds__(256) void gemv_w4_b1o_kernel(const uint8_t *__restrict__ Wq, const void *__restrict__ S,
+                                                          const int32_t *__restrict__ Z, const uint16_t *__restrict__ x,
+                                                          uint16_t *__restrict__ y, int N, int K, int group, int Sr) {
+    using F = W4Fmt<FMT>;
+    const NibbleMasks nm;
+    constexpr int NROW = EPI == EPI_SWIGLU ? 2 : 1;
+    constexpr int V = NROW * R;
+    const int lane = threadIdx.x & 63;
+    const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * R);
+    if (n0 >= N) return;  // no block-level synchronization in this kernel
+    const int G = K / group;
+    int gl[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) gl[u] = min(32 * (lane + 64 * u) / group, G - 1);
+    const uint32_t rowb = (uint32_t)K / 2;
+    // activations first (cache hits), then every row's weights, scales and zero points
+    const rsrc_t xr = make_rsrc(x, (uint32_t)K * 2u);
+    v4i xd[CPL][4];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xd[u][j] = buf_ld16(xr, (uint32_t)(lane + 64 * u) * 64u + 16u * j);
+    v4i w[R][NROW][CPL];
+    uint32_t sr[R][NROW][CPL], zr[R][NROW][CPL];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < NROW; ++i) {
+            const int row = n0 + r, rc = min(row, N - 1);
+            const int wr = i ? Sr + row : row, wc = i ? Sr + rc : rc;
+            const rsrc_t rr = make_rsrc(Wq + (size_t)wr * rowb, row < N ? rowb : 0u);
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) {
+                w[r][i][u] = buf_ld16_nt(rr, (lane + 64 * u) * 16);
+                sr[r][i][u] = F::scale_raw(S, wc, gl[u], G);
+                zr[r][i][u] = F::zero_raw(Z, wc, gl[u], G);
+            }
+        }
+    const int ns = min(n0 + min(lane / (64 / V), R - 1), N - 1);
+    const uint32_t h0 = EPI == EPI_RESIDUAL ? y[ns] : 0u;
+    uint32_t xp[CPL][16];
+    float xs[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+        float t4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) xp[u][4 * j + p] = xpair(xd[u][j], p);
+            float t = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t += bf2f_lo((uint32_t)xd[u][j][e]) + bf2f_hi((uint32_t)xd[u][j][e]);
+            t4[j] = t;
+        }
+        xs[u] = ((t4[0] + t4[1]) + t4[2]) + t4[3];
+    }
+    float part[V];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < NROW; ++i) {
+            float acc = 0.f;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) {
+                float d = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        d = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nm.pair((uint32_t)w[r][i][u][j], p)),
+                                                            as_bf16x2(xp[u][4 * j + p]), d, false);
+                acc += F::scale_of(sr[r][i][u]) * (d - (float)(128 + F::zero_of(zr[r][i][u], gl[u])) * xs[u]);
+            }
+            part[i * R + r] = acc;
+        }
+    const float rs = fold_sum<V>(part);
+    const float us = EPI == EPI_SWIGLU ? __uint_as_float(__builtin_amdgcn_permlane32_swap(
+                                             __float_as_uint(rs), __float_as_uint(rs), false, false)[1])
+                                       : 0.f;
+    constexpr int LPV = 64 / V;
+    const int r = lane / LPV, row = n0 + r;
+    if (lane % LPV != 0 || r >= R || row >= N) return;
+    y[row] = (uint16_t)f2bf(epi_value(EPI, rs, us, h0));
+}
+
 // ------------------------------------------------------------------------------------------------ batch 2..16
 // A workgroup owns RT tiles of TR = 16 / KS output rows (EPI_SWIGLU: plus the matching w3 rows, NT = 2 RT tiles);
 // its NWK wavefronts split K into contiguous runs of 256-k blocks (one 128-byte line per row), KB blocks per stage,
@@ -436,6 +529,20 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
     const int C = K / 32;
     const int blocks = std::min((N + 3) / 4, std::max(1, device_cus() * wpc / 4));
     const dim3 grid(blocks);
+    // one-shot (two rows per wavefront) below 32768 weight rows; LFM2Q_W4_ONESHOT = 0 / 1 forces the persistent /
+    // one-shot kernel (read on every call)
+    bool oneshot = wrows < 32768;
+    if (const char *e = getenv("LFM2Q_W4_ONESHOT")) oneshot = atoi(e) != 0;
+    if (oneshot && C <= 256) {
+        const dim3 go((N + 7) / 8);
+        if (C <= 64)
+            gemv_w4_b1o_kernel<FMT, 1, EPI, 2><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
+        else if (C <= 128)
+            gemv_w4_b1o_kernel<FMT, 2, EPI, 2><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
+        else
+            gemv_w4_b1o_kernel<FMT, 4, EPI, 2><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
+        return;
+    }
     if (C <= 64)
         gemv_w4_b1_kernel<FMT, 1, EPI><<<grid, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
     else if (C <= 128)

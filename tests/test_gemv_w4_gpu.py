@@ -221,3 +221,23 @@ def test_w4_argument_errors_raise_before_launch(E):
         E.gemv_w4z(torch.zeros(64, 64, device="cuda", dtype=torch.int32), S.half(),
                    torch.zeros(64, 2, device="cuda", dtype=torch.int32), x, y)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("N,K,group", [(3001, 2048, 128), (130, 4096, 128), (257, 8192, 128), (77, 1024, 64)])
+def test_one_shot_matches_persistent(E, monkeypatch, fmt, N, K, group):
+    """Batch 1: the one-shot kernel (LFM2Q_W4_ONESHOT=1, the default below 32768 weight rows) and the persistent
+    kernel (LFM2Q_W4_ONESHOT=0) give the same bits, plain, SwiGLU and residual, in both weight formats."""
+    h0 = oracle.f2bf(np.random.default_rng(N).standard_normal((1, N)).astype(np.float32) * 4)
+    if fmt == 0:
+        Wp, S, x = gen_ref(N + K, 1, N, K, group)
+        runs = lambda epi, h=None, n=N: run_ref(E, Wp[:n], S[:n], x, epi, h)  # noqa: E731
+    else:
+        Wq, S, Z, x = gen_zp(N + K + 1, 1, N, K, group)
+        runs = lambda epi, h=None, n=N: run_zp(E, Wq[:n], S[:n], Z[:n], x, epi, h)  # noqa: E731
+    res = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("LFM2Q_W4_ONESHOT", mode)
+        res[mode] = (runs(0), runs(1, n=2 * (N // 2)), runs(2, h0))
+    for a, b in zip(res["1"], res["0"]):
+        assert np.array_equal(a, b)
