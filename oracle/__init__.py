@@ -1,7 +1,8 @@
 """CPU oracle for the quantized matrix-multiply hot path (numpy front end over oracle.c).
 
 TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package,
-and only as the checker. The product (liblfm2q.so and the lfm2opt package) never imports or calls it.
+and only as what results are compared with. The product (liblfm2q.so and the lfm2opt package) never imports or
+calls it.
 
 bf16 arrays are numpy uint16 arrays holding the raw bf16 bit patterns. Every function cites the reference code it
 restates (paths relative to the reference repository root); the arithmetic itself lives in oracle.c.

@@ -2,7 +2,8 @@
  *
  * TEST INFRASTRUCTURE ONLY. This file restates, in plain C, the arithmetic of the reference repository's kernels
  * and test references so that the GPU library can be checked against it. Only tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg may load it, and only as the checker; the product (liblfm2q + lfm2opt) never calls it.
+ * bench.py's cpu_baseline leg may load it, and only as the reference results are compared with (or, in the
+ * baseline, as the timed CPU path); the product (liblfm2q + lfm2opt) never calls it.
  *
  * Built with -ffp-contract=off and without fast-math: every fp32 operation below rounds exactly once, in the
  * order written, like the reference's __fmul_rn / __fadd_rn sequences. bf16 values are raw uint16 patterns.
