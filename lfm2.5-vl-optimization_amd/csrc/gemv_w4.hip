@@ -554,8 +554,9 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
 // Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
 // [2 S, K/8] matrix) then split K alike, which keeps the fused epilogues bit-identical:
 //   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows; RT = 2 for 6144+ weight rows unless
-//   KS = 2; NWK from the 256-k blocks per wavefront: 2 (4 when KS = 2, with at least 4 wavefronts past K = 2048),
-//   at most 8 wavefronts for two-tile workgroups and 16 otherwise. INT4 costs twice the VALU work per weight byte
+//   KS = 2, RT = 4 (at most 4 wavefronts) for 32768+ rows without SwiGLU (the lm_head, batch 8: 27.9 -> 26.6 us);
+//   NWK from the 256-k blocks per wavefront: 2 (4 when KS = 2, with at least 4 wavefronts past K = 2048), at most 8
+//   wavefronts for two-tile workgroups and 16 otherwise. INT4 costs twice the VALU work per weight byte
 //   of INT8, so its wavefronts take half the blocks (measured on MI355X at batches 2, 4 and 8). LFM2Q_W4_MFMA =
 //   "KS,RT,NWK" overrides the shape (read on every call).
 template <int FMT, int EPI, int KS, int RT>
@@ -581,6 +582,7 @@ void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uin
     const int nblk = (K + 255) / 256;
     int ks = (B <= 8 && wrows <= 2048) ? 2 : 1;
     int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
+    if (EPI != EPI_SWIGLU && ks == 1 && wrows >= 32768) rt = 4;  // the lm_head: four tiles share each activation load
     const int bpw = ks == 2 ? 4 : 2;  // target blocks per wavefront
     int nwk = 1;
     // at most 8 wavefronts with two tiles pairs (16 would cap the registers at 128 and spill); 8-row tiles keep at
@@ -589,11 +591,18 @@ void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uin
     int fk = 0, fr = 0, fn = 0;
     if (const char *e = getenv("LFM2Q_W4_MFMA"))
         if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
-            (fr == 1 || fr == 2) && (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
+            (fr == 1 || fr == 2 || (fr == 4 && fk == 1 && EPI != EPI_SWIGLU)) &&
+            (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
             ks = fk;
             rt = fr;
             nwk = fn;
         }
+    if constexpr (EPI != EPI_SWIGLU) {
+        if (rt == 4) {
+            launch_w4_shape<FMT, EPI, 1, 4>(W, S, Z, x, y, B, N, K, group, std::min(nwk, 4), st);
+            return;
+        }
+    }
     if (ks == 2)
         launch_w4_shape<FMT, EPI, 2, 1>(W, S, Z, x, y, B, N, K, group, nwk, st);
     else if (rt == 2)

@@ -101,7 +101,7 @@ def test_gemv_w4_vs_oracle(E, B, N, K, group):
     assert_close_bf16(run_ref(E, Wp, S, x), oracle.gemv_w4(Wp, S, x), what=f"gemv_w4 B={B} [{N}x{K}] g{group}")
 
 
-@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,2", "1,2,16", "2,1,1", "2,1,4", "2,1,16"])
+@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,2", "1,2,16", "1,4,2", "1,4,4", "2,1,1", "2,1,4", "2,1,16"])
 def test_gemv_w4_mfma_launch_shapes(E, monkeypatch, shape):
     """Every batch-2..16 launch shape of the matrix-core INT4 kernel (k-parts KS, row tiles RT, wavefronts NWK,
     forced through LFM2Q_W4_MFMA) against the oracle, in both weight formats, with a trailing half block
