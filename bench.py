@@ -325,6 +325,62 @@ def decode_results(B, steps, warmup, wfmt="int8"):
     return res
 
 
+def single_gemv_results(reps, cpu=True):
+    """The standalone decode up-projection GEMV: x bf16 [1, 2048] ~ N(0, 1), W int8 [8192, 2048] uniform over
+    [-127, 127], scale |N(0, 1)| 0.01 + 1e-3, y = bf16((x W^T) scale). Each call reads its own weights (>= 512 MB of
+    distinct matrices rotated, as profiling/bench_gemv.py:40 does with 400 MB on its GPU), timed as graph replays
+    and as eager back-to-back launches; beside it the reference's PyTorch dequant-matmul of the same GEMV
+    (tests/test_kernels.py:137) on the host cores, on one matrix."""
+    from lfm2opt.kernels import ext
+
+    E = ext()
+    N, K = 8192, 2048
+    g = torch.Generator(device="cuda").manual_seed(0)
+    ncopy = -(-512 * 2 ** 20 // (N * K))
+    Ws = [torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g) for _ in range(ncopy)]
+    ss = [torch.randn(N, device="cuda", generator=g).abs() * 0.01 + 1e-3 for _ in range(ncopy)]
+    x = torch.randn(1, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty(1, N, device="cuda", dtype=torch.bfloat16)
+
+    def run():
+        for W, sc in zip(Ws, ss):
+            E.gemv(W, sc, x, y)
+
+    gr = capture(run)
+    t_graph, _ = time_graph(gr, reps, 3)
+    run()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(max(3, reps // 4)):
+        run()
+    t1.record()
+    t1.synchronize()
+    us_graph = t_graph * 1e3 / ncopy
+    us_eager = t0.elapsed_time(t1) * 1e3 / (max(3, reps // 4) * ncopy)
+    nbytes = gemv_bytes(N, K, 1)
+    res = {"workload": "INT8 GEMV 8192 x 2048, batch 1", "bytes_per_call": nbytes, "weight_copies": ncopy,
+           "us_graph": round(us_graph, 2), "gbs_graph": round(nbytes / us_graph / 1e3, 1),
+           "hbm_frac_graph": round(nbytes / us_graph / 1e3 / HBM_PEAK_GBS, 4),
+           "us_eager": round(us_eager, 2), "gbs_eager": round(nbytes / us_eager / 1e3, 1),
+           "hbm_frac_eager": round(nbytes / us_eager / 1e3 / HBM_PEAK_GBS, 4)}
+    del gr, Ws, ss
+    torch.cuda.empty_cache()
+    if cpu:
+        from oracle.cpu_baseline import gemv_w8_dequant_matmul
+
+        gc = torch.Generator().manual_seed(0)
+        xc = torch.randn(1, K, generator=gc).to(torch.bfloat16)
+        Wc = torch.randint(-127, 128, (N, K), generator=gc, dtype=torch.int8)
+        sc = torch.randn(N, generator=gc).abs() * 0.01 + 1e-3
+        t, n = _median_time(lambda: gemv_w8_dequant_matmul(Wc, sc, xc), 3.0)
+        res["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "us": round(t * 1e6, 1),
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"one 8192 x 2048 GEMV, F.linear(x.float(), Wq.float() * scale[:, None])"
+                                         f".to(bf16) with the dequant inside the timed region, median of {n}"}
+    return res
+
+
 def w8a8_results(reps):
     """Per shape: per-token quantization of the bf16 activations + W8A8 GEMM (bf16 out, bias / GELU where the
     layer has them), each call on its own weights (>= 512 MB of distinct weights rotated). Activations ~N(0,1)
@@ -612,6 +668,8 @@ def main():
                      "us_per_launch": dom["us_per_launch"], "bytes_per_launch": dom["bytes_per_launch"]},
         "decode": {str(B): r for B, r in [(batches[0], res1)] + list(extra.items())},
     }
+    log("single GEMV 8192 x 2048")
+    out["single_gemv"] = single_gemv_results(max(20, args.steps // 2), cpu=not args.no_cpu)
     w4b = [int(b) for b in args.w4_batches.split(",") if b]
     if w4b:
         out["decode_w4"] = {str(B): decode_results(B, max(20, args.steps // 2), args.warmup, "int4") for B in w4b}

@@ -40,6 +40,19 @@ const char *lfm2q_last_error(void);
 /* Library version string. */
 const char *lfm2q_version(void);
 
+/* Tuning knobs: force one launch configuration of a kernel family that is otherwise chosen automatically (tile,
+ * K split, kernel form, wavefronts per CU), e.g. lfm2q_set_tuning("LFM2Q_GEMM_BM", "128"). value = 1 to 4
+ * comma-separated integers, or NULL / "" for automatic. A knob starts from the environment variable of the same
+ * name (read once, at the first launch) and is read with one atomic load per launch. Results may differ in the last
+ * bits between configurations where a kernel's summation order depends on them (the GEMV launch shapes); the W8A8
+ * int32 paths are exact whatever the configuration. Knob names: LFM2Q_GEMV_{WPC, PERSIST, R, VALU, MFMA, CHUNK},
+ * LFM2Q_W4_{WPC, ONESHOT, MFMA, B1_MFMA}, LFM2Q_GEMM_{BM, BN, KSPLIT, SWZ, BIGP, RING, STAGES}.
+ * Replaces the reference's implementation switches: set_gemv_impl() (kernels/lfm2_decode.cu:662-663, bound at
+ * kernels/lfm2_decode.cpp:166) and the LFM2_INT8_BM tile override (kernels/int8_gemm.cu:691). */
+int lfm2q_set_tuning(const char *name, const char *value);
+/* Current value of a knob: count = number of values set (0 = automatic), values[0..3]. */
+int lfm2q_get_tuning(const char *name, int *values, int *count);
+
 /* ------------------------------------------------------------------------------------------ decode GEMVs */
 
 /* Weight-only INT8 GEMV: y[b, n] = bf16( (sum_k W[n, k] * x[b, k]) * scale[n] ).

@@ -930,7 +930,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 // Tile choice by a two-term cost model fitted to MI355X timings of the seven configurations over the LFM2 prefill and
 // SigLIP2 vision shapes: with `per` = ceil(tiles / CUs) tiles on the busiest CU, time ~ a x per x BM x BN x K (the
 // CU's matrix-core work, a = microseconds per million MACs, lower for bigger tiles) + b x ceil(per / resident) (b =
-// per-round prologue / epilogue cost, `resident` = workgroups one CU holds). LFM2Q_GEMM_BM / _BN force a tile.
+// per-round prologue / epilogue cost, `resident` = workgroups one CU holds). The LFM2Q_GEMM_BM / _BN knobs force a tile.
 struct TileCfg {
     int bm, bn, resident;
     double a, b;
@@ -948,7 +948,7 @@ inline bool tile_in(const TileCfg &o, int set) {
 }
 
 inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
-    const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
+    const int force_bm = knob_int(KNOB_GEMM_BM, 0), force_bn = knob_int(KNOB_GEMM_BN, 0);
     static const TileCfg opts[] = {{256, 256, 1, 0.1488, 18.64}, {128, 256, 2, 0.2726, 10.38},
                                    {256, 128, 2, 0.2795, 9.88},  {128, 128, 3, 0.3312, 4.92},
                                    {128, 64, 4, 0.4559, 1.98},   {64, 128, 4, 0.4571, 2.03},
@@ -974,11 +974,11 @@ inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
 
 // Per-token path: the seven tiles, each also with K split over 2 (and, for the small tiles, 4) wavefront groups,
 // fitted like the table above to MI355X timings of every (tile, split) on the 13 LFM2 prefill / SigLIP2 shapes
-// (`resident` = workgroups one CU holds at that split). LFM2Q_GEMM_BM / _BN force a tile, LFM2Q_GEMM_KSPLIT its
-// split (default 1 when a tile is forced).
+// (`resident` = workgroups one CU holds at that split). The LFM2Q_GEMM_BM / _BN knobs force a tile,
+// LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced).
 inline TileCfg pick_tile_pt(int M, int N, int K) {
-    const int force_bm = env_int("LFM2Q_GEMM_BM", 0), force_bn = env_int("LFM2Q_GEMM_BN", 0);
-    const int force_ks = env_int("LFM2Q_GEMM_KSPLIT", 0);
+    const int force_bm = knob_int(KNOB_GEMM_BM, 0), force_bn = knob_int(KNOB_GEMM_BN, 0);
+    const int force_ks = knob_int(KNOB_GEMM_KSPLIT, 0);
     static const TileCfg opts[] = {
         {256, 256, 1, 0.1582, 10.87, 1}, {128, 256, 2, 0.2912, 7.604, 1}, {128, 256, 1, 0.2721, 10.14, 2},
         {256, 128, 2, 0.2911, 7.455, 1}, {256, 128, 1, 0.2572, 10.95, 2}, {128, 128, 3, 0.3494, 5.003, 1},
@@ -1013,20 +1013,20 @@ template <int OUT>
 void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float *sw, const uint16_t *bias, void *Y,
                  int M, int N, int K, hipStream_t st) {
     const TileCfg t = pick_tile_pt(M, N, K);
-    static const int sh = env_int("LFM2Q_GEMM_SWZ", 2);
+    const int sh = knob_int(KNOB_GEMM_SWZ, 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
     if (t.bm == 256 && t.bn == 256) {
         if constexpr (OUT == OUT_BF16 || OUT == OUT_BF16_GELU) {
             // persistent form: one workgroup per CU (its LDS allows no second), at most one per tile
-            if (env_int("LFM2Q_GEMM_BIGP", 1) && K > 0 && (N & 7) == 0 && ((uintptr_t)Y & 15) == 0 &&
+            if (knob_int(KNOB_GEMM_BIGP, 1) && K > 0 && (N & 7) == 0 && ((uintptr_t)Y & 15) == 0 &&
                 ((uintptr_t)bias & 3) == 0 && (size_t)M * N * 2 < 0x80000000ull) {
                 const int pgrid = (int)std::min<long>((long)grid.x, device_cus());
                 gemm_i8_bigp_kernel<OUT><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 return;
             }
         }
-        // ring shape (K bytes per stage x stages); LFM2Q_GEMM_RING = 1282 / 644 / 645 forces one
-        switch (env_int("LFM2Q_GEMM_RING", 1282)) {
+        // ring shape (K bytes per stage x stages); the LFM2Q_GEMM_RING knob (1282 / 644 / 645) forces one
+        switch (knob_int(KNOB_GEMM_RING, 1282)) {
         case 644: gemm_i8_big_kernel<OUT, 64, 4><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;
         case 645: gemm_i8_big_kernel<OUT, 64, 5><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;
         default: gemm_i8_big_kernel<OUT, 128, 2><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;
@@ -1035,11 +1035,11 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
     }
     // LDS ring depth 6 (4 stages in flight) for a small tile whose grid leaves one workgroup per CU on a long K: a
     // lone workgroup with 2 stages in flight is bound by the operand latency (w2 at 512 tokens: 45 -> 35 us); the
-    // deeper ring's LDS costs occupancy everywhere else. LFM2Q_GEMM_STAGES = 3 / 6 forces it (6 for any tile but
+    // deeper ring's LDS costs occupancy everywhere else. The LFM2Q_GEMM_STAGES knob (3 / 6) forces it (6 for any tile but
     // 256 x 256, which has its own ring).
     const bool small = t.bm + t.bn <= 192;
     int nst = (small && (long)grid.x <= device_cus() && K >= 4096) ? 6 : 3;
-    if (const int f = env_int("LFM2Q_GEMM_STAGES", 0)) nst = f == 6 && t.bm + t.bn <= 384 ? 6 : 3;
+    if (const int f = knob_int(KNOB_GEMM_STAGES, 0)) nst = f == 6 && t.bm + t.bn <= 384 ? 6 : 3;
     // K split inside the workgroup (t.ksp groups of 4 wavefronts, int32 partials summed in LDS): where the tiles
     // leave one workgroup per CU, a lone workgroup's stage is bound by its LDS -> MFMA dependency chain and a second
     // or fourth group of wavefronts on other K stages fills the CU (w2 at 512 tokens: 36 -> 27 us).
@@ -1074,7 +1074,7 @@ template <int OUT>
 void launch_gemm_grouped(const int8_t *A, const int8_t *B, const float *sxT, const float *sw, const uint16_t *bias,
                          void *Y, float *YsT, int M, int N, int K, hipStream_t st) {
     const TileCfg t = pick_tile(M, N, K, out_q8(OUT) ? TILES_Q8 : TILES_GROUPED);
-    static const int sh = env_int("LFM2Q_GEMM_SWZ", 2);
+    const int sh = knob_int(KNOB_GEMM_SWZ, 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
@@ -1097,11 +1097,11 @@ void launch_gemm_w8(const uint16_t *X, const int8_t *W, const float *sw, const u
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
     // K split inside the workgroup where the tiles leave at most one workgroup per CU (a lone workgroup of 4
     // wavefronts is bound by its LDS -> convert -> MFMA chain): 4 groups for 64 x 64 tiles, 2 for the others (LDS).
-    // LFM2Q_GEMM_KSPLIT = 1 / 2 / 4 forces it (4 only for 64 x 64).
+    // The LFM2Q_GEMM_KSPLIT knob (1 / 2 / 4) forces it (4 only for 64 x 64).
     const int KT = (K + 63) / 64;
     const bool s64 = t.bm == 64 && t.bn == 64;
     int ksp = ((long)grid.x <= device_cus() && KT >= 8) ? (s64 ? 4 : 2) : 1;
-    if (const int f = env_int("LFM2Q_GEMM_KSPLIT", 0)) ksp = f == 4 && s64 ? 4 : f == 2 ? 2 : 1;
+    if (const int f = knob_int(KNOB_GEMM_KSPLIT, 0)) ksp = f == 4 && s64 ? 4 : f == 2 ? 2 : 1;
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
         if (ksp == 4 && BM_ == 64 && BN_ == 64)                                                                      \

@@ -600,25 +600,25 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
-// Batch 1. Persistent kernel (LFM2Q_GEMV_WPC wavefronts per CU, default 8: the read-stream optimum measured on
+// Batch 1. Persistent kernel (knob LFM2Q_GEMV_WPC wavefronts per CU, default 8: the read-stream optimum measured on
 // MI355X) once every wavefront gets at least 64 rows (the 65536-row lm_head is 2.2 us faster one-shot), one-shot
 // kernel below that with R output rows per wavefront:
 // R = 2 from 6144 weight rows (half the wavefronts, each with twice the loads in flight and one reduction for both
-// rows), else 1; LFM2Q_GEMV_R = 1, 2 or 4 overrides it where the registers allow (read on every call). Both need
+// rows), else 1; the LFM2Q_GEMV_R knob (1, 2 or 4) overrides it where the registers allow. Both need
 // K = 64 PER CPL with CPL in {1, 2, 4, 8}; other K take the one-shot kernel's generic loop, where `rows` (1, 2, 4)
 // sets the output rows per wavefront. Per-row arithmetic is the same in all of them.
 template <typename WT, int EPI>
 void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int N, int K, int S, int rows,
                hipStream_t st) {
     constexpr int PER = PairDot<WT>::PER;
-    static const int wpc = env_int("LFM2Q_GEMV_WPC", 8);
+    const int wpc = knob_int(KNOB_GEMV_WPC, 8);
     const int C = K / PER;
     const int cpl = C % 64 == 0 ? C / 64 : 0;
     const int blocks_p = device_cus() * (wpc < 4 ? 1 : wpc / 4);
     bool persistent = (long)N >= 64L * 4 * blocks_p;
-    if (const char *e = getenv("LFM2Q_GEMV_PERSIST")) persistent = atoi(e) != 0 && cpl > 0;  // forced (tests)
+    if (const KnobVal f = knob(KNOB_GEMV_PERSIST); f.n) persistent = f.v[0] != 0 && cpl > 0;  // forced
     int r1 = (EPI == EPI_SWIGLU ? 2L * N : (long)N) >= 6144 ? 2 : 1;
-    if (const char *e = getenv("LFM2Q_GEMV_R")) r1 = atoi(e);
+    if (const KnobVal f = knob(KNOB_GEMV_R); f.n) r1 = f.v[0];
     auto grid = [&](int R) { return dim3((N + 4 * R - 1) / (4 * R)); };
     const dim3 gridp(std::min((N + 3) / 4, blocks_p));
 #define LFM2Q_B1(C_)                                                                                        \
@@ -651,14 +651,13 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 
 // Batch 2 on the VALU kernel when a row is at most 128 chunks (K <= 2048 int8, 1024 bf16), R as for batch 1
 // (measured on MI355X: 4 % off the batch-2 decode step; at batch 3-4 the matrix-core kernel is faster). Returns
-// false where it does not apply. LFM2Q_GEMV_VALU = 0 turns it off (read on every call).
+// false where it does not apply. The LFM2Q_GEMV_VALU knob = 0 turns it off.
 template <typename WT, int EPI>
 bool launch_bn(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int N, int K, int S,
                hipStream_t st) {
     constexpr int PER = PairDot<WT>::PER;
     if (B != 2 || K % (64 * PER) || K / (64 * PER) > 2) return false;
-    if (const char *e = getenv("LFM2Q_GEMV_VALU"))
-        if (atoi(e) == 0) return false;
+    if (knob_int(KNOB_GEMV_VALU, 1) == 0) return false;
     const int cpl = K / (64 * PER);
     const int r = (EPI == EPI_SWIGLU ? 2L * N : (long)N) >= 6144 ? 2 : 1;
     const dim3 grid((N + 4 * r - 1) / (4 * r));
@@ -683,8 +682,7 @@ bool launch_bn(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 //   NWK from the 128-k blocks per wavefront: 2 when RT = 2 or BT > 1, 4 when KS = RT = BT = 1, 8 BT when KS = 2 (at
 //   least 4 wavefronts with two batch tiles); at most 16 / BT (LDS), 8 / BT for 32768+ rows with several batch
 //   tiles. Measured on MI355X over the LFM2 decode shapes at batches 4 to 64.
-// LFM2Q_GEMV_MFMA = "KS,RT,NWK[,BT]" overrides the shape (read on every call; the last bits of the sums change with
-// it).
+// The LFM2Q_GEMV_MFMA knob = "KS,RT,NWK[,BT]" overrides the shape (the last bits of the sums change with it).
 template <typename WT, int EPI, int KS, int RT, int BT>
 void launch_mfma_shape(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int N, int K, int S,
                        int nwk, hipStream_t st) {
@@ -728,9 +726,8 @@ inline MfmaShape mfma_shape(int epi, long wrows, int B, int K) {
     m.nwk = 1;
     while (m.nwk < 16 && (nblk >= bpw * 2 * m.nwk || (m.ks == 2 && m.bt > 1 && m.nwk < 4))) m.nwk *= 2;
     m.nwk = std::min(m.nwk, (head && m.bt > 1 ? 8 : 16) / m.bt);
-    int fk = 0, fr = 0, fn = 0, fb = 1;
-    if (const char *e = getenv("LFM2Q_GEMV_MFMA")) {
-        const int got = sscanf(e, "%d,%d,%d,%d", &fk, &fr, &fn, &fb);
+    if (const KnobVal f = knob(KNOB_GEMV_MFMA); f.n) {
+        const int got = f.n, fk = f.v[0], fr = f.v[1], fn = f.v[2], fb = f.n >= 4 ? f.v[3] : 1;
         const bool bt_ok = (fb == 1 || fb == 2 || (fb == 4 && fk == 1)) && B <= (16 / fk) * fb;
         const bool rt_ok = fr == 1 || (fr == 2 && fk == 1) || (fr == 4 && fk == 1 && epi != EPI_SWIGLU);
         if (got >= 3 && (fk == 1 || (fk == 2 && fr == 1)) && bt_ok && rt_ok &&
@@ -774,7 +771,7 @@ void launch_mfma(const WT *W, const float *scale, const uint16_t *x, uint16_t *y
 }
 
 // y: [B, Nout] (Nout = S for SwiGLU). Batches run as consecutive chunks of at most 64 rows (16 when the activations
-// of 64 rows reach 1 GiB, or with LFM2Q_GEMV_CHUNK=16, read on every call); a chunk of one row takes the batch-1
+// of 64 rows reach 1 GiB, or with the LFM2Q_GEMV_CHUNK knob = 16); a chunk of one row takes the batch-1
 // kernels.
 template <typename WT, int EPI>
 int gemv_run(const char *name, const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int B, int Nout,
@@ -789,8 +786,7 @@ int gemv_run(const char *name, const WT *W, const float *scale, const uint16_t *
     const int S = Nout;  // SwiGLU: w3 rows start at S
     // the activation resource of a chunk must stay below the out-of-range offset (1 GiB) the kernel uses
     int chunk = 64L * K * 2 < (1L << 30) ? 64 : 16;
-    if (const char *e = getenv("LFM2Q_GEMV_CHUNK"))
-        if (atoi(e) == 16) chunk = 16;
+    if (knob_int(KNOB_GEMV_CHUNK, 0) == 16) chunk = 16;
     for (int b0 = 0; b0 < B; b0 += chunk) {
         const int bs = B - b0 < chunk ? B - b0 : chunk;
         const uint16_t *xb = x + (size_t)b0 * K;

@@ -522,17 +522,17 @@ template <int FMT, int EPI>
 void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int N, int K,
                   int group, hipStream_t st) {
     // wavefronts per CU: 4 up to 3072 rows (each wavefront amortizes its activation repack over more rows), 16 from
-    // 32768 rows (more loads in flight on a long stream), else 8; LFM2Q_W4_WPC overrides (read once)
-    static const int wpc_env = env_int("LFM2Q_W4_WPC", 0);
+    // 32768 rows (more loads in flight on a long stream), else 8; the LFM2Q_W4_WPC knob overrides it
+    const int wpc_env = knob_int(KNOB_W4_WPC, 0);
     const long wrows = (EPI == EPI_SWIGLU ? 2L : 1L) * N;
     const int wpc = wpc_env > 0 ? wpc_env : wrows <= 3072 ? 4 : wrows >= 32768 ? 16 : 8;
     const int C = K / 32;
     const int blocks = std::min((N + 3) / 4, std::max(1, device_cus() * wpc / 4));
     const dim3 grid(blocks);
-    // one-shot (two rows per wavefront) below 32768 weight rows; LFM2Q_W4_ONESHOT = 0 / 1 forces the persistent /
-    // one-shot kernel (read on every call)
+    // one-shot (two rows per wavefront) below 32768 weight rows; the LFM2Q_W4_ONESHOT knob = 0 / 1 forces the
+    // persistent / one-shot kernel
     bool oneshot = wrows < 32768;
-    if (const char *e = getenv("LFM2Q_W4_ONESHOT")) oneshot = atoi(e) != 0;
+    if (const KnobVal f = knob(KNOB_W4_ONESHOT); f.n) oneshot = f.v[0] != 0;
     if (oneshot && C <= 256) {
         const dim3 go((N + 7) / 8);
         if (C <= 64)
@@ -557,8 +557,8 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
 //   KS = 2, RT = 4 (at most 4 wavefronts) for 32768+ rows without SwiGLU (the lm_head, batch 8: 27.9 -> 26.6 us);
 //   NWK from the 256-k blocks per wavefront: 2 (4 when KS = 2, with at least 4 wavefronts past K = 2048), at most 8
 //   wavefronts for two-tile workgroups and 16 otherwise. INT4 costs twice the VALU work per weight byte
-//   of INT8, so its wavefronts take half the blocks (measured on MI355X at batches 2, 4 and 8). LFM2Q_W4_MFMA =
-//   "KS,RT,NWK" overrides the shape (read on every call).
+//   of INT8, so its wavefronts take half the blocks (measured on MI355X at batches 2, 4 and 8). The
+//   LFM2Q_W4_MFMA knob = "KS,RT,NWK" overrides the shape.
 template <int FMT, int EPI, int KS, int RT>
 void launch_w4_shape(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x, uint16_t *y, int B, int N,
                      int K, int group, int nwk, hipStream_t st) {
@@ -588,15 +588,16 @@ void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uin
     // at most 8 wavefronts with two tiles pairs (16 would cap the registers at 128 and spill); 8-row tiles keep at
     // least 4 wavefronts past 2048 k (2 for K = 2048: the narrow o / out_proj kernels, measured at batch 8)
     while (nwk < (rt == 2 ? 8 : 16) && (nblk >= bpw * 2 * nwk || (ks == 2 && nblk > 8 && nwk < 4))) nwk *= 2;
-    int fk = 0, fr = 0, fn = 0;
-    if (const char *e = getenv("LFM2Q_W4_MFMA"))
-        if (sscanf(e, "%d,%d,%d", &fk, &fr, &fn) == 3 && (fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
+    if (const KnobVal f = knob(KNOB_W4_MFMA); f.n == 3) {
+        const int fk = f.v[0], fr = f.v[1], fn = f.v[2];
+        if ((fk == 1 || (fk == 2 && B <= 8 && fr == 1)) &&
             (fr == 1 || fr == 2 || (fr == 4 && fk == 1 && EPI != EPI_SWIGLU)) &&
             (fn == 1 || fn == 2 || fn == 4 || fn == 8 || fn == 16)) {
             ks = fk;
             rt = fr;
             nwk = fn;
         }
+    }
     if constexpr (EPI != EPI_SWIGLU) {
         if (rt == 4) {
             launch_w4_shape<FMT, EPI, 1, 4>(W, S, Z, x, y, B, N, K, group, std::min(nwk, 4), st);
@@ -618,7 +619,7 @@ void w4_run(const uint8_t *W, const void *S, const int32_t *Z, const uint16_t *x
         const int bs = std::min(16, B - b0);
         const uint16_t *xb = x + (size_t)b0 * K;
         uint16_t *yb = y + (size_t)b0 * N;
-        static const bool b1_mfma = env_int("LFM2Q_W4_B1_MFMA", 0) != 0;
+        const bool b1_mfma = knob_int(KNOB_W4_B1_MFMA, 0) != 0;
         if ((bs > 1 || b1_mfma) && group % 128 == 0) {
             launch_w4_mfma<FMT, EPI>(W, S, Z, xb, yb, bs, N, K, group, st);
         } else {

@@ -1,4 +1,5 @@
-// Host-side status plumbing shared by the entry points: per-thread error message, argument checks, launch checks.
+// Host-side status plumbing shared by the entry points: per-thread error message, argument checks, launch checks,
+// and the tuning knobs that force a kernel configuration.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -17,8 +18,40 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // Compute units of the current device (queried once per device, then cached; 256 on MI355X).
 int device_cus();
 
-// Integer tuning knob from the environment (read once per name by the caller), or `dflt` when unset.
-int env_int(const char *name, int dflt);
+// Tuning knobs: each forces one choice of a launch path (tile, split, kernel form) that is otherwise automatic.
+// A knob holds up to four integers ("n" of them set; n == 0 = automatic). Initial values come from the environment
+// variable of the same name, read once on first use; lfm2q_set_tuning changes them at run time. Every knob is one
+// 64-bit atomic word, so a launch reads it with one load and never sees half of a concurrent update.
+enum Knob {
+    KNOB_GEMV_WPC,      // batch-1 persistent GEMV: wavefronts per CU
+    KNOB_GEMV_PERSIST,  // batch-1 GEMV: 1 persistent, 0 one-shot kernel
+    KNOB_GEMV_R,        // batch-1 one-shot GEMV: output rows per wavefront (1, 2, 4)
+    KNOB_GEMV_VALU,     // batch-2 GEMV: 0 turns the VALU kernel off
+    KNOB_GEMV_MFMA,     // batch 2..64 GEMV shape "KS,RT,NWK[,BT]"
+    KNOB_GEMV_CHUNK,    // GEMV batch chunk (16 or 64 rows)
+    KNOB_W4_WPC,        // batch-1 persistent INT4 GEMV: wavefronts per CU
+    KNOB_W4_ONESHOT,    // batch-1 INT4 GEMV: 1 one-shot, 0 persistent kernel
+    KNOB_W4_MFMA,       // INT4 batch 2..16 shape "KS,RT,NWK"
+    KNOB_W4_B1_MFMA,    // INT4 batch 1 on the matrix-core kernel (1)
+    KNOB_GEMM_BM,       // W8A8 / W8A16 tile rows
+    KNOB_GEMM_BN,       // W8A8 / W8A16 tile columns
+    KNOB_GEMM_KSPLIT,   // K split inside the workgroup (1, 2, 4)
+    KNOB_GEMM_SWZ,      // XCD band traversal group (log2 of M-tiles per group)
+    KNOB_GEMM_BIGP,     // 256 x 256 tiles: 0 = one workgroup per tile instead of the persistent kernel
+    KNOB_GEMM_RING,     // 256 x 256 one-workgroup-per-tile ring shape (1282, 644, 645)
+    KNOB_GEMM_STAGES,   // LDS ring depth (3, 6)
+    KNOB_COUNT
+};
+struct KnobVal {
+    int n;     // values set (0: automatic)
+    int v[4];  // the values, v[i] = 0 for i >= n
+};
+KnobVal knob(Knob k);
+// The knob's first value, or dflt when it is not set.
+inline int knob_int(Knob k, int dflt) {
+    const KnobVal kv = knob(k);
+    return kv.n ? kv.v[0] : dflt;
+}
 
 }  // namespace lfm2q
 

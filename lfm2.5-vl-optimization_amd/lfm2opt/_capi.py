@@ -34,6 +34,8 @@ SIGNATURES = {
     "lfm2q_gemm_i8_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_w8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_i32": [_P, _P, _P, _I, _I, _I, _P],
+    "lfm2q_set_tuning": [ctypes.c_char_p, ctypes.c_char_p],
+    "lfm2q_get_tuning": [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(_I)],
 }
 
 _lib = None
@@ -62,6 +64,18 @@ def call(name, *args):
     st = getattr(lib(), name)(*args)
     if st != 0:
         raise RuntimeError(lib().lfm2q_last_error().decode())
+
+
+def set_tuning(name, value=None):
+    """Force a launch configuration (lfm2q_set_tuning): value "a,b,..." or an int, None = automatic."""
+    call("lfm2q_set_tuning", name.encode(), None if value is None else str(value).encode())
+
+
+def get_tuning(name):
+    """The knob's values as a tuple (empty = automatic)."""
+    vals, n = (_I * 4)(), _I(0)
+    call("lfm2q_get_tuning", name.encode(), vals, ctypes.byref(n))
+    return tuple(vals[: n.value])
 
 
 def stream(t):

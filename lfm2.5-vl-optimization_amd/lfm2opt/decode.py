@@ -78,10 +78,12 @@ class DecodeLinears:
 
     weights: {key: BF16 [N, K]} on the GPU. w4_pre: {key: (packed uint8 [N, K/2], scales fp32 [N, K/group])
     (the reference's format), optionally + inv_s [K]} or {key: (qweight int32 [N, K/8], scales fp16, qzeros int32)
-    (GPTQ-style), optionally + inv_s}. drop_bf16 frees the BF16 copies the quantized weights no longer need
+    (GPTQ-style), optionally + inv_s}. w4_clip: INT4 scales by the clip search of quantize_int4 (runtime.py:186).
+    drop_bf16 frees the BF16 copies the quantized weights no longer need
     (runtime.py:200-215); it requires mode "int8" as in the reference (runtime.py:33-34)."""
 
-    def __init__(self, weights, gemv="int8", w4_group=GROUP, w4_keep_int8=(), w4_pre=None, drop_bf16=False):
+    def __init__(self, weights, gemv="int8", w4_group=GROUP, w4_keep_int8=(), w4_pre=None, drop_bf16=False,
+                 w4_clip=False):
         if gemv not in MODES:
             raise ValueError(f"gemv must be one of {MODES}, got {gemv!r}")
         if drop_bf16 and gemv != "int8":
@@ -105,7 +107,7 @@ class DecodeLinears:
             elif key in w4_pre:  # runtime.py:180-181, with the AWQ inv_s of :183-184 carried along
                 self._set_w4_pre(key, w, w4_pre[key])
             else:
-                self.lin[key], self.lin_scale[key] = quantize_int4(w, w4_group)
+                self.lin[key], self.lin_scale[key] = quantize_int4(w, w4_group, w4_clip)
             if self.lin[key].dtype == torch.int8:
                 self.w8[key] = Int8Linear(q=self.lin[key], scale=self.lin_scale[key], a8=False)
         if drop_bf16:

@@ -24,14 +24,35 @@ def quantize_int8(w: torch.Tensor):
     return q.contiguous(), scale.contiguous()
 
 
+CLIP_FRACTIONS = torch.linspace(0.70, 1.00, 16)  # clip search: candidate scales absmax * a / 7
+CLIP_ROWS = 1024  # clip search: weight rows per pass (16 candidates x rows x K fp32 values live at once)
+
+
+def _clip_scales(wg: torch.Tensor, amax: torch.Tensor):
+    """Per group, the candidate scale amax * a / 7 (a in CLIP_FRACTIONS) whose round-to-nearest INT4 reconstruction
+    has the smallest squared error; the first such candidate on ties. wg [n, G, group], amax [n, G]."""
+    out = torch.empty_like(amax)
+    cand = CLIP_FRACTIONS.to(wg.device)[:, None, None]
+    for r0 in range(0, wg.shape[0], CLIP_ROWS):
+        w = wg[r0:r0 + CLIP_ROWS]
+        s = amax[None, r0:r0 + CLIP_ROWS] * cand / 7                          # [16, n, G]
+        rec = torch.round(w[None] / s[..., None]).clamp(-8, 7) * s[..., None]  # [16, n, G, group]
+        err = (rec - w[None]).pow(2).sum(-1)                                  # [16, n, G]
+        best = err.argmin(0, keepdim=True)                                     # first minimum
+        out[r0:r0 + CLIP_ROWS] = s.gather(0, best)[0]
+    return out
+
+
 @torch.no_grad()
-def quantize_int4(w: torch.Tensor, group: int = GROUP):
-    """Symmetric round-to-nearest INT4: (packed uint8 [N, K/2], scale fp32 [N, K/group]); scale = amax / 7.
-    The reference's optional clip search (a calibration-time refinement) is not provided."""
+def quantize_int4(w: torch.Tensor, group: int = GROUP, clip_search: bool = False):
+    """Symmetric round-to-nearest INT4: (packed uint8 [N, K/2], scale fp32 [N, K/group]); scale = amax / 7, or with
+    clip_search the scale amax * a / 7, a in 0.70 .. 1.00 (16 steps), with the smallest squared reconstruction error
+    of its group (reference: src/lfm2opt/quant.py:21-39)."""
     N, K = w.shape
     assert K % group == 0
     wg = w.float().view(N, K // group, group)
-    scale = wg.abs().amax(-1).clamp_min(1e-12) / 7
+    amax = wg.abs().amax(-1).clamp_min(1e-12)
+    scale = _clip_scales(wg, amax) if clip_search else amax / 7
     q = torch.round(wg / scale[..., None]).clamp(-8, 7).to(torch.int16).view(N, K) + 8
     return ((q[:, 0::2] | (q[:, 1::2] << 4)).to(torch.uint8).contiguous(), scale.contiguous())
 

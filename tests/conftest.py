@@ -24,3 +24,20 @@ def cuda():
     if not torch.cuda.is_available():
         pytest.fail("GPU test selected but torch.cuda.is_available() is False")
     return torch.device("cuda", 0)
+
+
+@pytest.fixture
+def tune():
+    """tune(knob, value): force a launch configuration through lfm2q_set_tuning for the rest of the test; every knob
+    set is back to automatic afterwards."""
+    from lfm2opt import _capi
+
+    names = []
+
+    def set_knob(name, value):
+        _capi.set_tuning(name, value)
+        names.append(name)
+
+    yield set_knob
+    for name in names:
+        _capi.set_tuning(name, None)

@@ -75,3 +75,41 @@ def test_python_checks_match_reference_wording():
         E.set_gemv_impl(3)
     E.set_pdl(False)
     E.set_gemv_impl(0)
+
+
+def test_tuning_knobs_set_get_reset():
+    """lfm2q_set_tuning / lfm2q_get_tuning: 1-4 integers per knob, NULL or "" back to automatic, unknown names and
+    malformed values rejected with LFM2Q_ERR_ARG and a message (no GPU call involved)."""
+    from lfm2opt import _capi
+
+    _capi.set_tuning("LFM2Q_GEMV_MFMA", "1,2,8,2")
+    assert _capi.get_tuning("LFM2Q_GEMV_MFMA") == (1, 2, 8, 2)
+    _capi.set_tuning("LFM2Q_GEMM_RING", 644)
+    assert _capi.get_tuning("LFM2Q_GEMM_RING") == (644,)
+    _capi.set_tuning("LFM2Q_GEMV_WPC", "-3")
+    assert _capi.get_tuning("LFM2Q_GEMV_WPC") == (-3,)
+    for name in ("LFM2Q_GEMV_MFMA", "LFM2Q_GEMM_RING", "LFM2Q_GEMV_WPC"):
+        _capi.set_tuning(name, None)
+        assert _capi.get_tuning(name) == ()
+    _capi.set_tuning("LFM2Q_GEMM_BM", "")
+    assert _capi.get_tuning("LFM2Q_GEMM_BM") == ()
+    for bad in ("1,2,3,4,5", "x", "1,", "1,,2", "99999", "3 4"):
+        with pytest.raises(RuntimeError, match="expected 1 to 4 comma-separated integers"):
+            _capi.set_tuning("LFM2Q_GEMV_MFMA", bad)
+        assert _capi.get_tuning("LFM2Q_GEMV_MFMA") == ()  # a rejected value leaves the knob as it was
+    with pytest.raises(RuntimeError, match="unknown knob"):
+        _capi.set_tuning("LFM2Q_NO_SUCH_KNOB", "1")
+
+
+def test_every_documented_knob_exists():
+    """Each knob name the header lists is accepted by lfm2q_get_tuning."""
+    from lfm2opt import _capi
+
+    text = HEADER.read_text()
+    listed = re.search(r"Knob names: (.*?)\.\n", text, flags=re.S).group(1)
+    names = []
+    for prefix, body in re.findall(r"(LFM2Q_\w+?)_\{([^}]*)\}", listed):
+        names += [f"{prefix}_{n.strip()}" for n in body.split(",")]
+    assert len(names) >= 17
+    for n in names:
+        _capi.get_tuning(n)

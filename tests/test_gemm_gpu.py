@@ -149,15 +149,15 @@ TILES = [(256, 256), (128, 256), (256, 128), (128, 128), (128, 64), (64, 128), (
                          + [(bm, bn, 6, 1) for bm, bn in TILES if bm + bn <= 384]
                          + [(bm, bn, 3, 2) for bm, bn in TILES if bm + bn <= 384]
                          + [(bm, bn, 3, 4) for bm, bn in TILES if bm + bn <= 192])
-def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, monkeypatch):
+def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, tune):
     """Each kernel configuration (tile forced through LFM2Q_GEMM_BM / _BN, LDS ring depth through
     LFM2Q_GEMM_STAGES, K split over 1, 2 or 4 wavefront groups through LFM2Q_GEMM_KSPLIT) on shapes with M, N and K
     tails; with a K split also K whose stages divide unevenly (1104: 18 stages) and K with fewer stages than groups
     (96: 2 stages), where some groups have nothing to add. int32 accumulators exact, bf16 epilogue bit-exact."""
-    monkeypatch.setenv("LFM2Q_GEMM_BM", str(bm))
-    monkeypatch.setenv("LFM2Q_GEMM_BN", str(bn))
-    monkeypatch.setenv("LFM2Q_GEMM_STAGES", str(stages))
-    monkeypatch.setenv("LFM2Q_GEMM_KSPLIT", str(ksplit))
+    tune("LFM2Q_GEMM_BM", str(bm))
+    tune("LFM2Q_GEMM_BN", str(bn))
+    tune("LFM2Q_GEMM_STAGES", str(stages))
+    tune("LFM2Q_GEMM_KSPLIT", str(ksplit))
     M, N = 300, 520
     for K in (4304, 1104, 96) if ksplit > 1 else (4304,):
         xq, sx, wq, sw, b = _operands(bm * 7 + bn + K, M, K, N, True)
@@ -171,20 +171,20 @@ def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, monkeypatch):
 
 
 @pytest.mark.parametrize("bias,gelu", [(False, False), (True, True)])
-def test_gemm_persistent_big_tiles(E, bias, gelu, monkeypatch):
+def test_gemm_persistent_big_tiles(E, bias, gelu, tune):
     """The persistent 256 x 256 kernel with more tiles than workgroups (17 x 17 tiles on one workgroup per CU, so
     workgroups take a second tile whose first stage and epilogue operands load during the first tile's epilogue),
     with M, N and K tails: bf16 output against the oracle's epilogue of the exact int32 product (bit-exact, <= 1 ulp
     with GELU) and bit-identical to the one-tile-per-workgroup kernel (LFM2Q_GEMM_BIGP=0)."""
-    monkeypatch.setenv("LFM2Q_GEMM_BM", "256")
-    monkeypatch.setenv("LFM2Q_GEMM_BN", "256")
+    tune("LFM2Q_GEMM_BM", "256")
+    tune("LFM2Q_GEMM_BN", "256")
     M, K, N = 4100, 272, 4104
     xq, sx, wq, sw, b = _operands(M + N + int(gelu), M, K, N, bias)
     acc = oracle.gemm_i8_i32(xq, wq)
     ref = oracle.gemm_i8_epilogue(acc, sx, sw, b, gelu)
     outs = []
     for persistent in ("1", "0"):
-        monkeypatch.setenv("LFM2Q_GEMM_BIGP", persistent)
+        tune("LFM2Q_GEMM_BIGP", persistent)
         y = torch.full((M, N), 3.0, device="cuda", dtype=torch.bfloat16)
         E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), None if b is None else dev_bf16(b), y, gelu)
         outs.append(host_bits(y))
@@ -192,12 +192,12 @@ def test_gemm_persistent_big_tiles(E, bias, gelu, monkeypatch):
     assert np.array_equal(outs[0], outs[1])
 
 
-def test_gemm_big_tiles_unaligned_operands(E, monkeypatch):
+def test_gemm_big_tiles_unaligned_operands(E, tune):
     """256 x 256 tiles with a bias view 2 bytes off a 4-byte boundary and an output view 8 bytes off a 16-byte one:
     the launcher leaves the persistent kernel (dword bias loads, 16-byte staged stores) for the one-tile-per-workgroup
     kernel's predicated path; bf16 output still bit-exact against the oracle."""
-    monkeypatch.setenv("LFM2Q_GEMM_BM", "256")
-    monkeypatch.setenv("LFM2Q_GEMM_BN", "256")
+    tune("LFM2Q_GEMM_BM", "256")
+    tune("LFM2Q_GEMM_BN", "256")
     M, K, N = 520, 128, 520
     xq, sx, wq, sw, b = _operands(11, M, K, N, True)
     ref = oracle.gemm_i8_epilogue(oracle.gemm_i8_i32(xq, wq), sx, sw, b, False)

@@ -56,10 +56,10 @@ def test_gemm_grouped_vs_oracle(E, M, K, N, bias, gelu):
 
 
 @pytest.mark.parametrize("tile", ["128x128", "128x64", "64x128", "64x64"])
-def test_gemm_grouped_every_tile(E, tile, monkeypatch):
+def test_gemm_grouped_every_tile(E, tile, tune):
     bm, bn = tile.split("x")
-    monkeypatch.setenv("LFM2Q_GEMM_BM", bm)
-    monkeypatch.setenv("LFM2Q_GEMM_BN", bn)
+    tune("LFM2Q_GEMM_BM", bm)
+    tune("LFM2Q_GEMM_BN", bn)
     xq, sxT, wq, sw, b = operands(5, 200, 576, 264, True)
     y = run_grouped(E, xq, sxT, wq, sw, b, False)
     assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))

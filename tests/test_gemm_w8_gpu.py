@@ -50,13 +50,13 @@ def test_gemm_w8_vs_oracle(E, M, K, N, bias, gelu):
 
 @pytest.mark.parametrize("tile,ksplit", [(t, k) for t in ("128x128", "128x64", "64x128", "64x64") for k in (1, 2)]
                          + [("64x64", 4)])
-def test_gemm_w8_every_tile(E, tile, ksplit, monkeypatch):
+def test_gemm_w8_every_tile(E, tile, ksplit, tune):
     """Every tile with K split over 1, 2 or 4 wavefront groups (LFM2Q_GEMM_KSPLIT), with K = 576 (9 stages), 1104
     (18 stages, uneven split) and 128 (2 stages: some groups have nothing to add)."""
     bm, bn = tile.split("x")
-    monkeypatch.setenv("LFM2Q_GEMM_BM", bm)
-    monkeypatch.setenv("LFM2Q_GEMM_BN", bn)
-    monkeypatch.setenv("LFM2Q_GEMM_KSPLIT", str(ksplit))
+    tune("LFM2Q_GEMM_BM", bm)
+    tune("LFM2Q_GEMM_BN", bn)
+    tune("LFM2Q_GEMM_KSPLIT", str(ksplit))
     for K in (576, 1104, 128):
         x, W, sw, b = operands(3 + K, 200, K, 264, True)
         assert_close_bf16(run(E, x, W, sw, b, False), oracle.gemm_w8(x, W, sw, b),

@@ -17,7 +17,8 @@ from gpu_util import assert_close_bf16, dev, dev_bf16, host_bits
 
 pytestmark = pytest.mark.gpu
 
-DECODE_SHAPES = [(3072, 2048), (2048, 2048), (6144, 2048), (16384, 2048), (2048, 8192), (65536, 2048)]
+# the LFM2 decode step's GEMV shapes, plus the standalone 8192 x 2048 up-projection GEMV of the single-GEMV workload
+DECODE_SHAPES = [(3072, 2048), (2048, 2048), (6144, 2048), (8192, 2048), (16384, 2048), (2048, 8192), (65536, 2048)]
 
 
 @pytest.fixture(scope="module")
@@ -115,11 +116,11 @@ def _launch_batches(shape):
 
 @pytest.mark.parametrize("shape", MFMA_SHAPES)
 @pytest.mark.parametrize("wt", ["int8", "bf16"])
-def test_gemv_mfma_launch_shapes(E, monkeypatch, shape, wt):
+def test_gemv_mfma_launch_shapes(E, tune, shape, wt):
     """Every matrix-core launch shape (k-parts KS, row tiles RT, wavefronts NWK, batch tiles BT, forced through
     LFM2Q_GEMV_MFMA) against the oracle, with a trailing half block (K = 1088), N not a multiple of the tile rows and
     a partial last batch tile; the residual epilogue bit-identical to the plain GEMV + add."""
-    monkeypatch.setenv("LFM2Q_GEMV_MFMA", shape)
+    tune("LFM2Q_GEMV_MFMA", shape)
     N, K = 300, 1088
     g = torch.Generator().manual_seed(len(shape))
     for B in _launch_batches(shape):
@@ -155,7 +156,7 @@ def test_gemv_w8_rows_hint_same_result(E, rows):
 
 @pytest.mark.parametrize("wt,N,K", [("int8", 5000, 2048), ("int8", 3001, 8192), ("int8", 4000, 1024),
                                     ("bf16", 5000, 1024)])
-def test_gemv_persistent_matches_one_shot(E, monkeypatch, wt, N, K):
+def test_gemv_persistent_matches_one_shot(E, tune, wt, N, K):
     """Batch 1: the persistent kernel (forced with LFM2Q_GEMV_PERSIST=1; by default only for 131072+ rows at 8 wavefronts per CU) and the
     one-shot kernel give the same bits, plain, SwiGLU and residual, and match the oracle."""
     g = torch.Generator(device="cuda").manual_seed(N + K)
@@ -171,7 +172,7 @@ def test_gemv_persistent_matches_one_shot(E, monkeypatch, wt, N, K):
     W2, s2 = W[:2 * S].contiguous(), None if scale is None else scale[:2 * S].contiguous()
     res = {}
     for mode in ("1", "0"):
-        monkeypatch.setenv("LFM2Q_GEMV_PERSIST", mode)
+        tune("LFM2Q_GEMV_PERSIST", mode)
         y = torch.empty(1, N, device="cuda", dtype=torch.bfloat16)
         E.gemv(W, scale, x, y)
         a = torch.empty(1, S, device="cuda", dtype=torch.bfloat16)
@@ -308,3 +309,19 @@ def test_argument_errors_raise_before_launch(E):
     with pytest.raises(RuntimeError, match="short-conv"):
         E.gemv_epi(1, W, s, x, y)
     torch.cuda.synchronize()
+
+
+def test_single_gemv_8192x2048_full_oracle(E):
+    """The standalone decode up-projection: x bf16 [1, 2048] ~ N(0, 1), W int8 [8192, 2048] uniform over [-127, 127],
+    scale |N(0, 1)| 0.01 + 1e-3, y = bf16((x W^T) scale), seeded. Every output against the CPU oracle and against
+    the reference's PyTorch dequant-matmul (tests/test_kernels.py:137) evaluated on the CPU in fp32."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 2048, generator=g).to(torch.bfloat16)
+    W = torch.randint(-127, 128, (8192, 2048), generator=g, dtype=torch.int8)
+    scale = torch.randn(8192, generator=g).abs() * 0.01 + 1e-3
+    y = torch.empty(1, 8192, device="cuda", dtype=torch.bfloat16)
+    E.gemv(W.cuda(), scale.cuda(), x.cuda(), y)
+    out = host_bits(y)
+    assert_close_bf16(out, oracle.gemv(W.numpy(), scale.numpy(), host_bits(x)), what="gemv 8192x2048 vs oracle")
+    ref = F.linear(x.float(), W.float() * scale[:, None]).to(torch.bfloat16)
+    assert_close_bf16(out, host_bits(ref), what="gemv 8192x2048 vs CPU dequant-matmul")

@@ -101,23 +101,80 @@ def test_gemv_w4_vs_oracle(E, B, N, K, group):
     assert_close_bf16(run_ref(E, Wp, S, x), oracle.gemv_w4(Wp, S, x), what=f"gemv_w4 B={B} [{N}x{K}] g{group}")
 
 
-@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,2", "1,2,16", "1,4,2", "1,4,4", "2,1,1", "2,1,4", "2,1,16"])
-def test_gemv_w4_mfma_launch_shapes(E, monkeypatch, shape):
+@pytest.mark.parametrize("shape", ["1,1,1", "1,1,4", "1,2,2", "1,2,4", "1,2,16", "1,4,2", "1,4,4", "2,1,1", "2,1,4",
+                                   "2,1,16"])
+def test_gemv_w4_mfma_launch_shapes(E, tune, shape):
     """Every batch-2..16 launch shape of the matrix-core INT4 kernel (k-parts KS, row tiles RT, wavefronts NWK,
-    forced through LFM2Q_W4_MFMA) against the oracle, in both weight formats, with a trailing half block
-    (K = 1152) and N not a multiple of the tile rows; the residual epilogue bit-identical to the plain GEMV + add."""
-    monkeypatch.setenv("LFM2Q_W4_MFMA", shape)
+    forced through the LFM2Q_W4_MFMA knob), with a trailing half block (K = 1152) and N not a multiple of the tile
+    rows, in both weight formats and with every epilogue:
+      plain       against the oracle;
+      SwiGLU      (W = w1|w3, 2 N rows; RT = 2 puts two w1 and two w3 tiles in one workgroup) against the oracle, and
+                  bit-identical to the plain GEMV + silu_mul under the same shape (RT = 4 does not apply to SwiGLU,
+                  whose shape then differs from the plain call's, so only the oracle bar holds there);
+      residual    bit-identical to the plain GEMV + the bf16 add."""
+    tune("LFM2Q_W4_MFMA", shape)
     N, K, group = 300, 1152, 128
+    same_shape = shape.split(",")[1] != "4"
     for B in (3, 8) if shape.startswith("2") else (3, 13):
+        h0 = oracle.f2bf(np.random.default_rng(B).standard_normal((B, N)).astype(np.float32) * 4)
+        # reference format
         Wp, S, x = gen_ref(B + 7, B, N, K, group)
         y = run_ref(E, Wp, S, x)
         assert_close_bf16(y, oracle.gemv_w4(Wp, S, x), what=f"gemv_w4 shape {shape} B={B}")
-        h0 = oracle.f2bf(np.random.default_rng(B).standard_normal((B, N)).astype(np.float32) * 4)
-        ref_h = oracle.f2bf(oracle.bf2f(h0) + oracle.bf2f(y))
-        assert np.array_equal(run_ref(E, Wp, S, x, 2, h0), ref_h)
+        assert np.array_equal(run_ref(E, Wp, S, x, 2, h0), oracle.f2bf(oracle.bf2f(h0) + oracle.bf2f(y)))
+        W2, S2, x2 = gen_ref(B + 8, B, 2 * N, K, group)
+        sw = run_ref(E, W2, S2, x2, 1)
+        plain2 = run_ref(E, W2, S2, x2)
+        assert_close_bf16(sw, oracle.silu_mul(oracle.gemv_w4(W2, S2, x2)), what=f"gemv_w4 swiglu shape {shape} B={B}")
+        if same_shape:
+            assert np.array_equal(sw, oracle.silu_mul(plain2)), f"swiglu != gemv + silu_mul, shape {shape} B={B}"
+        # GPTQ-style format
         Wq, Sz, Z, xz = gen_zp(B + 9, B, N, K, group)
-        assert_close_bf16(run_zp(E, Wq, Sz, Z, xz), oracle.gemv_w4z(Wq, Sz, Z, xz, group),
-                          what=f"gemv_w4z shape {shape} B={B}")
+        yz = run_zp(E, Wq, Sz, Z, xz)
+        assert_close_bf16(yz, oracle.gemv_w4z(Wq, Sz, Z, xz, group), what=f"gemv_w4z shape {shape} B={B}")
+        assert np.array_equal(run_zp(E, Wq, Sz, Z, xz, 2, h0), oracle.f2bf(oracle.bf2f(h0) + oracle.bf2f(yz)))
+        Wq2, Sz2, Z2, xz2 = gen_zp(B + 10, B, 2 * N, K, group)
+        swz = run_zp(E, Wq2, Sz2, Z2, xz2, 1)
+        assert_close_bf16(swz, oracle.gemv_w4z(Wq2, Sz2, Z2, xz2, group, swiglu=True),
+                          what=f"gemv_w4z swiglu shape {shape} B={B}")
+        if same_shape:
+            assert np.array_equal(swz, oracle.silu_mul(run_zp(E, Wq2, Sz2, Z2, xz2)))
+
+
+@pytest.mark.parametrize("B", [2, 8, 16])
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_gemv_w4_swiglu_two_row_tiles_at_w13_shape(E, B, fmt):
+    """w1|w3 at its decode shape (16384 x 2048) at batches 2-16: the automatic launch takes two row tiles per
+    workgroup (6144+ weight rows), the path config 5's batch-8 decode step runs. Against the oracle on 64 sampled
+    output rows, and bit-identical to the plain GEMV + silu_mul."""
+    Sn, K, group = 8192, 2048, 128
+    r = np.random.default_rng(90 + B + fmt)
+    rows = np.sort(r.permutation(Sn)[:64])
+    wr = np.concatenate([rows, Sn + rows])
+    if fmt == 0:
+        Wp, S, x = gen_ref(91 + B, B, 2 * Sn, K, group)
+        fused, plain = run_ref(E, Wp, S, x, 1), run_ref(E, Wp, S, x, 0)
+        ref = oracle.silu_mul(oracle.gemv_w4(Wp[wr], S[wr], x))
+    else:
+        Wq, S, Z, x = gen_zp(92 + B, B, 2 * Sn, K, group)
+        fused, plain = run_zp(E, Wq, S, Z, x, 1), run_zp(E, Wq, S, Z, x, 0)
+        ref = oracle.gemv_w4z(Wq[wr], S[wr], Z[wr], x, group, swiglu=True)
+    assert_close_bf16(fused[:, rows], ref, what=f"w4 fmt {fmt} w1|w3 swiglu B={B} sampled rows")
+    assert np.array_equal(fused, oracle.silu_mul(plain))
+
+
+@pytest.mark.parametrize("B", [1, 4, 8, 16])
+def test_gemv_w4z_residual_vs_oracle_and_add(E, B):
+    """The GPTQ-style residual epilogue at the w2 and out-proj shapes: against the oracle's GEMV + bf16 add on 64
+    sampled rows, and bit-identical to the library's plain GEMV + the bf16 add."""
+    for N, K in ((2048, 8192), (2048, 2048)):
+        Wq, S, Z, x = gen_zp(95 + B + K, B, N, K, 128)
+        h0 = oracle.f2bf(np.random.default_rng(B + K).standard_normal((B, N)).astype(np.float32) * 4)
+        fused, plain = run_zp(E, Wq, S, Z, x, 2, h0), run_zp(E, Wq, S, Z, x, 0)
+        assert np.array_equal(fused, oracle.f2bf(oracle.bf2f(h0) + oracle.bf2f(plain)))
+        rows = np.sort(np.random.default_rng(K).permutation(N)[:64])
+        ref = oracle.f2bf(oracle.bf2f(h0[:, rows]) + oracle.bf2f(oracle.gemv_w4z(Wq[rows], S[rows], Z[rows], x, 128)))
+        assert_close_bf16(fused[:, rows], ref, what=f"gemv_w4z residual B={B} [{N}x{K}] sampled rows")
 
 
 @pytest.mark.parametrize("B", [1, 3, 8, 17])
@@ -225,7 +282,7 @@ def test_w4_argument_errors_raise_before_launch(E):
 
 @pytest.mark.parametrize("fmt", [0, 1])
 @pytest.mark.parametrize("N,K,group", [(3001, 2048, 128), (130, 4096, 128), (257, 8192, 128), (77, 1024, 64)])
-def test_one_shot_matches_persistent(E, monkeypatch, fmt, N, K, group):
+def test_one_shot_matches_persistent(E, tune, fmt, N, K, group):
     """Batch 1: the one-shot kernel (LFM2Q_W4_ONESHOT=1, the default below 32768 weight rows) and the persistent
     kernel (LFM2Q_W4_ONESHOT=0) give the same bits, plain, SwiGLU and residual, in both weight formats."""
     h0 = oracle.f2bf(np.random.default_rng(N).standard_normal((1, N)).astype(np.float32) * 4)
@@ -237,7 +294,7 @@ def test_one_shot_matches_persistent(E, monkeypatch, fmt, N, K, group):
         runs = lambda epi, h=None, n=N: run_zp(E, Wq[:n], S[:n], Z[:n], x, epi, h)  # noqa: E731
     res = {}
     for mode in ("1", "0"):
-        monkeypatch.setenv("LFM2Q_W4_ONESHOT", mode)
+        tune("LFM2Q_W4_ONESHOT", mode)
         res[mode] = (runs(0), runs(1, n=2 * (N // 2)), runs(2, h0))
     for a, b in zip(res["1"], res["0"]):
         assert np.array_equal(a, b)

@@ -89,3 +89,50 @@ def test_oracle_gemv_w4z_reads_the_packed_layout():
     exact = oracle.bf2f(x).astype(np.float64) @ deq.T
     got = oracle.bf2f(y).astype(np.float64)
     assert np.all(np.abs(got - exact) <= np.abs(exact) * 2.0 ** -8 + 1e-6)
+
+
+def _int4_sq_err(wg, s):
+    """fp64 squared error of the symmetric INT4 reconstruction of each group with scale s (brute force)."""
+    q = np.clip(np.round(wg / s[..., None]), -8, 7)
+    return ((q * s[..., None] - wg) ** 2).sum(-1)
+
+
+def test_quantize_int4_clip_search_brute_force():
+    """clip_search (src/lfm2opt/quant.py:23-35): per group the chosen scale is one of the 16 candidates amax * a / 7,
+    a in linspace(0.70, 1.00, 16), and no candidate reconstructs the group with a smaller squared error (checked in
+    fp64 over every candidate); groups with one large outlier pick a clipped scale (a < 1); the packed weights are
+    round(w / s) of the chosen scale; without the search the scale stays amax / 7."""
+    N, K, group = 6, 512, 128
+    w = torch.randn(N, K, generator=G) * 0.02
+    w[1, 5] = 0.5   # outliers: clipping the rest of the group lowers the error
+    w[4, 300] = -0.4
+    packed, s = quant.quantize_int4(w, group, True)
+    _, s_plain = quant.quantize_int4(w, group, False)
+    wg = w.double().numpy().reshape(N, K // group, group)
+    amax = np.maximum(np.abs(w.float().numpy().reshape(N, K // group, group)).max(-1), 1e-12).astype(np.float32)
+    fr = torch.linspace(0.70, 1.00, 16).numpy()
+    cands = np.stack([amax * np.float32(a) / np.float32(7) for a in fr])        # fp32 arithmetic, as the search
+    errs = np.stack([_int4_sq_err(wg, c.astype(np.float64)) for c in cands])   # [16, N, G]
+    sn = s.numpy()
+    chosen = (cands == sn[None]).argmax(0)
+    assert ((cands == sn[None]).any(0)).all(), "scale is not one of the candidates"
+    best = errs.min(0)
+    got = np.take_along_axis(errs, chosen[None], 0)[0]
+    assert (got <= best * (1 + 1e-6) + 1e-18).all()
+    assert chosen[1, 0] < 15 and chosen[4, 2] < 15  # the outlier groups are clipped
+    assert torch.equal(s_plain, (w.abs().view(N, -1, group).amax(-1).clamp_min(1e-12) / 7))
+    p = packed.numpy().astype(np.int64)
+    q = np.empty((N, K), np.int64)
+    q[:, 0::2], q[:, 1::2] = (p & 15) - 8, (p >> 4) - 8
+    ref = np.clip(np.round(w.numpy().reshape(N, -1, group) / sn[..., None]), -8, 7).reshape(N, K)
+    assert np.array_equal(q, ref)
+
+
+def test_quantize_int4_clip_search_row_chunks():
+    """The search runs over row chunks: a matrix larger than one chunk gives the rows of the chunked and the
+    one-chunk searches the same scales."""
+    w = torch.randn(2 * quant.CLIP_ROWS + 3, 256, generator=G) * 0.02
+    _, s_all = quant.quantize_int4(w, 128, True)
+    for r0 in (0, quant.CLIP_ROWS - 1, 2 * quant.CLIP_ROWS):
+        _, s_part = quant.quantize_int4(w[r0:r0 + 2], 128, True)
+        assert torch.equal(s_all[r0:r0 + 2], s_part)
