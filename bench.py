@@ -103,8 +103,9 @@ class DecodeStep:
         self.bcx = torch.empty(B, CONV_IN, device=device, dtype=bf)
         self.act = torch.empty(B, FFN, device=device, dtype=bf)
         self.logits = torch.empty(B, VOCAB, device=device, dtype=bf)
-        self.ops = []      # (kind, fn, bytes)
-        self.weights = []  # keep alive
+        self.ops = []        # (kind, fn, bytes)
+        self.weights = []    # keep alive
+        self.chain_ops = []  # the same GEMVs as (epi, W, scale, x, y) for the one-launch chain (batch 1)
         for t in LAYER_TYPES:
             if t == "A":
                 Wq, sq = w8(QKV, H)
@@ -112,6 +113,7 @@ class DecodeStep:
                 self.ops.append(("qkv", lambda W=Wq, s=sq: E.gemv(W, s, self.x, self.qkv), gemv_bytes(QKV, H, B)))
                 self.ops.append(("o+res", lambda W=Wo, s=so: E.gemv_residual(W, s, self.mix, self.h),
                                  gemv_bytes(H, H, B, True)))
+                self.chain_ops += [(0, Wq, sq, self.x, self.qkv), (2, Wo, so, self.mix, self.h)]
                 self.weights += [Wq, sq, Wo, so]
             else:
                 Wi, si = w8(CONV_IN, H)
@@ -119,6 +121,7 @@ class DecodeStep:
                 self.ops.append(("in", lambda W=Wi, s=si: E.gemv(W, s, self.x, self.bcx), gemv_bytes(CONV_IN, H, B)))
                 self.ops.append(("out+res", lambda W=Wc, s=sc: E.gemv_residual(W, s, self.mix, self.h),
                                  gemv_bytes(H, H, B, True)))
+                self.chain_ops += [(0, Wi, si, self.x, self.bcx), (2, Wc, sc, self.mix, self.h)]
                 self.weights += [Wi, si, Wc, sc]
             W13, s13 = w8(2 * FFN, H)
             W2, s2 = w8(H, FFN)
@@ -126,9 +129,11 @@ class DecodeStep:
                              swiglu_bytes(FFN, H, B)))
             self.ops.append(("w2+res", lambda W=W2, s=s2: E.gemv_residual(W, s, self.act, self.h),
                              gemv_bytes(H, FFN, B, True)))
+            self.chain_ops += [(1, W13, s13, self.x, self.act), (2, W2, s2, self.act, self.h)]
             self.weights += [W13, s13, W2, s2]
         Wh, sh = w8(VOCAB, H)
         self.ops.append(("lm_head", lambda: E.gemv(Wh, sh, self.x, self.logits), gemv_bytes(VOCAB, H, B)))
+        self.chain_ops.append((0, Wh, sh, self.x, self.logits))
         self.weights += [Wh, sh]
         self.bytes = sum(b for _, _, b in self.ops)
         self.weight_bytes = sum(w.numel() * w.element_size() for w in self.weights if w.dtype == torch.int8)
@@ -320,6 +325,8 @@ def decode_results(B, steps, warmup, wfmt="int8"):
         del g
     res["kinds"] = kinds
     log(f"decode step ({wfmt}), batch {B}: {ms * 1e3:.1f} us/step, {res['gbs']:.0f} GB/s")
+    if wfmt == "int8" and B == 1:
+        res["chain"] = chain_results(step, steps, warmup)
     del graph, step
     torch.cuda.empty_cache()
     return res
@@ -378,6 +385,22 @@ def single_gemv_results(reps, cpu=True):
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"one 8192 x 2048 GEMV, F.linear(x.float(), Wq.float() * scale[:, None])"
                                          f".to(bf16) with the dequant inside the timed region, median of {n}"}
+    return res
+
+
+def chain_results(step, steps, warmup):
+    """The same 65 GEMVs as one lfm2q_gemv_chain launch (each op waits on the device for the one before it, the
+    weights of later ops streaming meanwhile), captured into a HIP graph of one node; a step is one replay."""
+    from lfm2opt.kernels import ext
+
+    chain = ext().gemv_chain(step.chain_ops)
+    graph = capture(chain)
+    ms, wall = time_graph(graph, steps, warmup)
+    expired = chain.wait_expired()
+    res = {"ms_per_step": ms, "wall_ms_per_step": wall, "bytes_per_step": step.bytes, "gbs": step.bytes / ms / 1e6,
+           "hbm_frac": step.bytes / ms / 1e6 / HBM_PEAK_GBS, "launches": 1, "ops": chain.n, "wait_expired": expired}
+    log(f"decode chain, batch 1: {ms * 1e3:.1f} us/step, {res['gbs']:.0f} GB/s" + (" WAIT EXPIRED" if expired else ""))
+    del graph, chain
     return res
 
 

@@ -17,6 +17,7 @@
 #ifndef LFM2Q_H
 #define LFM2Q_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -98,6 +99,35 @@ int lfm2q_gemv_residual(int wtype, const void *W, const float *scale, const lfm2
  * which is fmt 0, epi 0 and batch 1 only). */
 int lfm2q_gemv_w4(int fmt, const void *Wq, const void *S, const int32_t *Z, const lfm2q_bf16 *x, lfm2q_bf16 *y,
                   int B, int N, int K, int group, int epi, lfm2q_stream_t stream);
+
+/* One GEMV of a chain: batch 1, int8 W [R, K] (R = N, or 2N = w1|w3 for epi 1) with fp32 scale [R], bf16 x [K],
+ * bf16 y [N]. epi 0: y = bf16(acc * s); epi 1: the SwiGLU of lfm2q_gemv_swiglu; epi 2: y = bf16(y + bf16(acc * s))
+ * in place (lfm2q_gemv_residual). */
+typedef struct lfm2q_gemv_op {
+    const void *W;
+    const float *scale;
+    const lfm2q_bf16 *x;
+    lfm2q_bf16 *y;
+    int32_t N, K, epi, reserved;
+} lfm2q_gemv_op;
+
+/* Bytes of the workspace lfm2q_gemv_chain needs (a few KiB). */
+size_t lfm2q_gemv_chain_workspace_bytes(void);
+
+/* A decode step's GEMVs as one launch: ops[0 .. n_ops-1] in order, where op j may read anything ops 0 .. j-1
+ * wrote (its inputs are read only after every output of op j - 1 is written). Each output is bit-identical to the
+ * separate lfm2q_gemv_w8 / lfm2q_gemv_swiglu / lfm2q_gemv_residual call on the same inputs. The weights of later
+ * ops stream while an op waits for its inputs, which hides the per-GEMV launch and memory-latency cost.
+ * ops: the table on the host (checked there); ops_dev: the same n_ops descriptors in device memory (the kernel
+ * reads these; 16-byte aligned). K in {1024, 2048, 4096, 8192}, N <= 512 x the CU count, n_ops <= 128.
+ * workspace: lfm2q_gemv_chain_workspace_bytes() of device memory, 256-byte aligned, zero-filled before its first
+ * use and then left alone (it carries a launch counter between calls); calls sharing a workspace must be ordered
+ * (one stream). Word 1 of the workspace (uint32) becomes nonzero if a dependency wait ran out (20 ms, e.g. because
+ * not every workgroup of the launch could be resident); the outputs of that launch are then undefined.
+ * No counterpart entry point in the reference, which chains separate launches with programmatic dependent launch
+ * (kernels/lfm2_decode.cu:24-62, the weight prefetch before the dependency wait at :500-512, :600-609). */
+int lfm2q_gemv_chain(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops, void *workspace,
+                     size_t workspace_bytes, lfm2q_stream_t stream);
 
 /* y[b, i] = bf16( bf16(silu(g[b, i])) * g[b, I + i] ), g bf16 [B, 2I], y bf16 [B, I].
  * Replaces launch_silu_mul kernels/lfm2_decode.cu:954-969 (bound as silu_mul(), kernels/lfm2_decode.cpp:100-103). */

@@ -1,0 +1,387 @@
+// A chain of batch-1 weight-only INT8 GEMVs (a decode step's linears) as one persistent launch on gfx950.
+//
+// Op j of the chain is y_j = epi(x_j W_j^T s_j) (plain, SwiGLU over w1|w3, or residual add into y_j), and op j may
+// read anything ops 0 .. j-1 wrote: op j's math starts only once every output of op j - 1 is written. Launched as
+// separate kernels, each GEMV pays a kernel boundary and then its first HBM round trip before any weight arrives
+// (~1.6 us + ~2 us for a 4-34 MB matrix). Here the weights -- which never depend on an earlier op -- are streamed
+// continuously across op boundaries, and only the activations wait for the dependency:
+//
+//   * One workgroup per CU (grid = CU count, every workgroup resident at once), output rows of each op split evenly
+//     over the workgroups, whole rows dealt round-robin to the 4 compute wavefronts of a workgroup.
+//   * Each compute wavefront streams its rows' weights, 1 KiB (16 bytes per lane) per load, straight into a private
+//     ring of 32 LDS slots with buffer_load_dwordx4 ... lds, running up to 32 KiB ahead of its math, across op
+//     boundaries (128 KiB in flight per CU, 32 MiB over the chip: ~5 us of HBM time, which covers a dependency
+//     wait). Its vector memory counter tracks nothing but the ring, so "slot p has landed" is a constant
+//     s_waitcnt vmcnt(32 - B) before every item of B slots, followed by B refills.
+//   * A fifth wavefront does all other memory traffic: it waits for the previous op (below), stages x_j, the
+//     scales and the residual rows of the workgroup's outputs into LDS, and after the compute wavefronts are done
+//     stores the outputs and publishes the op's completion.
+//   * Completion: workgroup g writes its outputs with device-coherent stores (sc1, written through to the memory
+//     side), waits for them (s_waitcnt vmcnt(0)), then stores flag[g] = epoch(j). A waiter polls the flags of all
+//     workgroups with device-coherent loads until each has reached epoch(j), and reads every input of op j + 1
+//     with device-coherent loads. No cache-wide writeback or invalidate, no read-modify-write atomics.
+//   * epoch(j) = gen * 1024 + j + 1 for the gen-th launch on a workspace (gen is read at the start, incremented
+//     once all workgroups have read it), compared as a wrapping difference, so the flags never need resetting.
+//     Every wait is bounded (20 ms of the real-time counter): a wait that runs out sets the workspace's error word,
+//     and from then on every wait of every workgroup returns at once, so the kernel always finishes.
+//
+// Per row the arithmetic is exactly the batch-1 GEMV kernels' (gemv_math.hpp: lane l owns 16-byte chunk l + 64 u of
+// the row, chunk products on v_dot2_f32_bf16 in order of u, fold_sum over the lanes, the same epilogue), so each
+// output is bit-identical to the separate lfm2q_gemv_w8 / _swiglu / _residual call on the same inputs.
+//
+// Reference: the reference overlaps consecutive decode GEMVs with programmatic dependent launch
+// (kernels/lfm2_decode.cu:24-62): a kernel prefetches its weights before griddepcontrol.wait (:500-512, :600-609).
+#include "common.hpp"
+#include "gemv_math.hpp"
+#include "status.hpp"
+
+#include <algorithm>
+
+namespace lfm2q {
+namespace {
+
+constexpr int CW = 4;                 // compute wavefronts per workgroup
+constexpr int SLOTS = 32;             // 1 KiB ring slots per compute wavefront
+constexpr int UNIT = 1024;            // bytes per slot: one wavefront load, 16 bytes per lane
+constexpr int MAX_K = 8192;
+constexpr int MAX_ROWS = 512;         // output rows of one op per workgroup
+constexpr int MAX_OPS = 128;          // ops per launch (the op table lives in LDS)
+constexpr uint32_t EPOCHS = 1024;
+constexpr int MAX_G = 1024;           // workgroups (= CUs)
+constexpr int WS_GEN = 0, WS_ERR = 1; // workspace words; the flags start 128 bytes in
+constexpr int WS_FLAGS = 32;
+constexpr uint64_t WAIT_TICKS = 2000000;  // 20 ms at the 100 MHz s_memrealtime clock
+constexpr int AUX_SC1 = 16;           // device-scope coherent access (sc1)
+
+struct ChainOp {
+    const int8_t *W;
+    const float *scale;
+    const uint16_t *x;
+    uint16_t *y;
+    int N, K, epi, reserved;
+};
+static_assert(sizeof(ChainOp) == sizeof(lfm2q_gemv_op), "descriptor layout");
+
+struct Lds {
+    uint8_t ring[CW][SLOTS][UNIT];  // 128 KiB
+    ChainOp ops[MAX_OPS];           // the op table (6 KiB)
+    uint16_t xs[MAX_K];             // x_j
+    float sc[2][MAX_ROWS];          // scales of the workgroup's rows (w1, w3 for SwiGLU)
+    uint16_t hs[MAX_ROWS];          // residual rows (epi 2)
+    uint16_t outs[MAX_ROWS];        // results, stored by the sync wavefront
+};
+
+__device__ __forceinline__ void rows_of(int N, int g, int G, int &r0, int &r1) {
+    r0 = (int)((long)g * N / G);
+    r1 = (int)((long)(g + 1) * N / G);
+}
+
+// a pointer read from LDS as a wavefront-uniform (scalar) value; readfirstlane returns int, so each half goes
+// back through uint32_t before widening (a sign-extended low half would corrupt the address)
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<T *>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Device-coherent accesses through a buffer resource.
+__device__ __forceinline__ v4u ld_dev16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_SC1));
+}
+__device__ __forceinline__ uint32_t ld_dev4(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX_SC1);
+}
+__device__ __forceinline__ uint16_t ld_dev2(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, AUX_SC1);
+}
+__device__ __forceinline__ void st_dev4(uint32_t v, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, AUX_SC1);
+}
+__device__ __forceinline__ void st_dev2(uint16_t v, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)off, 0, AUX_SC1);
+}
+
+// The weight stream of one compute wavefront: op by op, the wavefront's items t = r0 + w, r0 + w + CW, ... < r1,
+// per item its NROW weight rows (row t, and S + t for SwiGLU), per row its K / 1024 units. Every member is
+// wavefront-uniform (scalar registers); past the last op every load reads zeros through an empty range.
+struct Loader {
+    const ChainOp *ops;  // the LDS copy
+    int n_ops, g, G, w;
+    int j;
+    v4i desc;
+    uint32_t rowb;
+    int cpl, nrow, S, t, t_end, r, u;
+
+    __device__ __forceinline__ void open(int from) {
+        for (j = from; j < n_ops; ++j) {
+            const int N = __builtin_amdgcn_readfirstlane(ops[j].N);
+            int r0, r1;
+            rows_of(N, g, G, r0, r1);
+            t = r0 + w;
+            t_end = r1;
+            if (t < t_end) {
+                const int K = __builtin_amdgcn_readfirstlane(ops[j].K);
+                nrow = __builtin_amdgcn_readfirstlane(ops[j].epi) == EPI_SWIGLU ? 2 : 1;
+                S = N;
+                rowb = (uint32_t)K;
+                cpl = K / UNIT;
+                r = u = 0;
+                desc = make_desc(uniform_ptr(ops[j].W), (uint32_t)(nrow * N) * rowb);
+                return;
+            }
+        }
+        // past the last op: an empty range over a valid base (the last op's weights), so every load reads zeros
+        // without touching memory
+        desc = make_desc(uniform_ptr(ops[n_ops - 1].W), 0u);
+    }
+    __device__ __forceinline__ uint32_t offset() const {
+        return j < n_ops ? (uint32_t)(r ? S + t : t) * rowb + (uint32_t)u * UNIT : 0u;
+    }
+    __device__ __forceinline__ void advance() {
+        if (j >= n_ops) return;
+        if (++u < cpl) return;
+        u = 0;
+        if (++r < nrow) return;
+        r = 0;
+        t += CW;
+        if (t < t_end) return;
+        open(j + 1);
+    }
+    __device__ __forceinline__ void issue(void *slot, int lane) {
+        // the resource must reach the instruction in scalar registers (an asm operand is not moved there by itself)
+        const v4i d = {__builtin_amdgcn_readfirstlane(desc[0]), __builtin_amdgcn_readfirstlane(desc[1]),
+                       __builtin_amdgcn_readfirstlane(desc[2]), __builtin_amdgcn_readfirstlane(desc[3])};
+        lds_dma16(d, (uint32_t)lane * 16u + offset(), lds_addr(slot));
+    }
+    // the next n units of the stream into the ring slots from position p on (a loop, not unrolled: one copy of
+    // advance() per call site)
+    __device__ __forceinline__ void issue_n(Lds &L, uint32_t p, int n, int lane);
+};
+
+__device__ __forceinline__ void Loader::issue_n(Lds &L, uint32_t p, int n, int lane) {
+#pragma nounroll
+    for (int b = 0; b < n; ++b) {
+        issue(L.ring[w][(p + b) & (SLOTS - 1)], lane);
+        advance();
+    }
+}
+
+// Wait until at most SLOTS - B ring loads are outstanding: the B oldest (the next item's slots) have landed.
+__device__ __forceinline__ void wait_ring(int B) {
+    switch (B) {
+        case 1: wait_vm<SLOTS - 1>(); break;
+        case 2: wait_vm<SLOTS - 2>(); break;
+        case 4: wait_vm<SLOTS - 4>(); break;
+        case 8: wait_vm<SLOTS - 8>(); break;
+        default: wait_vm<SLOTS - 16>(); break;
+    }
+}
+
+// One op's items of a compute wavefront. An item is one output row: its weight row (w1 and w3 rows for SwiGLU),
+// cpl units each. Items go in groups whose row sums fill the 8 values of one fold_sum (8 items, or 4 SwiGLU items
+// = 4 w1 + 4 w3 sums); before each item its B = nrow cpl slots are waited for, read, and refilled with the next B
+// units of the stream. One routine for every K and epilogue (run-time cpl, epi; fixed-size register arrays
+// indexed by unrolled loop counters).
+__device__ __forceinline__ void chain_items(Lds &L, Loader &ld, uint32_t &pos, int lane, int w, int r0, int r1,
+                                            int cpl, int epi) {
+    using D = PairDot<int8_t>;
+    const bool swiglu = epi == EPI_SWIGLU;
+    const int B = swiglu ? 2 * cpl : cpl;
+    const int per_group = swiglu ? 4 : 8;
+    v4i xr[8][2];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        if (u < cpl)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                xr[u][q] = *reinterpret_cast<const v4i *>(&L.xs[(lane + 64 * u) * 16 + 8 * q]);
+    for (int t0 = r0 + w; t0 < r1; t0 += per_group * CW) {
+        float part[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part[i] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (i >= per_group || t0 + i * CW >= r1) continue;
+            v4i c1[8], c2[8];  // the item's w1 (or only) row and, for SwiGLU, its w3 row
+            wait_ring(B);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (u < cpl) c1[u] = *reinterpret_cast<const v4i *>(&L.ring[w][(pos + u) & (SLOTS - 1)][16 * lane]);
+            if (swiglu)
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (u < cpl)
+                        c2[u] = *reinterpret_cast<const v4i *>(&L.ring[w][(pos + cpl + u) & (SLOTS - 1)][16 * lane]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slots are read before they refill
+            ld.issue_n(L, pos, B, lane);
+            pos += B;
+            float a = 0.f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (u < cpl) a = D::dot(c1[u], xr[u], a);
+            part[i] = a;
+            if (swiglu) {
+                float a3 = 0.f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (u < cpl) a3 = D::dot(c2[u], xr[u], a3);
+                part[(4 + i) & 7] = a3;
+            }
+        }
+        const float rs = fold_sum<8>(part);  // value v in lanes 8 v .. 8 v + 7
+        // SwiGLU: the w3 sum of item i (value 4 + i) sits 32 lanes above its w1 sum (value i)
+        const float ru = __uint_as_float(
+            __builtin_amdgcn_permlane32_swap(__float_as_uint(rs), __float_as_uint(rs), false, false)[1]);
+        const int i = lane >> 3, t = t0 + i * CW;
+        if ((lane & 7) == 0 && i < per_group && t < r1) {
+            const int k = t - r0;
+            const float sg = L.sc[0][k];
+            uint16_t v;
+            if (epi == EPI_SWIGLU)
+                v = gemv_epilogue<EPI_SWIGLU>(rs, sg, ru, L.sc[1][k], 0u, true);
+            else if (epi == EPI_RESIDUAL)
+                v = gemv_epilogue<EPI_RESIDUAL>(rs, sg, 0.f, 1.f, L.hs[k], true);
+            else
+                v = gemv_epilogue<EPI_NONE>(rs, sg, 0.f, 1.f, 0u, true);
+            L.outs[k] = v;
+        }
+    }
+}
+
+// Wait until every workgroup's flag has reached `target`, or the error word is set, or the bound runs out (which
+// sets the error word). One 16-byte coherent load covers 4 flags per lane.
+__device__ __forceinline__ void wait_flags(rsrc_t wsr, int G, uint32_t target, int lane) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        bool ok = true;
+        for (int b = 4 * lane; b < G; b += 256) {
+            const v4u f = ld_dev16(wsr, (uint32_t)(WS_FLAGS + b) * 4u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ok = ok && (b + e >= G || (int)(f[e] - target) >= 0);
+        }
+        const uint32_t err = ld_dev4(wsr, WS_ERR * 4);
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0 || err) return;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > WAIT_TICKS) {
+            if (lane == 0) st_dev4(1u, wsr, WS_ERR * 4);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+__global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp *__restrict__ ops, int n_ops,
+                                                                   uint32_t *__restrict__ ws, int G) {
+    __shared__ __attribute__((aligned(1024))) Lds L;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = blockIdx.x;
+    const rsrc_t wsr = make_rsrc(ws, (uint32_t)(WS_FLAGS + MAX_G) * 4u);
+    // the op table into LDS, before any wavefront starts its loads
+    for (int i = threadIdx.x; i < n_ops * (int)(sizeof(ChainOp) / 16); i += blockDim.x)
+        reinterpret_cast<v4i *>(L.ops)[i] = reinterpret_cast<const v4i *>(ops)[i];
+    __syncthreads();
+
+    if (w == CW) {  // ------------------------------------------------------------------ the sync wavefront
+        const uint32_t gen = __builtin_amdgcn_readfirstlane(ld_dev4(wsr, WS_GEN * 4));
+        for (int j = 0; j < n_ops; ++j) {
+            if (j) wait_flags(wsr, G, gen * EPOCHS + (uint32_t)j, lane);  // op j - 1 complete everywhere
+            const int N = __builtin_amdgcn_readfirstlane(L.ops[j].N), K = __builtin_amdgcn_readfirstlane(L.ops[j].K);
+            const int epi = __builtin_amdgcn_readfirstlane(L.ops[j].epi);
+            const float *scale = uniform_ptr(L.ops[j].scale);
+            int r0, r1;
+            rows_of(N, g, G, r0, r1);
+            const int nr = r1 - r0;
+            const rsrc_t xr = make_rsrc(uniform_ptr(L.ops[j].x), (uint32_t)K * 2u);
+            for (int off = 16 * lane; off < K * 2; off += 1024)
+                *reinterpret_cast<v4u *>(reinterpret_cast<uint8_t *>(L.xs) + off) = ld_dev16(xr, (uint32_t)off);
+            for (int i = lane; i < nr; i += 64) {
+                L.sc[0][i] = scale[r0 + i];
+                if (epi == EPI_SWIGLU) L.sc[1][i] = scale[N + r0 + i];
+            }
+            const rsrc_t yr = make_rsrc(uniform_ptr(L.ops[j].y), (uint32_t)N * 2u);
+            if (epi == EPI_RESIDUAL)
+                for (int i = lane; i < nr; i += 64) L.hs[i] = ld_dev2(yr, (uint32_t)(r0 + i) * 2u);
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            wg_barrier();  // A_j: op j's inputs are in LDS
+            wg_barrier();  // B_j: op j's outputs are in LDS
+            for (int i = lane; i < nr; i += 64) st_dev2(L.outs[i], yr, (uint32_t)(r0 + i) * 2u);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the outputs are written before the flag
+            if (lane == 0) st_dev4(gen * EPOCHS + (uint32_t)j + 1u, wsr, (uint32_t)(WS_FLAGS + g) * 4u);
+        }
+        if (g == 0) {  // once every workgroup is past the last op (so has read gen), advance gen for the next launch
+            wait_flags(wsr, G, gen * EPOCHS + (uint32_t)n_ops, lane);
+            if (lane == 0) st_dev4(gen + 1u, wsr, WS_GEN * 4);
+        }
+        return;
+    }
+
+    // ------------------------------------------------------------------------------------ compute wavefronts
+    Loader ld{L.ops, n_ops, g, G, w, 0, {}, 0u, 0, 0, 0, 0, 0, 0, 0};
+    ld.open(0);
+    ld.issue_n(L, 0u, SLOTS, lane);
+    uint32_t pos = 0;  // next stream position to consume; pos + SLOTS have been issued
+    for (int j = 0; j < n_ops; ++j) {
+        wg_barrier();  // A_j
+        const int N = __builtin_amdgcn_readfirstlane(L.ops[j].N), epi = __builtin_amdgcn_readfirstlane(L.ops[j].epi);
+        const int cpl = __builtin_amdgcn_readfirstlane(L.ops[j].K) / UNIT;
+        int r0, r1;
+        rows_of(N, g, G, r0, r1);
+        chain_items(L, ld, pos, lane, w, r0, r1, cpl, epi);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // outs written
+        wg_barrier();  // B_j
+    }
+    wait_vm<0>();  // the ring's trailing loads (empty ranges past the last op) before the wavefront ends
+}
+
+int check_op(const lfm2q_gemv_op &o, int j, int G) {
+    LFM2Q_REQUIRE(o.W && o.scale && o.x && o.y, LFM2Q_ERR_ARG, "gemv_chain: op %d: null pointer", j);
+    LFM2Q_REQUIRE(o.epi >= 0 && o.epi <= 2, LFM2Q_ERR_ARG,
+                  "gemv_chain: op %d: epi must be 0 (none), 1 (SwiGLU) or 2 (residual), got %d", j, o.epi);
+    LFM2Q_REQUIRE(o.K >= UNIT && o.K <= MAX_K && (o.K & (o.K - 1)) == 0, LFM2Q_ERR_SHAPE,
+                  "gemv_chain: op %d: K must be 1024, 2048, 4096 or 8192 (K=%d)", j, o.K);
+    LFM2Q_REQUIRE(o.N >= 1 && (o.N + G - 1) / G <= MAX_ROWS, LFM2Q_ERR_SHAPE,
+                  "gemv_chain: op %d: N must be in [1, %d] (N=%d)", j, MAX_ROWS * G, o.N);
+    LFM2Q_REQUIRE((long)(o.epi == 1 ? 2 : 1) * o.N * o.K < (1L << 31), LFM2Q_ERR_SHAPE,
+                  "gemv_chain: op %d: W must be smaller than 2 GiB", j);
+    LFM2Q_REQUIRE(aligned16(o.W) && aligned16(o.x) && ((uintptr_t)o.y & 1) == 0 && ((uintptr_t)o.scale & 3) == 0,
+                  LFM2Q_ERR_ALIGN, "gemv_chain: op %d: W and x must be 16-byte aligned", j);
+    return LFM2Q_OK;
+}
+
+}  // namespace
+}  // namespace lfm2q
+
+using namespace lfm2q;
+
+extern "C" size_t lfm2q_gemv_chain_workspace_bytes(void) { return (size_t)(WS_FLAGS + MAX_G) * 4u; }
+
+extern "C" int lfm2q_gemv_chain(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops, void *workspace,
+                                size_t workspace_bytes, lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(ops && ops_dev && workspace, LFM2Q_ERR_ARG, "gemv_chain: null pointer");
+    LFM2Q_REQUIRE(n_ops >= 1 && n_ops <= MAX_OPS, LFM2Q_ERR_SHAPE, "gemv_chain: 1 to %d ops (got %d)", MAX_OPS, n_ops);
+    LFM2Q_REQUIRE(workspace_bytes >= lfm2q_gemv_chain_workspace_bytes(), LFM2Q_ERR_SHAPE,
+                  "gemv_chain: the workspace needs %zu bytes (got %zu)", lfm2q_gemv_chain_workspace_bytes(),
+                  workspace_bytes);
+    LFM2Q_REQUIRE(((uintptr_t)workspace & 255) == 0 && aligned16(ops_dev), LFM2Q_ERR_ALIGN,
+                  "gemv_chain: the workspace must be 256-byte and the device op table 16-byte aligned");
+    const int G = device_cus();
+    LFM2Q_REQUIRE(G >= 1 && G <= MAX_G, LFM2Q_ERR_DEVICE, "gemv_chain: %d compute units (at most %d)", G, MAX_G);
+    for (int j = 0; j < n_ops; ++j)
+        if (int st = check_op(ops[j], j, G)) return st;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_chain_kernel, 64 * (CW + 1), 0) != hipSuccess ||
+        per_cu < 1)
+        return set_error(LFM2Q_ERR_DEVICE, "gemv_chain: the kernel does not fit a compute unit");
+    gemv_chain_kernel<<<G, 64 * (CW + 1), 0, (hipStream_t)stream>>>(reinterpret_cast<const ChainOp *>(ops_dev), n_ops,
+                                                                    reinterpret_cast<uint32_t *>(workspace), G);
+    return launch_status("gemv_chain");
+}

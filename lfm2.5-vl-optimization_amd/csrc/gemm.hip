@@ -92,27 +92,6 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     }
 }
 
-// Raw buffer descriptor in four SGPRs: base, stride 0, num_records = bytes, gfx9 word 3.
-__device__ __forceinline__ v4i make_desc(const void *base, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
-}
-// 16 bytes per lane from buffer offset `voff` straight into LDS at lds_base + 16 * lane (lds_base is passed in M0,
-// which the compiler loads for the asm). Written as inline asm so the compiler, which cannot see which LDS bytes
-// the load writes, does not drain every outstanding load before each LDS read or barrier; the kernel orders it with
-// explicit s_waitcnt + barrier.
-__device__ __forceinline__ void lds_dma16(v4i desc, uint32_t voff, uint32_t lds_base) {
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base) : "memory");
-}
-// 4 bytes per lane from buffer offset `voff` into LDS at lds_base + 4 * lane
-__device__ __forceinline__ void lds_dma4(v4i desc, uint32_t voff, uint32_t lds_base) {
-    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base) : "memory");
-}
-// LDS address of p as a wavefront-uniform (SGPR) value for M0
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(p));
-}
-
 // Epilogue of one wavefront block: tokens mb .. mb + 32 TM - 1 x weight rows nb .. nb + 32 TN - 1. Per tile (i, j)
 // and run q the lane holds 4 consecutive output columns n .. n + 3 of token row m.
 template <int TM, int TN, int OUT, typename ACC>

@@ -21,6 +21,7 @@
 // Reference: kernels/lfm2_decode.cu:429-950 (gemv_direct_kernel :576-661, gemv_epi_kernel :724-805,
 // gemv_dispatch :667-706), kernels/lfm2_decode.cu:954-963 (silu_mul), :108-113 (residual rounding).
 #include "common.hpp"
+#include "gemv_math.hpp"
 #include "status.hpp"
 
 #include <algorithm>
@@ -30,50 +31,6 @@
 
 namespace lfm2q {
 namespace {
-
-enum Epi { EPI_NONE = 0, EPI_SWIGLU = 1, EPI_RESIDUAL = 2 };
-
-// ------------------------------------------------------------------------------------------------ chunk math
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ v2bf as_bf16x2(uint32_t v) { return __builtin_bit_cast(v2bf, v); }
-// the upper halves of two fp32 values as one bf16 pair (lo in bits 0-15): v_perm_b32 takes bytes 2, 3 of `lo`
-// (selectors 2, 3) and bytes 2, 3 of `hi` (selectors 6, 7); exact when both values are bf16-representable
-__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
-    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-// acc + sum of one 16-byte weight chunk times its activations, the activations given as bf16 pairs (the chunk's
-// PER values, packed as loaded). int8 weights are converted exactly to bf16 pairs; v_dot2_f32_bf16 multiplies and
-// adds a pair per instruction with fp32 accumulation, so the activations are never unpacked.
-template <typename WT>
-struct PairDot;
-template <>
-struct PairDot<int8_t> {
-    static constexpr int PER = 16, XL = 2;  // 16 weights, activations in two 16-byte vectors
-    __device__ static float dot(v4i c, const v4i *xq, float acc) {
-        float a = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int d = c[j];
-            const uint32_t p0 = pack_hi16((float)(int8_t)d, (float)(int8_t)(d >> 8));
-            const uint32_t p1 = pack_hi16((float)(int8_t)(d >> 16), (float)(d >> 24));
-            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(p0), as_bf16x2((uint32_t)xq[j >> 1][2 * (j & 1)]), a, false);
-            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(p1), as_bf16x2((uint32_t)xq[j >> 1][2 * (j & 1) + 1]), a,
-                                                false);
-        }
-        return acc + a;
-    }
-};
-template <>
-struct PairDot<uint16_t> {
-    static constexpr int PER = 8, XL = 1;
-    __device__ static float dot(v4i c, const v4i *xq, float acc) {
-        float a = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2((uint32_t)c[j]), as_bf16x2((uint32_t)xq[0][j]), a, false);
-        return acc + a;
-    }
-};
 
 // ------------------------------------------------------------------------------------------------ batch 1
 // Persistent batch-1 GEMV: about WPC wavefronts per CU, wavefront g handles output rows g, g + nw, g + 2 nw, ...

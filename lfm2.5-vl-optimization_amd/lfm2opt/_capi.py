@@ -16,7 +16,17 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 
-# name -> argument types (every entry point returns an int status)
+
+class GemvOp(ctypes.Structure):
+    """lfm2q_gemv_op: one GEMV of a chain (include/lfm2q.h)."""
+    _fields_ = [("W", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("epi", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+# entry points that return something other than an int status
+RESTYPES = {"lfm2q_gemv_chain_workspace_bytes": ctypes.c_size_t}
+
+# name -> argument types (every entry point returns an int status unless listed in RESTYPES)
 SIGNATURES = {
     "lfm2q_gemv_w8": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemv_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
@@ -34,6 +44,8 @@ SIGNATURES = {
     "lfm2q_gemm_i8_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_w8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_i32": [_P, _P, _P, _I, _I, _I, _P],
+    "lfm2q_gemv_chain": [_P, _P, _I, _P, ctypes.c_size_t, _P],
+    "lfm2q_gemv_chain_workspace_bytes": [],
     "lfm2q_set_tuning": [ctypes.c_char_p, ctypes.c_char_p],
     "lfm2q_get_tuning": [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(_I)],
 }
@@ -54,7 +66,7 @@ def lib():
         L.lfm2q_version.argtypes = []
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
-            fn.argtypes, fn.restype = args, ctypes.c_int
+            fn.argtypes, fn.restype = args, RESTYPES.get(name, ctypes.c_int)
         _lib = L
     return _lib
 

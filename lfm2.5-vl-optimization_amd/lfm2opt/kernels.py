@@ -7,6 +7,7 @@ errors raise RuntimeError with the reference's TORCH_CHECK wording (kernels/lfm2
 launch. Ops outside the quantized-matmul path (attention, norms, convolutions) are not provided.
 """
 
+import ctypes
 import os
 
 import torch
@@ -149,6 +150,10 @@ class DecodeOps:
         _same_device(g, y)
         _capi.call("lfm2q_silu_mul", g.data_ptr(), y.data_ptr(), B, I2 // 2, _capi.stream(g))
 
+    def gemv_chain(self, ops):
+        """A GemvChain over ops [(epi, W, scale, x, y), ...] (an addition): call it to run all of them in one launch."""
+        return GemvChain(ops)
+
     def set_pdl(self, on):
         """Accepted for compatibility (kernels/lfm2_decode.cpp:165); HIP has no programmatic dependent launch,
         back-to-back kernels on one stream are ordered by the stream and captured into HIP graphs instead."""
@@ -190,6 +195,57 @@ class DecodeOps:
                 raise RuntimeError("scale must have one element per row of W")
         _same_device(W, x, y, scale)
         return W, scale, B, Nout, K, 0 if int8 else 1
+
+
+class GemvChain:
+    """A fixed sequence of batch-1 INT8 GEMVs run as one launch (lfm2q_gemv_chain): op j may read anything ops
+    0 .. j-1 wrote; every output equals the separate gemv / gemv_epi(0) / gemv_residual call bit for bit.
+
+    ops: (epi, W, scale, x, y) per GEMV -- epi 0 y = x W^T s, 1 SwiGLU over W = w1|w3 (y [1, S]), 2 y += x W^T s in
+    place; W int8 [R, K] with K in {1024, 2048, 4096, 8192}, scale fp32 [R], x bf16 [1, K], y bf16 [1, N]. The
+    tensors are kept alive and their addresses fixed in the table, so the chain is replayed on the same buffers
+    (graph-capturable: one kernel launch, no allocation). The op table is copied to the device and a workspace
+    allocated once, here."""
+
+    def __init__(self, ops):
+        if not ops:
+            raise RuntimeError("gemv_chain: at least one op")
+        lib = _capi.lib()
+        self._keep, table = [], []
+        dev = None
+        for j, (epi, W, scale, x, y) in enumerate(ops):
+            if epi not in (0, 1, 2):
+                raise RuntimeError(f"gemv_chain: op {j}: epi 0 (none), 1 (swiglu) or 2 (residual)")
+            _check_t(W, torch.int8, f"op {j}: W")
+            _check_t(scale, torch.float32, f"op {j}: scale")
+            _check_bf16(x, f"op {j}: x")
+            _check_bf16(y, f"op {j}: y")
+            R, K = W.shape
+            N = R // 2 if epi == 1 else R
+            if (epi == 1 and R % 2) or scale.numel() != R or x.numel() != K or y.numel() != N:
+                raise RuntimeError(f"gemv_chain: op {j}: x [1, K], W [{'2N' if epi == 1 else 'N'}, K], y [1, N]")
+            _same_device(W, scale, x, y)
+            if dev is not None and W.device != dev:
+                raise RuntimeError("all tensors must be on the same device")
+            dev = W.device
+            self._keep += [W, scale, x, y]
+            table.append(_capi.GemvOp(W.data_ptr(), scale.data_ptr(), x.data_ptr(), y.data_ptr(), N, K, epi, 0))
+        self.n = len(table)
+        self.host = (_capi.GemvOp * self.n)(*table)
+        self.dev = torch.frombuffer(bytearray(bytes(self.host)), dtype=torch.uint8).to(dev)
+        self.ws_bytes = lib.lfm2q_gemv_chain_workspace_bytes()
+        self.ws = torch.zeros(-(-self.ws_bytes // 4), dtype=torch.int32, device=dev)
+        self.device = dev
+
+    def __call__(self):
+        with torch.cuda.device(self.device):
+            _capi.call("lfm2q_gemv_chain", ctypes.addressof(self.host), self.dev.data_ptr(), self.n,
+                       self.ws.data_ptr(), self.ws_bytes, torch.cuda.current_stream(self.device).cuda_stream)
+
+    def wait_expired(self):
+        """True if a dependency wait of a launch on this chain ran out (its outputs are then undefined). Reads the
+        workspace's error word on the host (synchronizes)."""
+        return int(self.ws[1].item()) != 0
 
 
 class Int8Ops:
