@@ -96,13 +96,7 @@ class DecodeStep:
             self._init_w4(E, B, device, g, w4)
             return
 
-        self.x = torch.randn(B, H, device=device, generator=g).to(bf)       # normed residual stream
-        self.mix = torch.randn(B, H, device=device, generator=g).to(bf)     # attention / conv output
-        self.h = torch.randn(B, H, device=device, generator=g).to(bf)       # residual stream (updated in place)
-        self.qkv = torch.empty(B, QKV, device=device, dtype=bf)
-        self.bcx = torch.empty(B, CONV_IN, device=device, dtype=bf)
-        self.act = torch.empty(B, FFN, device=device, dtype=bf)
-        self.logits = torch.empty(B, VOCAB, device=device, dtype=bf)
+        self._dependent_buffers(B, device, g)
         self.ops = []        # (kind, fn, bytes)
         self.weights = []    # keep alive
         self.chain_ops = []  # the same GEMVs as (epi, W, scale, x, y) for the one-launch chain (batch 1)
@@ -110,43 +104,36 @@ class DecodeStep:
             if t == "A":
                 Wq, sq = w8(QKV, H)
                 Wo, so = w8(H, H)
-                self.ops.append(("qkv", lambda W=Wq, s=sq: E.gemv(W, s, self.x, self.qkv), gemv_bytes(QKV, H, B)))
+                self.ops.append(("qkv", lambda W=Wq, s=sq: E.gemv(W, s, self.h, self.qkv), gemv_bytes(QKV, H, B)))
                 self.ops.append(("o+res", lambda W=Wo, s=so: E.gemv_residual(W, s, self.mix, self.h),
                                  gemv_bytes(H, H, B, True)))
-                self.chain_ops += [(0, Wq, sq, self.x, self.qkv), (2, Wo, so, self.mix, self.h)]
+                self.chain_ops += [(0, Wq, sq, self.h, self.qkv), (2, Wo, so, self.mix, self.h)]
                 self.weights += [Wq, sq, Wo, so]
             else:
                 Wi, si = w8(CONV_IN, H)
                 Wc, sc = w8(H, H)
-                self.ops.append(("in", lambda W=Wi, s=si: E.gemv(W, s, self.x, self.bcx), gemv_bytes(CONV_IN, H, B)))
+                self.ops.append(("in", lambda W=Wi, s=si: E.gemv(W, s, self.h, self.bcx), gemv_bytes(CONV_IN, H, B)))
                 self.ops.append(("out+res", lambda W=Wc, s=sc: E.gemv_residual(W, s, self.mix, self.h),
                                  gemv_bytes(H, H, B, True)))
-                self.chain_ops += [(0, Wi, si, self.x, self.bcx), (2, Wc, sc, self.mix, self.h)]
+                self.chain_ops += [(0, Wi, si, self.h, self.bcx), (2, Wc, sc, self.mix, self.h)]
                 self.weights += [Wi, si, Wc, sc]
             W13, s13 = w8(2 * FFN, H)
             W2, s2 = w8(H, FFN)
-            self.ops.append(("w1|w3+swiglu", lambda W=W13, s=s13: E.gemv_epi(0, W, s, self.x, self.act),
+            self.ops.append(("w1|w3+swiglu", lambda W=W13, s=s13: E.gemv_epi(0, W, s, self.h, self.act),
                              swiglu_bytes(FFN, H, B)))
             self.ops.append(("w2+res", lambda W=W2, s=s2: E.gemv_residual(W, s, self.act, self.h),
                              gemv_bytes(H, FFN, B, True)))
-            self.chain_ops += [(1, W13, s13, self.x, self.act), (2, W2, s2, self.act, self.h)]
+            self.chain_ops += [(1, W13, s13, self.h, self.act), (2, W2, s2, self.act, self.h)]
             self.weights += [W13, s13, W2, s2]
         Wh, sh = w8(VOCAB, H)
-        self.ops.append(("lm_head", lambda: E.gemv(Wh, sh, self.x, self.logits), gemv_bytes(VOCAB, H, B)))
-        self.chain_ops.append((0, Wh, sh, self.x, self.logits))
+        self.ops.append(("lm_head", lambda: E.gemv(Wh, sh, self.h, self.logits), gemv_bytes(VOCAB, H, B)))
+        self.chain_ops.append((0, Wh, sh, self.h, self.logits))
         self.weights += [Wh, sh]
         self.bytes = sum(b for _, _, b in self.ops)
         self.weight_bytes = sum(w.numel() * w.element_size() for w in self.weights if w.dtype == torch.int8)
 
     def _init_w4(self, E, B, device, g, w4):
-        bf = torch.bfloat16
-        self.x = torch.randn(B, H, device=device, generator=g).to(bf)
-        self.mix = torch.randn(B, H, device=device, generator=g).to(bf)
-        self.h = torch.randn(B, H, device=device, generator=g).to(bf)
-        self.qkv = torch.empty(B, QKV, device=device, dtype=bf)
-        self.bcx = torch.empty(B, CONV_IN, device=device, dtype=bf)
-        self.act = torch.empty(B, FFN, device=device, dtype=bf)
-        self.logits = torch.empty(B, VOCAB, device=device, dtype=bf)
+        self._dependent_buffers(B, device, g)
         self.ops, self.weights = [], []
 
         def op(kind, N, K, x, y, epi, out=None):
@@ -157,16 +144,34 @@ class DecodeStep:
 
         for t in LAYER_TYPES:
             if t == "A":
-                op("qkv", QKV, H, self.x, self.qkv, 0)
+                op("qkv", QKV, H, self.h, self.qkv, 0)
                 op("o+res", H, H, self.mix, self.h, 2)
             else:
-                op("in", CONV_IN, H, self.x, self.bcx, 0)
+                op("in", CONV_IN, H, self.h, self.bcx, 0)
                 op("out+res", H, H, self.mix, self.h, 2)
-            op("w1|w3+swiglu", 2 * FFN, H, self.x, self.act, 1, out=FFN)
+            op("w1|w3+swiglu", 2 * FFN, H, self.h, self.act, 1, out=FFN)
             op("w2+res", H, FFN, self.act, self.h, 2)
-        op("lm_head", VOCAB, H, self.x, self.logits, 0)
+        op("lm_head", VOCAB, H, self.h, self.logits, 0)
         self.bytes = sum(b for _, _, b in self.ops)
         self.weight_bytes = sum(w.numel() * w.element_size() for w in self.weights)
+
+    def _dependent_buffers(self, B, device, g):
+        """Activations with the step's data dependencies: h is the residual stream (read by every projection,
+        updated in place by o/out_proj and w2), the o/out_proj input is the first H values of the projection before
+        it (at batch 1; the attention / short-conv between them is not part of this path), w2 reads the SwiGLU
+        activations of w1|w3. The norms between are left out, so every GEMV reads what an earlier GEMV wrote."""
+        bf = torch.bfloat16
+        self.h = torch.randn(B, H, device=device, generator=g).to(bf)
+        self.proj = torch.empty(B, max(QKV, CONV_IN), device=device, dtype=bf)  # qkv / in_proj output
+        self.qkv, self.bcx = self.proj[:, :QKV], self.proj[:, :CONV_IN]
+        if B == 1:
+            self.mix = self.proj[:, :H]
+        else:  # a column slice of several rows is not a contiguous GEMV input: its own buffer
+            self.mix = torch.randn(B, H, device=device, generator=g).to(bf)
+            self.qkv = torch.empty(B, QKV, device=device, dtype=bf)
+            self.bcx = torch.empty(B, CONV_IN, device=device, dtype=bf)
+        self.act = torch.empty(B, FFN, device=device, dtype=bf)
+        self.logits = torch.empty(B, VOCAB, device=device, dtype=bf)
 
     def run(self, kinds=None):
         for kind, fn, _ in self.ops:

@@ -111,13 +111,15 @@ typedef struct lfm2q_gemv_op {
     int32_t N, K, epi, reserved;
 } lfm2q_gemv_op;
 
-/* Bytes of the workspace lfm2q_gemv_chain needs (a few KiB). */
+/* Bytes of the workspace lfm2q_gemv_chain needs (about 34 KiB). */
 size_t lfm2q_gemv_chain_workspace_bytes(void);
 
 /* A decode step's GEMVs as one launch: ops[0 .. n_ops-1] in order, where op j may read anything ops 0 .. j-1
  * wrote (its inputs are read only after every output of op j - 1 is written). Each output is bit-identical to the
  * separate lfm2q_gemv_w8 / lfm2q_gemv_swiglu / lfm2q_gemv_residual call on the same inputs. The weights of later
- * ops stream while an op waits for its inputs, which hides the per-GEMV launch and memory-latency cost.
+ * ops stream while an op waits for its inputs, but each op boundary still costs about 3 us of device-coherent round
+ * trips: on MI355X a whole decode step as one chain is slower than the same GEMVs replayed from one HIP graph, and
+ * on a par with separate eager launches.
  * ops: the table on the host (checked there); ops_dev: the same n_ops descriptors in device memory (the kernel
  * reads these; 16-byte aligned). K in {1024, 2048, 4096, 8192}, N <= 512 x the CU count, n_ops <= 128.
  * workspace: lfm2q_gemv_chain_workspace_bytes() of device memory, 256-byte aligned, zero-filled before its first

@@ -4,22 +4,27 @@
 // read anything ops 0 .. j-1 wrote: op j's math starts only once every output of op j - 1 is written. Launched as
 // separate kernels, each GEMV pays a kernel boundary and then its first HBM round trip before any weight arrives
 // (~1.6 us + ~2 us for a 4-34 MB matrix). Here the weights -- which never depend on an earlier op -- are streamed
-// continuously across op boundaries, and only the activations wait for the dependency:
+// continuously across op boundaries, and only the activations wait for the dependency. (Measured on MI355X, each op
+// boundary still costs about 3 us -- flag seen ~0.7 us after it lands, inputs staged ~1 us, outputs stored ~0.5 us,
+// all device-coherent round trips to the memory side -- so a whole LFM2-1.2B decode step runs slower as one chain
+// than as separate kernels replayed from one HIP graph; it is on a par with separate eager launches.)
 //
 //   * One workgroup per CU (grid = CU count, every workgroup resident at once), output rows of each op split evenly
-//     over the workgroups, whole rows dealt round-robin to the 4 compute wavefronts of a workgroup.
+//     over the workgroups, whole rows dealt round-robin to the 8 compute wavefronts of a workgroup.
 //   * Each compute wavefront streams its rows' weights, 1 KiB (16 bytes per lane) per load, straight into a private
-//     ring of 32 LDS slots with buffer_load_dwordx4 ... lds, running up to 32 KiB ahead of its math, across op
-//     boundaries (128 KiB in flight per CU, 32 MiB over the chip: ~5 us of HBM time, which covers a dependency
-//     wait). Its vector memory counter tracks nothing but the ring, so "slot p has landed" is a constant
-//     s_waitcnt vmcnt(32 - B) before every item of B slots, followed by B refills.
-//   * A fifth wavefront does all other memory traffic: it waits for the previous op (below), stages x_j, the
+//     ring of 16 LDS slots with buffer_load_dwordx4 ... nt lds, running up to 16 KiB ahead of its math, across op
+//     boundaries (128 KiB per CU, 32 MiB over the chip). Its vector memory counter tracks nothing but the ring, so
+//     "the next B slots have landed" is a constant s_waitcnt vmcnt(16 - B) before every item of B slots; after the
+//     item's math the B slots are refilled.
+//   * A ninth wavefront does all other memory traffic: it waits for the previous op (below), stages x_j, the
 //     scales and the residual rows of the workgroup's outputs into LDS, and after the compute wavefronts are done
 //     stores the outputs and publishes the op's completion.
 //   * Completion: workgroup g writes its outputs with device-coherent stores (sc1, written through to the memory
-//     side), waits for them (s_waitcnt vmcnt(0)), then stores flag[g] = epoch(j). A waiter polls the flags of all
-//     workgroups with device-coherent loads until each has reached epoch(j), and reads every input of op j + 1
-//     with device-coherent loads. No cache-wide writeback or invalidate, no read-modify-write atomics.
+//     side), waits for them (s_waitcnt vmcnt(0)), then stores flag[g] = epoch(j) into each of 8 copies of the flag
+//     array. A waiter polls the flags of all workgroups in copy g % 8 with device-coherent loads until each has
+//     reached epoch(j) -- with one copy, 256 pollers on the same 8 cache lines queue at one memory channel -- and
+//     reads every input of op j + 1 with device-coherent loads. No cache-wide writeback or invalidate, no
+//     read-modify-write atomics.
 //   * epoch(j) = gen * 1024 + j + 1 for the gen-th launch on a workspace (gen is read at the start, incremented
 //     once all workgroups have read it), compared as a wrapping difference, so the flags never need resetting.
 //     Every wait is bounded (20 ms of the real-time counter): a wait that runs out sets the workspace's error word,
@@ -40,8 +45,11 @@
 namespace lfm2q {
 namespace {
 
-constexpr int CW = 4;                 // compute wavefronts per workgroup
-constexpr int SLOTS = 32;             // 1 KiB ring slots per compute wavefront
+#ifndef LFM2Q_CHAIN_CW
+#define LFM2Q_CHAIN_CW 8
+#endif
+constexpr int CW = LFM2Q_CHAIN_CW;    // compute wavefronts per workgroup (two per SIMD)
+constexpr int SLOTS = 128 / CW;       // 1 KiB ring slots per compute wavefront: 128 KiB of ring per workgroup
 constexpr int UNIT = 1024;            // bytes per slot: one wavefront load, 16 bytes per lane
 constexpr int MAX_K = 8192;
 constexpr int MAX_ROWS = 512;         // output rows of one op per workgroup
@@ -50,6 +58,8 @@ constexpr uint32_t EPOCHS = 1024;
 constexpr int MAX_G = 1024;           // workgroups (= CUs)
 constexpr int WS_GEN = 0, WS_ERR = 1; // workspace words; the flags start 128 bytes in
 constexpr int WS_FLAGS = 32;
+constexpr int FLAG_COPIES = 8;        // every flag is written to 8 copies of the flag array; workgroup g polls copy g % 8
+constexpr int FLAG_STRIDE = 1088;     // words between copies (4352 bytes: the copies sit in different memory channels)
 constexpr uint64_t WAIT_TICKS = 2000000;  // 20 ms at the 100 MHz s_memrealtime clock
 constexpr int AUX_SC1 = 16;           // device-scope coherent access (sc1)
 
@@ -61,6 +71,7 @@ struct ChainOp {
     int N, K, epi, reserved;
 };
 static_assert(sizeof(ChainOp) == sizeof(lfm2q_gemv_op), "descriptor layout");
+static_assert(FLAG_STRIDE >= MAX_G && CW * SLOTS * UNIT == 128 * 1024, "workspace and ring layout");
 
 struct Lds {
     uint8_t ring[CW][SLOTS][UNIT];  // 128 KiB
@@ -71,9 +82,10 @@ struct Lds {
     uint16_t outs[MAX_ROWS];        // results, stored by the sync wavefront
 };
 
+// rows [r0, r1) of an op of N rows for workgroup g of G (g N < 2^31: N <= 512 G, G <= 1024, checked on the host)
 __device__ __forceinline__ void rows_of(int N, int g, int G, int &r0, int &r1) {
-    r0 = (int)((long)g * N / G);
-    r1 = (int)((long)(g + 1) * N / G);
+    r0 = (int)((uint32_t)(g * N) / (uint32_t)G);
+    r1 = (int)((uint32_t)((g + 1) * N) / (uint32_t)G);
 }
 
 // a pointer read from LDS as a wavefront-uniform (scalar) value; readfirstlane returns int, so each half goes
@@ -97,21 +109,15 @@ __device__ __forceinline__ void wait_vm() {
 __device__ __forceinline__ v4u ld_dev16(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_SC1));
 }
-__device__ __forceinline__ uint32_t ld_dev4(rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX_SC1);
-}
 __device__ __forceinline__ uint16_t ld_dev2(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, AUX_SC1);
-}
-__device__ __forceinline__ void st_dev4(uint32_t v, rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, AUX_SC1);
 }
 __device__ __forceinline__ void st_dev2(uint16_t v, rsrc_t r, uint32_t off) {
     __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)off, 0, AUX_SC1);
 }
 
-// The weight stream of one compute wavefront: op by op, the wavefront's items t = r0 + w, r0 + w + CW, ... < r1,
-// per item its NROW weight rows (row t, and S + t for SwiGLU), per row its K / 1024 units. Every member is
+// The weight stream of one compute wavefront: op by op, the wavefront's items t = w, w + CW, ... (local indices,
+// item t = row row0 + t), per item its NROW weight rows (that row, and S + it for SwiGLU), per row its K / 1024 units. Every member is
 // wavefront-uniform (scalar registers); past the last op every load reads zeros through an empty range.
 struct Loader {
     const ChainOp *ops;  // the LDS copy
@@ -119,15 +125,15 @@ struct Loader {
     int j;
     v4i desc;
     uint32_t rowb;
-    int cpl, nrow, S, t, t_end, r, u;
+    int cpl, nrow, S, row0, t, t_end, r, u;
 
     __device__ __forceinline__ void open(int from) {
         for (j = from; j < n_ops; ++j) {
             const int N = __builtin_amdgcn_readfirstlane(ops[j].N);
-            int r0, r1;
-            rows_of(N, g, G, r0, r1);
-            t = r0 + w;
-            t_end = r1;
+            int r1;
+            rows_of(N, g, G, row0, r1);
+            t = w;  // local item index; its row is row0 + t
+            t_end = r1 - row0;
             if (t < t_end) {
                 const int K = __builtin_amdgcn_readfirstlane(ops[j].K);
                 nrow = __builtin_amdgcn_readfirstlane(ops[j].epi) == EPI_SWIGLU ? 2 : 1;
@@ -144,7 +150,7 @@ struct Loader {
         desc = make_desc(uniform_ptr(ops[n_ops - 1].W), 0u);
     }
     __device__ __forceinline__ uint32_t offset() const {
-        return j < n_ops ? (uint32_t)(r ? S + t : t) * rowb + (uint32_t)u * UNIT : 0u;
+        return j < n_ops ? (uint32_t)(r ? S + row0 + t : row0 + t) * rowb + (uint32_t)u * UNIT : 0u;
     }
     __device__ __forceinline__ void advance() {
         if (j >= n_ops) return;
@@ -160,7 +166,10 @@ struct Loader {
         // the resource must reach the instruction in scalar registers (an asm operand is not moved there by itself)
         const v4i d = {__builtin_amdgcn_readfirstlane(desc[0]), __builtin_amdgcn_readfirstlane(desc[1]),
                        __builtin_amdgcn_readfirstlane(desc[2]), __builtin_amdgcn_readfirstlane(desc[3])};
-        lds_dma16(d, (uint32_t)lane * 16u + offset(), lds_addr(slot));
+        // non-temporal: each weight byte is read once (measured: 6.2 -> 7.0 TB/s for a streaming ring like this one)
+        asm volatile("buffer_load_dwordx4 %0, %1, 0 offen nt lds" ::"v"((uint32_t)lane * 16u + offset()), "s"(d),
+                     "{m0}"(lds_addr(slot))
+                     : "memory");
     }
     // the next n units of the stream into the ring slots from position p on (a loop, not unrolled: one copy of
     // advance() per call site)
@@ -175,107 +184,124 @@ __device__ __forceinline__ void Loader::issue_n(Lds &L, uint32_t p, int n, int l
     }
 }
 
-// Wait until at most SLOTS - B ring loads are outstanding: the B oldest (the next item's slots) have landed.
-__device__ __forceinline__ void wait_ring(int B) {
-    switch (B) {
-        case 1: wait_vm<SLOTS - 1>(); break;
-        case 2: wait_vm<SLOTS - 2>(); break;
-        case 4: wait_vm<SLOTS - 4>(); break;
-        case 8: wait_vm<SLOTS - 8>(); break;
-        default: wait_vm<SLOTS - 16>(); break;
+// One op's items of a compute wavefront: items t = w, w + CW, ... < cnt (local indices; item t is output row
+// row0 + t), each NROW weight rows of CPL units. Before an item its B = NROW CPL slots are waited for and read; after
+// its math they are refilled with the next B units of the stream. The row sums are reduced on their own (fold_sum
+// over one value, or the w1 / w3 pair), which pairs the lanes exactly as the batch-1 GEMV kernels do, so the bits
+// are theirs.
+template <int CPL, int NROW>
+__device__ __forceinline__ void chain_items(Lds &L, Loader &ld, uint32_t &pos, int lane, int w, int cnt, int epi) {
+    using D = PairDot<int8_t>;
+    constexpr int B = NROW * CPL;
+    static_assert(B <= SLOTS, "an item fits the ring");
+    v4i xr[CPL][2];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) xr[u][q] = *reinterpret_cast<const v4i *>(&L.xs[(lane + 64 * u) * 16 + 8 * q]);
+    for (int t = w; t < cnt; t += CW) {
+        v4i c[B];
+        wait_vm<SLOTS - B>();  // units pos .. pos + B - 1 have landed (every earlier refill has been issued)
+#pragma unroll
+        for (int b = 0; b < B; ++b) c[b] = *reinterpret_cast<const v4i *>(&L.ring[w][(pos + b) & (SLOTS - 1)][16 * lane]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slots are read before they refill
+        const uint32_t p = pos;
+        pos += B;
+        float a[NROW];
+#pragma unroll
+        for (int rr = 0; rr < NROW; ++rr) {
+            a[rr] = 0.f;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) a[rr] = D::dot(c[rr * CPL + u], xr[u], a[rr]);
+        }
+        const float rs = fold_sum<NROW>(a);  // NROW 2: w1 sum in lanes 0-31, w3 sum in lanes 32-63
+        if (NROW == 2) {
+            const float ru = __uint_as_float(
+                __builtin_amdgcn_permlane32_swap(__float_as_uint(rs), __float_as_uint(rs), false, false)[1]);
+            if (lane == 0) L.outs[t] = gemv_epilogue<EPI_SWIGLU>(rs, L.sc[0][t], ru, L.sc[1][t], 0u, true);
+        } else if (lane == 0) {
+            L.outs[t] = epi == EPI_RESIDUAL ? gemv_epilogue<EPI_RESIDUAL>(rs, L.sc[0][t], 0.f, 1.f, L.hs[t], true)
+                                            : gemv_epilogue<EPI_NONE>(rs, L.sc[0][t], 0.f, 1.f, 0u, true);
+        }
+        ld.issue_n(L, p, B, lane);
     }
 }
 
-// One op's items of a compute wavefront. An item is one output row: its weight row (w1 and w3 rows for SwiGLU),
-// cpl units each. Items go in groups whose row sums fill the 8 values of one fold_sum (8 items, or 4 SwiGLU items
-// = 4 w1 + 4 w3 sums); before each item its B = nrow cpl slots are waited for, read, and refilled with the next B
-// units of the stream. One routine for every K and epilogue (run-time cpl, epi; fixed-size register arrays
-// indexed by unrolled loop counters).
-__device__ __forceinline__ void chain_items(Lds &L, Loader &ld, uint32_t &pos, int lane, int w, int r0, int r1,
-                                            int cpl, int epi) {
-    using D = PairDot<int8_t>;
-    const bool swiglu = epi == EPI_SWIGLU;
-    const int B = swiglu ? 2 * cpl : cpl;
-    const int per_group = swiglu ? 4 : 8;
-    v4i xr[8][2];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-        if (u < cpl)
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-                xr[u][q] = *reinterpret_cast<const v4i *>(&L.xs[(lane + 64 * u) * 16 + 8 * q]);
-    for (int t0 = r0 + w; t0 < r1; t0 += per_group * CW) {
-        float part[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) part[i] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (i >= per_group || t0 + i * CW >= r1) continue;
-            v4i c1[8], c2[8];  // the item's w1 (or only) row and, for SwiGLU, its w3 row
-            wait_ring(B);
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (u < cpl) c1[u] = *reinterpret_cast<const v4i *>(&L.ring[w][(pos + u) & (SLOTS - 1)][16 * lane]);
-            if (swiglu)
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (u < cpl)
-                        c2[u] = *reinterpret_cast<const v4i *>(&L.ring[w][(pos + cpl + u) & (SLOTS - 1)][16 * lane]);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slots are read before they refill
-            ld.issue_n(L, pos, B, lane);
-            pos += B;
-            float a = 0.f;
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (u < cpl) a = D::dot(c1[u], xr[u], a);
-            part[i] = a;
-            if (swiglu) {
-                float a3 = 0.f;
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (u < cpl) a3 = D::dot(c2[u], xr[u], a3);
-                part[(4 + i) & 7] = a3;
-            }
+__device__ __forceinline__ void chain_op(Lds &L, Loader &ld, uint32_t &pos, int lane, int w, int cnt, int cpl,
+                                         int epi) {
+    if (epi == EPI_SWIGLU) {
+        switch (cpl) {
+            case 1: chain_items<1, 2>(L, ld, pos, lane, w, cnt, epi); break;
+            case 2: chain_items<2, 2>(L, ld, pos, lane, w, cnt, epi); break;
+            case 4: chain_items<4, 2>(L, ld, pos, lane, w, cnt, epi); break;
+            default: chain_items<8, 2>(L, ld, pos, lane, w, cnt, epi); break;
         }
-        const float rs = fold_sum<8>(part);  // value v in lanes 8 v .. 8 v + 7
-        // SwiGLU: the w3 sum of item i (value 4 + i) sits 32 lanes above its w1 sum (value i)
-        const float ru = __uint_as_float(
-            __builtin_amdgcn_permlane32_swap(__float_as_uint(rs), __float_as_uint(rs), false, false)[1]);
-        const int i = lane >> 3, t = t0 + i * CW;
-        if ((lane & 7) == 0 && i < per_group && t < r1) {
-            const int k = t - r0;
-            const float sg = L.sc[0][k];
-            uint16_t v;
-            if (epi == EPI_SWIGLU)
-                v = gemv_epilogue<EPI_SWIGLU>(rs, sg, ru, L.sc[1][k], 0u, true);
-            else if (epi == EPI_RESIDUAL)
-                v = gemv_epilogue<EPI_RESIDUAL>(rs, sg, 0.f, 1.f, L.hs[k], true);
-            else
-                v = gemv_epilogue<EPI_NONE>(rs, sg, 0.f, 1.f, 0u, true);
-            L.outs[k] = v;
+    } else {
+        switch (cpl) {
+            case 1: chain_items<1, 1>(L, ld, pos, lane, w, cnt, epi); break;
+            case 2: chain_items<2, 1>(L, ld, pos, lane, w, cnt, epi); break;
+            case 4: chain_items<4, 1>(L, ld, pos, lane, w, cnt, epi); break;
+            default: chain_items<8, 1>(L, ld, pos, lane, w, cnt, epi); break;
         }
     }
+}
+
+// The workspace words are read and written as relaxed agent-scope atomics: device-coherent accesses (sc1) that the
+// compiler neither merges nor moves out of a polling loop (plain loads of one address in a loop with no store would
+// be folded into one).
+__device__ __forceinline__ uint32_t ld_word(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_word(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Wait until every workgroup's flag has reached `target`, or the error word is set, or the bound runs out (which
-// sets the error word). One 16-byte coherent load covers 4 flags per lane.
-__device__ __forceinline__ void wait_flags(rsrc_t wsr, int G, uint32_t target, int lane) {
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    for (;;) {
-        bool ok = true;
-        for (int b = 4 * lane; b < G; b += 256) {
-            const v4u f = ld_dev16(wsr, (uint32_t)(WS_FLAGS + b) * 4u);
+// sets the error word). Lane l reads flags l, l + 64, ... Up to 256 workgroups two polls are in flight, so a
+// completed dependency is seen about one memory round trip after its last flag lands; the error word and the clock
+// are checked every 8 rounds. Ends with a compiler barrier: the op's input loads are not moved above the wait.
+__device__ __forceinline__ bool all_reached(const uint32_t (&f)[4], int lane, int G, uint32_t target) {
+    bool ok = true;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) ok = ok && (b + e >= G || (int)(f[e] - target) >= 0);
+    for (int e = 0; e < 4; ++e) ok = ok && (lane + 64 * e >= G || (int)(f[e] - target) >= 0);
+    return __builtin_amdgcn_ballot_w64(!ok) == 0;
+}
+__device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target, int lane) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    const uint32_t *flags = ws + WS_FLAGS + (blockIdx.x % FLAG_COPIES) * FLAG_STRIDE;
+    if (G <= 256) {
+        uint32_t a[4], b[4];
+        auto poll = [&](uint32_t(&f)[4]) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = lane + 64 * e < G ? ld_word(flags + lane + 64 * e) : 0u;
+        };
+        poll(a);
+        poll(b);
+        for (int it = 0;; ++it) {
+            if (all_reached(a, lane, G, target)) break;
+            poll(a);
+            if (all_reached(b, lane, G, target)) break;
+            poll(b);
+            if ((it & 7) == 7) {
+                if (ld_word(ws + WS_ERR)) break;
+                if (__builtin_amdgcn_s_memrealtime() - t0 > WAIT_TICKS) {
+                    if (lane == 0) st_word(ws + WS_ERR, 1u);
+                    break;
+                }
+            }
         }
-        const uint32_t err = ld_dev4(wsr, WS_ERR * 4);
-        if (__builtin_amdgcn_ballot_w64(!ok) == 0 || err) return;
-        if (__builtin_amdgcn_s_memrealtime() - t0 > WAIT_TICKS) {
-            if (lane == 0) st_dev4(1u, wsr, WS_ERR * 4);
-            return;
+    } else {
+        for (;;) {
+            bool ok = true;
+            for (int i = lane; i < G; i += 64) ok = ok && (int)(ld_word(flags + i) - target) >= 0;
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0 || ld_word(ws + WS_ERR)) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > WAIT_TICKS) {
+                if (lane == 0) st_word(ws + WS_ERR, 1u);
+                break;
+            }
         }
-        __builtin_amdgcn_s_sleep(1);
     }
+    asm volatile("" ::: "memory");
 }
 
 __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp *__restrict__ ops, int n_ops,
@@ -284,48 +310,69 @@ __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = blockIdx.x;
-    const rsrc_t wsr = make_rsrc(ws, (uint32_t)(WS_FLAGS + MAX_G) * 4u);
     // the op table into LDS, before any wavefront starts its loads
     for (int i = threadIdx.x; i < n_ops * (int)(sizeof(ChainOp) / 16); i += blockDim.x)
         reinterpret_cast<v4i *>(L.ops)[i] = reinterpret_cast<const v4i *>(ops)[i];
     __syncthreads();
 
     if (w == CW) {  // ------------------------------------------------------------------ the sync wavefront
-        const uint32_t gen = __builtin_amdgcn_readfirstlane(ld_dev4(wsr, WS_GEN * 4));
+        const uint32_t gen = __builtin_amdgcn_readfirstlane(ld_word(ws + WS_GEN));
         for (int j = 0; j < n_ops; ++j) {
-            if (j) wait_flags(wsr, G, gen * EPOCHS + (uint32_t)j, lane);  // op j - 1 complete everywhere
+            if (j) wait_flags(ws, G, gen * EPOCHS + (uint32_t)j, lane);  // op j - 1 complete everywhere
             const int N = __builtin_amdgcn_readfirstlane(L.ops[j].N), K = __builtin_amdgcn_readfirstlane(L.ops[j].K);
             const int epi = __builtin_amdgcn_readfirstlane(L.ops[j].epi);
             const float *scale = uniform_ptr(L.ops[j].scale);
             int r0, r1;
             rows_of(N, g, G, r0, r1);
             const int nr = r1 - r0;
+            // every input of op j into LDS with all its loads in flight at once (one wait): x and the residual rows
+            // through device-coherent register loads (an earlier op may have written them), the scales of the
+            // workgroup's rows (never written by an op) straight into LDS
             const rsrc_t xr = make_rsrc(uniform_ptr(L.ops[j].x), (uint32_t)K * 2u);
-            for (int off = 16 * lane; off < K * 2; off += 1024)
-                *reinterpret_cast<v4u *>(reinterpret_cast<uint8_t *>(L.xs) + off) = ld_dev16(xr, (uint32_t)off);
-            for (int i = lane; i < nr; i += 64) {
-                L.sc[0][i] = scale[r0 + i];
-                if (epi == EPI_SWIGLU) L.sc[1][i] = scale[N + r0 + i];
+            v4u xv[MAX_K * 2 / 1024];
+#pragma unroll
+            for (int q = 0; q < MAX_K * 2 / 1024; ++q)
+                if (1024 * q < K * 2) xv[q] = ld_dev16(xr, (uint32_t)(1024 * q + 16 * lane));
+            const v4i sd = make_desc(scale, (uint32_t)(epi == EPI_SWIGLU ? 2 * N : N) * 4u);
+            for (int i = 0; i < nr; i += 64) {
+                asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"((uint32_t)(r0 + i + lane) * 4u), "s"(sd),
+                             "{m0}"(lds_addr(&L.sc[0][i]))
+                             : "memory");
+                if (epi == EPI_SWIGLU)
+                    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"((uint32_t)(N + r0 + i + lane) * 4u),
+                                 "s"(sd), "{m0}"(lds_addr(&L.sc[1][i]))
+                                 : "memory");
             }
             const rsrc_t yr = make_rsrc(uniform_ptr(L.ops[j].y), (uint32_t)N * 2u);
-            if (epi == EPI_RESIDUAL)
-                for (int i = lane; i < nr; i += 64) L.hs[i] = ld_dev2(yr, (uint32_t)(r0 + i) * 2u);
+            if (epi == EPI_RESIDUAL) {  // all row loads issued before the first LDS write
+                uint16_t hv[MAX_ROWS / 64];
+#pragma unroll
+                for (int q = 0; q < MAX_ROWS / 64; ++q)
+                    if (64 * q < nr) hv[q] = ld_dev2(yr, (uint32_t)(r0 + 64 * q + lane) * 2u);
+#pragma unroll
+                for (int q = 0; q < MAX_ROWS / 64; ++q)
+                    if (64 * q < nr) L.hs[64 * q + lane] = hv[q];
+            }
+#pragma unroll
+            for (int q = 0; q < MAX_K * 2 / 1024; ++q)
+                if (1024 * q < K * 2)
+                    *reinterpret_cast<v4u *>(reinterpret_cast<uint8_t *>(L.xs) + 1024 * q + 16 * lane) = xv[q];
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
             wg_barrier();  // A_j: op j's inputs are in LDS
             wg_barrier();  // B_j: op j's outputs are in LDS
             for (int i = lane; i < nr; i += 64) st_dev2(L.outs[i], yr, (uint32_t)(r0 + i) * 2u);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the outputs are written before the flag
-            if (lane == 0) st_dev4(gen * EPOCHS + (uint32_t)j + 1u, wsr, (uint32_t)(WS_FLAGS + g) * 4u);
+            if (lane < FLAG_COPIES) st_word(ws + WS_FLAGS + lane * FLAG_STRIDE + g, gen * EPOCHS + (uint32_t)j + 1u);
         }
         if (g == 0) {  // once every workgroup is past the last op (so has read gen), advance gen for the next launch
-            wait_flags(wsr, G, gen * EPOCHS + (uint32_t)n_ops, lane);
-            if (lane == 0) st_dev4(gen + 1u, wsr, WS_GEN * 4);
+            wait_flags(ws, G, gen * EPOCHS + (uint32_t)n_ops, lane);
+            if (lane == 0) st_word(ws + WS_GEN, gen + 1u);
         }
         return;
     }
 
     // ------------------------------------------------------------------------------------ compute wavefronts
-    Loader ld{L.ops, n_ops, g, G, w, 0, {}, 0u, 0, 0, 0, 0, 0, 0, 0};
+    Loader ld{L.ops, n_ops, g, G, w, 0, {}, 0u, 0, 0, 0, 0, 0, 0, 0, 0};
     ld.open(0);
     ld.issue_n(L, 0u, SLOTS, lane);
     uint32_t pos = 0;  // next stream position to consume; pos + SLOTS have been issued
@@ -335,7 +382,7 @@ __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp
         const int cpl = __builtin_amdgcn_readfirstlane(L.ops[j].K) / UNIT;
         int r0, r1;
         rows_of(N, g, G, r0, r1);
-        chain_items(L, ld, pos, lane, w, r0, r1, cpl, epi);
+        chain_op(L, ld, pos, lane, w, r1 - r0, cpl, epi);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // outs written
         wg_barrier();  // B_j
     }
@@ -362,7 +409,9 @@ int check_op(const lfm2q_gemv_op &o, int j, int G) {
 
 using namespace lfm2q;
 
-extern "C" size_t lfm2q_gemv_chain_workspace_bytes(void) { return (size_t)(WS_FLAGS + MAX_G) * 4u; }
+extern "C" size_t lfm2q_gemv_chain_workspace_bytes(void) {
+    return (size_t)(WS_FLAGS + FLAG_COPIES * FLAG_STRIDE) * 4u;
+}
 
 extern "C" int lfm2q_gemv_chain(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops, void *workspace,
                                 size_t workspace_bytes, lfm2q_stream_t stream) {
