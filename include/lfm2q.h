@@ -131,6 +131,18 @@ size_t lfm2q_gemv_chain_workspace_bytes(void);
 int lfm2q_gemv_chain(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops, void *workspace,
                      size_t workspace_bytes, lfm2q_stream_t stream);
 
+/* lfm2q_gemv_chain without a workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc); it allocates nothing and calls no
+ * allocating routine. No counterpart in the reference. Its workspace is a fixed array of
+ * lfm2q_gemv_chain_workspace_bytes() (34944) bytes in the library's device memory, one per GPU, held until the
+ * process ends; every call first zeroes it with a fill kernel on `stream`, so two calls on one GPU must not overlap
+ * (calls on different streams at once race on the array). Limits as lfm2q_gemv_chain: 1 <= n_ops <= 128 (beyond
+ * that LFM2Q_ERR_SHAPE), K in {1024, 2048, 4096, 8192}, N <= 512 x the CU count, at most 1024 CUs.
+ * status: optional (NULL or a device uint32, 4-byte aligned), set at the end of the launch to 0, or nonzero if a
+ * dependency wait ran out (the outputs are then undefined). Outputs are bit-identical to lfm2q_gemv_chain's. */
+int lfm2q_gemv_chain_noalloc(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops, uint32_t *status,
+                             lfm2q_stream_t stream);
+
 /* y[b, i] = bf16( bf16(silu(g[b, i])) * g[b, I + i] ), g bf16 [B, 2I], y bf16 [B, I].
  * Replaces launch_silu_mul kernels/lfm2_decode.cu:954-969 (bound as silu_mul(), kernels/lfm2_decode.cpp:100-103). */
 int lfm2q_silu_mul(const lfm2q_bf16 *g, lfm2q_bf16 *y, int B, int I, lfm2q_stream_t stream);

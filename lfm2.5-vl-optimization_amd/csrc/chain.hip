@@ -41,6 +41,7 @@
 #include "status.hpp"
 
 #include <algorithm>
+#include <atomic>
 
 namespace lfm2q {
 namespace {
@@ -305,7 +306,8 @@ __device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target,
 }
 
 __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp *__restrict__ ops, int n_ops,
-                                                                   uint32_t *__restrict__ ws, int G) {
+                                                                   uint32_t *__restrict__ ws, int G,
+                                                                   uint32_t *__restrict__ status) {
     __shared__ __attribute__((aligned(1024))) Lds L;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -367,6 +369,8 @@ __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp
         if (g == 0) {  // once every workgroup is past the last op (so has read gen), advance gen for the next launch
             wait_flags(ws, G, gen * EPOCHS + (uint32_t)n_ops, lane);
             if (lane == 0) st_word(ws + WS_GEN, gen + 1u);
+            // every workgroup has stored its last flag, so any expired wait has set the error word by now
+            if (lane == 0 && status) st_word(status, ld_word(ws + WS_ERR));
         }
         return;
     }
@@ -409,9 +413,63 @@ int check_op(const lfm2q_gemv_op &o, int j, int G) {
 
 using namespace lfm2q;
 
-extern "C" size_t lfm2q_gemv_chain_workspace_bytes(void) {
-    return (size_t)(WS_FLAGS + FLAG_COPIES * FLAG_STRIDE) * 4u;
+namespace lfm2q {
+namespace {
+
+constexpr int WS_WORDS = WS_FLAGS + FLAG_COPIES * FLAG_STRIDE;
+
+// The checks every chain launch makes (G: the grid, one workgroup per CU).
+int check_chain(const char *who, const lfm2q_gemv_op *ops, int n_ops, int &G) {
+    G = device_cus();
+    LFM2Q_REQUIRE(G >= 1 && G <= MAX_G, LFM2Q_ERR_DEVICE, "%s: %d compute units (at most %d)", who, G, MAX_G);
+    for (int j = 0; j < n_ops; ++j)
+        if (int st = check_op(ops[j], j, G)) return st;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_chain_kernel, 64 * (CW + 1), 0) != hipSuccess ||
+        per_cu < 1)
+        return set_error(LFM2Q_ERR_DEVICE, "%s: the kernel does not fit a compute unit", who);
+    return LFM2Q_OK;
 }
+
+int launch_chain(const char *who, const lfm2q_gemv_op *ops_dev, int n_ops, int G, uint32_t *ws, uint32_t *status,
+                 hipStream_t stream) {
+    gemv_chain_kernel<<<G, 64 * (CW + 1), 0, stream>>>(reinterpret_cast<const ChainOp *>(ops_dev), n_ops, ws, G,
+                                                       status);
+    return launch_status(who);
+}
+
+// The workspace of lfm2q_gemv_chain_noalloc: one copy per GPU, in the library's own device memory, held until the
+// process ends. In host code `scratch` names only a host-side stand-in; the device address comes from
+// hipGetSymbolAddress, looked up once per device (with that device current) and kept in scratch_dev.
+static __device__ __align__(256) uint32_t scratch[WS_WORDS];
+constexpr int MAX_DEVICES = 64;
+std::atomic<uint32_t *> scratch_dev[MAX_DEVICES];
+
+int scratch_of_current_device(uint32_t **out) {
+    int dev = -1;
+    const hipError_t de = hipGetDevice(&dev);
+    LFM2Q_REQUIRE(de == hipSuccess && dev >= 0 && dev < MAX_DEVICES, LFM2Q_ERR_DEVICE,
+                  "gemv_chain_noalloc: no current device below %d (%s)", MAX_DEVICES, hipGetErrorString(de));
+    uint32_t *ptr = scratch_dev[dev].load(std::memory_order_acquire);
+    if (!ptr) {
+        const hipError_t e = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+        LFM2Q_REQUIRE(e == hipSuccess && ptr, LFM2Q_ERR_DEVICE,
+                      "gemv_chain_noalloc: the scratch array's address on device %d: %s", dev, hipGetErrorString(e));
+        scratch_dev[dev].store(ptr, std::memory_order_release);  // a racing first call stores the same address
+    }
+    *out = ptr;
+    return LFM2Q_OK;
+}
+
+// zeroes n words (a kernel, not hipMemsetAsync, so that a captured graph replays it correctly)
+__global__ __launch_bounds__(256) void clear_words_kernel(uint32_t *__restrict__ p, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+}  // namespace
+}  // namespace lfm2q
+
+extern "C" size_t lfm2q_gemv_chain_workspace_bytes(void) { return (size_t)WS_WORDS * 4u; }
 
 extern "C" int lfm2q_gemv_chain(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops, void *workspace,
                                 size_t workspace_bytes, lfm2q_stream_t stream) {
@@ -422,15 +480,26 @@ extern "C" int lfm2q_gemv_chain(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *o
                   workspace_bytes);
     LFM2Q_REQUIRE(((uintptr_t)workspace & 255) == 0 && aligned16(ops_dev), LFM2Q_ERR_ALIGN,
                   "gemv_chain: the workspace must be 256-byte and the device op table 16-byte aligned");
-    const int G = device_cus();
-    LFM2Q_REQUIRE(G >= 1 && G <= MAX_G, LFM2Q_ERR_DEVICE, "gemv_chain: %d compute units (at most %d)", G, MAX_G);
-    for (int j = 0; j < n_ops; ++j)
-        if (int st = check_op(ops[j], j, G)) return st;
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_chain_kernel, 64 * (CW + 1), 0) != hipSuccess ||
-        per_cu < 1)
-        return set_error(LFM2Q_ERR_DEVICE, "gemv_chain: the kernel does not fit a compute unit");
-    gemv_chain_kernel<<<G, 64 * (CW + 1), 0, (hipStream_t)stream>>>(reinterpret_cast<const ChainOp *>(ops_dev), n_ops,
-                                                                    reinterpret_cast<uint32_t *>(workspace), G);
-    return launch_status("gemv_chain");
+    int G = 0;
+    if (int st = check_chain("gemv_chain", ops, n_ops, G)) return st;
+    return launch_chain("gemv_chain", ops_dev, n_ops, G, reinterpret_cast<uint32_t *>(workspace), nullptr,
+                        (hipStream_t)stream);
+}
+
+extern "C" int lfm2q_gemv_chain_noalloc(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops,
+                                        uint32_t *status, lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(ops && ops_dev, LFM2Q_ERR_ARG, "gemv_chain_noalloc: null pointer");
+    LFM2Q_REQUIRE(n_ops >= 1 && n_ops <= MAX_OPS, LFM2Q_ERR_SHAPE,
+                  "gemv_chain_noalloc: 1 to %d ops (got %d): the chain's op table holds at most %d", MAX_OPS, n_ops,
+                  MAX_OPS);
+    LFM2Q_REQUIRE(aligned16(ops_dev) && ((uintptr_t)status & 3) == 0, LFM2Q_ERR_ALIGN,
+                  "gemv_chain_noalloc: the device op table must be 16-byte and status 4-byte aligned");
+    int G = 0;
+    if (int st = check_chain("gemv_chain_noalloc", ops, n_ops, G)) return st;
+    uint32_t *ws = nullptr;
+    if (int st = scratch_of_current_device(&ws)) return st;
+    // the previous call on this GPU left its flags, launch counter and error word: start from zeros
+    clear_words_kernel<<<8, 256, 0, (hipStream_t)stream>>>(ws, WS_WORDS);
+    if (int st = launch_status("gemv_chain_noalloc")) return st;
+    return launch_chain("gemv_chain_noalloc", ops_dev, n_ops, G, ws, status, (hipStream_t)stream);
 }

@@ -45,6 +45,7 @@ SIGNATURES = {
     "lfm2q_gemm_w8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_i32": [_P, _P, _P, _I, _I, _I, _P],
     "lfm2q_gemv_chain": [_P, _P, _I, _P, ctypes.c_size_t, _P],
+    "lfm2q_gemv_chain_noalloc": [_P, _P, _I, _P, _P],
     "lfm2q_gemv_chain_workspace_bytes": [],
     "lfm2q_set_tuning": [ctypes.c_char_p, ctypes.c_char_p],
     "lfm2q_get_tuning": [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(_I)],

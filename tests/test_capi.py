@@ -57,6 +57,13 @@ def test_status_codes_without_launch(L):
     assert L.lfm2q_gemv_w8(ctypes.c_void_p(0x1001), fake, fake, fake, 1, 64, 512, 0, None) == 3  # misaligned
     assert L.lfm2q_gemv_swiglu(2, fake, fake, fake, fake, 1, 64, 512, None) == 1  # bad wtype
     assert L.lfm2q_silu_mul(None, fake, 1, 8, None) == 1
+    # the no-allocation chain: its op table (and so its scratch flags) hold at most 128 ops
+    table = (_capi.GemvOp * 1)()
+    assert L.lfm2q_gemv_chain_noalloc(None, fake, 1, None, None) == 1
+    assert L.lfm2q_gemv_chain_noalloc(ctypes.addressof(table), fake, 129, None, None) == 2
+    assert "at most 128" in L.lfm2q_last_error().decode()
+    assert L.lfm2q_gemv_chain_noalloc(ctypes.addressof(table), fake, 0, None, None) == 2
+    assert L.lfm2q_gemv_chain_noalloc(ctypes.addressof(table), ctypes.c_void_p(0x1008), 1, None, None) == 3
 
 
 def test_python_checks_match_reference_wording():
