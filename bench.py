@@ -14,6 +14,7 @@ activations N(0, 1), seeded.
 """
 
 import argparse
+import ctypes
 import json
 import os
 import pathlib
@@ -641,6 +642,47 @@ def producer_results(reps):
     return res
 
 
+def mfma_rate(iters=20000):
+    """The int8 matrix-core rate the chip sustains (lib/liblfm2q_calib.so: every SIMD issuing nothing but
+    independent v_mfma_i32_32x32x32_i8, two wavefronts per SIMD) on random and on all-zero operand bytes, with the
+    shader clock measured during the run (s_memtime against the 100 MHz s_memrealtime)."""
+    L = ctypes.CDLL(str(ROOT / "lfm2.5-vl-optimization_amd" / "lib" / "liblfm2q_calib.so"))
+    L.lfm2q_calib_mfma_i8.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    blocks = 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    waves = 4 * blocks
+    g = torch.Generator(device="cuda").manual_seed(7)
+    srcs = {"random": torch.randint(-128, 128, (waves * 8 * 1024,), device="cuda", dtype=torch.int8, generator=g),
+            "zeros": torch.zeros(waves * 8 * 1024, device="cuda", dtype=torch.int8)}
+    out = torch.empty(waves * 64, device="cuda", dtype=torch.int32)
+    clocks = torch.zeros(2, device="cuda", dtype=torch.int64)
+    ops = waves * iters * 8 * 65536.0
+    res = {}
+    for name, src in srcs.items():
+        def run():
+            st = L.lfm2q_calib_mfma_i8(src.data_ptr(), src.numel(), out.data_ptr(), out.numel() * 4,
+                                       clocks.data_ptr(), blocks, iters, torch.cuda.current_stream().cuda_stream)
+            assert st == 0, st
+        run()
+        torch.cuda.synchronize()
+        best = 1e30
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            run()
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e-3)
+        rt, sc = (int(v) for v in clocks.cpu())
+        ghz = sc / rt * 0.1 if rt else None
+        res[name] = {"tops": round(ops / best / 1e12, 1), "ms": round(best * 1e3, 3),
+                     "clock_ghz": round(ghz, 3) if ghz else None,
+                     "frac_of_published_peak": round(ops / best / 1e12 / INT8_PEAK_TOPS, 4)}
+        log(f"mfma rate ({name} operands): {res[name]['tops']} TOPS at {res[name]['clock_ghz']} GHz")
+    res["workload"] = f"{blocks} workgroups x 4 wavefronts x {iters} x 8 independent v_mfma_i32_32x32x32_i8"
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -655,6 +697,7 @@ def main():
                     help="run one decode kind (e.g. 'w1|w3+swiglu'), 'gemm:M,K,N', 'gemmg:M,K,N' (grouped scales) or 'copy' "
                          "eagerly, for counter collection")
     ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
+    ap.add_argument("--mfma-rate", action="store_true", help="only the sustained int8 matrix-core rate calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the library has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -663,6 +706,9 @@ def main():
 
     if args.eager_kind:
         eager_kind(args.eager_kind, int(args.batches.split(",")[0]), args.steps, args.wfmt)
+        return
+    if args.mfma_rate:
+        print(json.dumps({"mfma_sustained": mfma_rate()}))
         return
     if args.only_w8a8:
         print(json.dumps({"w8a8_shapes": w8a8_results(max(5, args.steps // 10))}))
@@ -715,6 +761,13 @@ def main():
                                     "kernel": "gemm_i8_bigp_kernel<0> (4096 x 2048 x 16384, persistent 256 x 256 tiles)",
                                     "achieved": big["tops_gemm"], "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                                     "frac": round(big["tops_gemm"] / INT8_PEAK_TOPS, 4)},
+                       # the same layer as the workload specifies it: bf16 activations quantized per token
+                       # (quant_rows) and then multiplied
+                       "roofline_with_quant": {"bound": "mfma", "kernels": "quant_kernel + gemm_i8_bigp_kernel<0>",
+                                               "achieved": big["tops_quant_gemm"], "peak": INT8_PEAK_TOPS,
+                                               "unit": "TOPS",
+                                               "frac": round(big["tops_quant_gemm"] / INT8_PEAK_TOPS, 4)},
+                       "mfma_sustained": mfma_rate(),
                        "all_shapes_tops_hipblaslt_int_mm_i32": round(ops / t_lib / 1e6, 1),
                        "all_shapes_tops_gemm": round(ops / t_gemm / 1e6, 1),
                        "all_shapes_tops_quant_gemm": round(ops / t_full / 1e6, 1),

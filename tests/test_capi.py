@@ -39,6 +39,12 @@ def test_ctypes_table_matches_header():
     assert sorted(_capi.SIGNATURES) == sorted(set(declared()) - {"lfm2q_last_error", "lfm2q_version"})
 
 
+def test_calibration_library_exports_its_entry_point():
+    """bench.py's MFMA-rate calibration (lib/liblfm2q_calib.so) is built beside the product library."""
+    calib = ctypes.CDLL(str(ROOT / "lfm2.5-vl-optimization_amd" / "lib" / "liblfm2q_calib.so"))
+    assert hasattr(calib, "lfm2q_calib_mfma_i8")
+
+
 def test_version(L):
     assert L.lfm2q_version().decode().startswith("lfm2q")
 
