@@ -142,8 +142,23 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.f + expf(-g)); }
 
 // GELU, tanh approximation, in fp32: 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
+// GELU, tanh form: 0.5 v (1 + tanh(u)), u = sqrt(2/pi) (v + 0.044715 v^3), with 1 + tanh(u) formed in fp32 as the
+// reference forms it (for large negative v that sum cancels, and the result follows it). tanh comes from the identity
+// tanh(a) = 1 - 2 / (e^{2a} + 1), a = |u|, sign restored afterwards: e^{2a} = 2^x, x = 2a log2(e) carried as
+// x_hi + x_lo (the fma residual of the rounded product plus the constant's own low part), 2^x_hi on v_exp_f32 times
+// the first-order correction 1 + x_lo ln 2, and v_rcp_f32 for the reciprocal (each within about an ulp). Near u = 0
+// the identity gives tanh only to ~1e-7 absolute -- not tanh's full relative accuracy there, but 1 + tanh(u) is all
+// the GELU uses, and that stays within an ulp or two. About 15 VALU instructions, against ~38 for the math
+// library's tanhf with its small-argument polynomial and range checks (the GELU epilogue dominated the GELU GEMMs).
 __device__ __forceinline__ float gelu_tanh_f32(float v) {
-    return 0.5f * v * (1.f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+    const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    const float a = __builtin_fabsf(u);
+    constexpr float C_HI = 2.88539004f, C_LO = 3.85192598e-8f;  // 2 log2(e) = C_HI + C_LO
+    const float xh = a * C_HI;
+    const float xl = __builtin_fmaf(a, C_HI, -xh) + a * C_LO;
+    const float e = __builtin_amdgcn_exp2f(xh) * __builtin_fmaf(xl, 0.693147182f, 1.f);  // e^{2a}; inf past 2^128
+    const float t = __builtin_fmaf(-2.f, __builtin_amdgcn_rcpf(e + 1.f), 1.f);            // tanh(a)
+    return 0.5f * v * (1.f + __builtin_copysignf(t, u));
 }
 
 }  // namespace lfm2q

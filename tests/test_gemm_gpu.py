@@ -106,6 +106,35 @@ def test_gemm_vs_oracle(E, M, K, N, bias, gelu):
     assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
 
 
+@pytest.mark.parametrize("tile", [None, (256, 256), (128, 64)])
+def test_gemm_gelu_epilogue_over_its_input_range(E, tile, tune):
+    """The GELU epilogue on ~1M distinct inputs: acc = 1 everywhere (one-hot A and B rows), so y[m, n] =
+    bf16(gelu((1 * sx[m]) * sw[n] + b[n])) with sx x sw spanning [-10, 10] densely, both tails included (the
+    negative tail, where 1 + tanh(u) cancels in fp32, and v > 3, where tanh(u) rounds to 1). Against the oracle's
+    fp32 GELU (the reference's formula with the C library's tanhf): <= 1 bf16 ulp everywhere, and 1-ulp outputs rare
+    (they can only come from fp32 values within a few ulps of a bf16 rounding boundary). Run on the persistent
+    256 x 256 epilogue and on a 4-wavefront tile."""
+    if tile:
+        tune("LFM2Q_GEMM_BM", tile[0])
+        tune("LFM2Q_GEMM_BN", tile[1])
+    M, N, K = 1024, 1032, 64
+    rng = np.random.default_rng(11)
+    xq = np.zeros((M, K), np.int8)
+    xq[:, 0] = 1
+    wq = np.zeros((N, K), np.int8)
+    wq[:, 0] = 1
+    sx = np.sort(rng.uniform(-10.0, 10.0, M)).astype(np.float32)
+    sw = rng.uniform(0.5, 1.0, N).astype(np.float32)
+    b = oracle.f2bf(rng.uniform(-0.05, 0.05, N).astype(np.float32))
+    ref = oracle.gemm_i8_epilogue(np.ones((M, N), np.int32), sx, sw, b, True)
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), dev_bf16(b), y, True)
+    u = ulp_dist(host_bits(y), ref)
+    print(f"GELU sweep: max {int(u.max())} ulp, {int((u > 0).sum())} of {u.size} outputs at 1 ulp")
+    assert int(u.max()) <= 1
+    assert (u > 0).sum() <= 1e-3 * u.size
+
+
 def _full_check(E, M, K, N, bias, gelu, seed):
     """Full-size GEMM: int32 against an exact fp64 product on the GPU, bf16 output of 256 sampled rows against the
     reference test's fp32 epilogue expression (tests/test_int8_gemm.py:166-172) evaluated by torch on the GPU."""
