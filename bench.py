@@ -445,18 +445,27 @@ def w8a8_results(reps):
             for W in Ws:
                 torch._int_mm(xq, W.t())
 
-        g_full, g_gemm, g_lib = capture(full), capture(gemm_only), capture(int_mm)
+        sx2 = torch.empty(M, device="cuda")
+
+        def fused():  # the same pair as one call: row scales, then the GEMM quantizing x on its way into LDS
+            for W in Ws:
+                E.gemm_i8_bf16a(x, sx2, W, sw, b, y, gelu)
+
+        g_full, g_gemm, g_lib, g_fused = capture(full), capture(gemm_only), capture(int_mm), capture(fused)
         t_full, _ = time_graph(g_full, reps, 2)
         t_gemm, _ = time_graph(g_gemm, reps, 2)
         t_lib, _ = time_graph(g_lib, reps, 2)
+        t_fused, _ = time_graph(g_fused, reps, 2)
         us_full, us_gemm, us_lib = t_full * 1e3 / ncopy, t_gemm * 1e3 / ncopy, t_lib * 1e3 / ncopy
+        us_fused = t_fused * 1e3 / ncopy
         ops = 2.0 * M * N * K
         out.append({"name": name, "M": M, "K": K, "N": N, "bias": bias, "gelu": gelu,
                     "us_gemm": round(us_gemm, 2), "us_quant_gemm": round(us_full, 2),
                     "tops_gemm": round(ops / us_gemm / 1e6, 1), "tops_quant_gemm": round(ops / us_full / 1e6, 1),
                     "mfma_frac_gemm": round(ops / us_gemm / 1e6 / INT8_PEAK_TOPS, 4),
-                    "us_hipblaslt_int_mm_i32": round(us_lib, 2), "tops_hipblaslt_int_mm_i32": round(ops / us_lib / 1e6, 1)})
-        del g_full, g_gemm, g_lib, Ws
+                    "us_hipblaslt_int_mm_i32": round(us_lib, 2), "tops_hipblaslt_int_mm_i32": round(ops / us_lib / 1e6, 1),
+                    "us_fused_quant_gemm": round(us_fused, 2), "tops_fused_quant_gemm": round(ops / us_fused / 1e6, 1)})
+        del g_full, g_gemm, g_lib, g_fused, Ws
         torch.cuda.empty_cache()
     return out
 
@@ -771,6 +780,8 @@ def main():
                        "all_shapes_tops_hipblaslt_int_mm_i32": round(ops / t_lib / 1e6, 1),
                        "all_shapes_tops_gemm": round(ops / t_gemm / 1e6, 1),
                        "all_shapes_tops_quant_gemm": round(ops / t_full / 1e6, 1),
+                       "all_shapes_tops_fused_quant_gemm": round(ops / sum(r["us_fused_quant_gemm"] for r in shapes)
+                                                                 / 1e6, 1),
                        "vision_layer_tops_gemm": round(vops / sum(r["us_gemm"] for r in vis) / 1e6, 1),
                        "vision_layer_tops_quant_gemm": round(vops / sum(r["us_quant_gemm"] for r in vis) / 1e6, 1),
                        "shapes": shapes}

@@ -189,6 +189,15 @@ int lfm2q_silu_mul_q(const lfm2q_bf16 *g, int8_t *q, float *s, lfm2q_bf16 *x, in
 int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
                   lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream);
 
+/* W8A8 GEMM on bf16 activations, quantized per token inside the GEMM: a first pass writes sa fp32 [M], the
+ * scales lfm2q_quant_rows would write for X, and the GEMM quantizes each stage of X bf16 [M, K] on its way into
+ * LDS with the quantizers' own code, so Y equals lfm2q_quant_rows + lfm2q_gemm_i8 on the same inputs bit for bit,
+ * without the int8 copy of X. K % 16 == 0; B, sb, bias, Y, gelu as in lfm2q_gemm_i8. Tiles of at most 128 x 128.
+ * The reference's per-token path runs quantize_rows and gemm_i8 as two kernels (src/lfm2opt/int8.py:45-51,
+ * kernels/int8_gemm.cu:391-432 then :125-297); this is the fused form of that pair. */
+int lfm2q_gemm_i8_bf16a(const lfm2q_bf16 *X, float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
+                        lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream);
+
 /* W8A8 GEMM with grouped-64 activation scales saT fp32 [K/64, M] (lfm2q_quant_groups' layout): per 64-wide K group g
  * the exact int32 partial sum folds into fp32 as facc = fma((float)part_g, saT[g, m], facc) in group order, then
  * Y[m, n] = bf16( gelu?( facc * sb[n] + bias[n] ) ) (two separately rounded ops). K % 64 == 0.

@@ -269,12 +269,13 @@ __device__ __forceinline__ void epilogue(const ACC (&acc)[TN][TM], const float *
 // facc = fma((float)acc, sxT[kt, m], facc), in stage order -- the reference's fold, exact per group since |acc| <=
 // 64 * 127^2 < 2^24. The group's scales for the tile's rows travel with the operands (one 4-byte direct load per
 // wavefront per stage into a 1 KiB LDS slot) and are read after the stage's barrier. YsT: OUT_Q8 scales.
-// Occupancy hint: two wavefronts per SIMD, except where the 6-stage ring of a large tile leaves room for one workgroup
-template <int BM, int BN, int NSTG>
-constexpr int gemm_waves_per_eu() { return NSTG == 6 && BM + BN > 192 ? 1 : 2; }
+// Occupancy hint: two wavefronts per SIMD, except where the 6-stage ring of a large tile (or the bf16 staging ring of
+// a 128-row tile) leaves room for one workgroup
+template <int BM, int BN, int NSTG, bool XBF = false>
+constexpr int gemm_waves_per_eu() { return (NSTG == 6 && BM + BN > 192) || (XBF && BM == 128) ? 1 : 2; }
 
-template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES, int KSP = 1>
-__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu<BM, BN, NSTG>()))) void gemm_i8_kernel(
+template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES, int KSP = 1, bool XBF = false>
+__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu<BM, BN, NSTG, XBF>()))) void gemm_i8_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
     int sh, float *__restrict__ YsT = nullptr) {
@@ -290,8 +291,14 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
     // grouped path folds fp32 scales stage by stage, in order.
     static_assert(KSP == 1 || (!GRP && !out_q8(OUT)), "split K needs the int32 accumulators of the per-token path");
     static_assert(KSP == 1 || (KSP - 1) * BM * BN * 4 <= KSP * NSTG * (BM + BN) * BK, "partials exceed the rings");
+    // XBF: X is bf16 [M, K] and sx its rows' quant_rows scales. Each stage's activations come global -> LDS by direct
+    // loads (bf16, 128-byte rows) beside the weights, and each wavefront quantizes the rows it loaded itself
+    // (quant8, the quantizers' own code) into the int8 slot the direct int8 loads would have filled.
+    static_assert(!XBF || (!GRP && KSP == 1 && NSTG == 3 && BM <= 128), "bf16 activations: per-token, 3-stage ring");
+    constexpr int IXB = XBF ? BM / 32 : 1;  // bf16 activation loads per wavefront per stage (8 rows x 128 bytes)
+    constexpr int XBS = XBF ? NSTG * BM * 2 * BK : 0;  // bf16 staging ring
     constexpr int RING = NSTG * (BM + BN) * BK;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[KSP * RING + (GRP ? NSTG * 1024 : 0)];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[KSP * RING + (GRP ? NSTG * 1024 : 0) + XBS];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int grp = KSP == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 8);  // K group of this wavefront
@@ -326,13 +333,57 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         cw[j] = 16 * ((lane & 3) ^ ((row >> sh) & 3));
         ow[j] = (uint32_t)row * K + cw[j];
     }
+    // XBF: instruction j of wavefront w loads tile rows 8 (4 j + w) .. + 7 of the stage into its bf16 slot (1 KiB,
+    // 128 bytes a row); lane i takes row 8 (4 j + w) + i / 8 and its values e8 = i % 8 (8 bf16), which become int8
+    // bytes 8 e8 .. + 7 of the row's 64-byte slice: logical chunk e8 / 2, half e8 % 2, at that chunk's swizzled
+    // slot. Rows past M and values past K read zeros.
+    uint8_t(*sXb)[BM * 2 * BK] = reinterpret_cast<uint8_t(*)[BM * 2 * BK]>(smem + KSP * RING + (GRP ? NSTG * 1024 : 0));
+    v4i rxb = {};
+    uint32_t oxb[IXB];
+    int dxb[IXB], exb[IXB];
+    float sxb[IXB], rxb_[IXB];
+    if constexpr (XBF) {
+        const uint16_t *Xb = reinterpret_cast<const uint16_t *>(X);
+        rxb = make_desc(Xb + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K * 2, 0x7fffffffL));
+#pragma unroll
+        for (int j = 0; j < IXB; ++j) {
+            const int row = 8 * (4 * j + wave) + (lane >> 3), e8 = lane & 7;
+            exb[j] = 8 * e8;
+            oxb[j] = (uint32_t)row * K * 2 + 16 * e8;
+            dxb[j] = swz(row, e8 >> 1, sh) + 8 * (e8 & 1);
+            sxb[j] = m0 + row < M ? sx[m0 + row] : 1.f;
+            rxb_[j] = 1.f / sxb[j];
+        }
+    }
+    // XBF: this wavefront's rows of stage kt, bf16 slot -> int8 slot (its own direct loads of the stage have
+    // landed: the caller waited; nothing else reads the bf16 slot)
+    auto quant_xb = [&](int kt) {
+        // the s_waitcnt builtin is not a memory operation to the compiler: keep the slot's reads below it
+        asm volatile("" ::: "memory");
+        const uint8_t *b_s = sXb[kt % NSTG];
+        uint8_t *x_s = sX[kt % NSTG];
+#pragma unroll
+        for (int j = 0; j < IXB; ++j) {
+            const v4i v = *reinterpret_cast<const v4i *>(b_s + 1024 * (4 * j + wave) + 16 * lane);
+            int lo, hi;
+            quant8(v, sxb[j], rxb_[j], lo, hi);
+            *reinterpret_cast<int2 *>(x_s + dxb[j]) = make_int2(lo, hi);
+        }
+    };
     auto issue = [&](int kt) {  // kt: this group's stage index
         const int buf = kt % NSTG, k0 = (kt0 + kt) * BK;
+        if constexpr (XBF)
 #pragma unroll
-        for (int j = 0; j < IX; ++j) {
-            const uint32_t vo = k0 + cx[j] < K ? ox[j] + k0 : 0xfffffff0u;
-            lds_dma16(rx, vo, lds_addr(sX[buf] + 1024 * (4 * j + wave)));
-        }
+            for (int j = 0; j < IXB; ++j) {
+                const uint32_t vo = k0 + exb[j] < K ? oxb[j] + 2 * k0 : 0xfffffff0u;
+                lds_dma16(rxb, vo, lds_addr(sXb[buf] + 1024 * (4 * j + wave)));
+            }
+        else
+#pragma unroll
+            for (int j = 0; j < IX; ++j) {
+                const uint32_t vo = k0 + cx[j] < K ? ox[j] + k0 : 0xfffffff0u;
+                lds_dma16(rx, vo, lds_addr(sX[buf] + 1024 * (4 * j + wave)));
+            }
 #pragma unroll
         for (int j = 0; j < IW; ++j) {
             const uint32_t vo = k0 + cw[j] < K ? ow[j] + k0 : 0xfffffff0u;
@@ -370,19 +421,8 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         for (int j = 0; j < TM; ++j) fx[kk][j] = swz(wm * WMt + 32 * j + lr, 2 * kk + lh, sh);
     }
 
-    static_assert((NSTG - 2) * (IX + IW + IS) <= 63 && NSTG - 2 <= 6, "vmcnt holds at most 63 loads");
-#pragma unroll
-    for (int p = 0; p < NSTG - 1; ++p)
-        if (p < KT) issue(p);
-    for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
-        // stage kt has landed once at most the loads of the (up to NSTG - 2) stages issued after it are outstanding
-        wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
-        // stage kt visible to all; everyone is done with stage kt - 1, whose buffer refills next. A bare s_barrier:
-        // __syncthreads()' fences would make the compiler drain every outstanding load here, the prefetches included
-        // (LDS needs no cache maintenance between the wavefronts of a workgroup).
-        asm volatile("s_barrier" ::: "memory");
-        if (KSP > 1 && kt >= KT) continue;  // this group's stages are done; it keeps meeting the barriers
-        if (kt + NSTG - 1 < KT) issue(kt + NSTG - 1);
+    // the MFMAs of stage kt (its operands are in LDS and visible)
+    auto compute = [&](int kt) {
         const uint8_t *x_s = sX[kt % NSTG], *w_s = sW[kt % NSTG];
         // both k steps' fragments are read up front, the second set while the first set's MFMAs run
         v4i wf[2][TN], xf[2][TM];
@@ -416,6 +456,45 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
                             __builtin_fmaf((float)acc[i][j][e], sj, facc[GRP ? i : 0][GRP ? j : 0][e]);
             }
         }
+    };
+
+    if constexpr (XBF) {
+        // Stage kt + 2 is issued after stage kt's barrier; after stage kt's MFMAs each wavefront waits for its own
+        // loads of stage kt + 1 and quantizes its activation rows into stage kt + 1's int8 slot (last read in stage
+        // kt - 2), which stage kt + 1's barrier then makes visible together with its weights.
+        constexpr int PER = IXB + IW;
+        static_assert(PER <= 63, "vmcnt holds at most 63 loads");
+        if (0 < KT) issue(0);
+        if (1 < KT) issue(1);
+        if (0 < KT) {
+            wait_stages<PER>(1 < KT ? 1 : 0);
+            quant_xb(0);
+        }
+        for (int kt = 0; kt < KT; ++kt) {
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (kt + 2 < KT) issue(kt + 2);
+            compute(kt);
+            if (kt + 1 < KT) {
+                wait_stages<PER>(kt + 2 < KT ? 1 : 0);
+                quant_xb(kt + 1);
+            }
+        }
+    } else {
+    static_assert((NSTG - 2) * (IX + IW + IS) <= 63 && NSTG - 2 <= 6, "vmcnt holds at most 63 loads");
+#pragma unroll
+    for (int p = 0; p < NSTG - 1; ++p)
+        if (p < KT) issue(p);
+    for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
+        // stage kt has landed once at most the loads of the (up to NSTG - 2) stages issued after it are outstanding
+        wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
+        // stage kt visible to all; everyone is done with stage kt - 1, whose buffer refills next. A bare s_barrier:
+        // __syncthreads()' fences would make the compiler drain every outstanding load here, the prefetches included
+        // (LDS needs no cache maintenance between the wavefronts of a workgroup).
+        asm volatile("s_barrier" ::: "memory");
+        if (KSP > 1 && kt >= KT) continue;  // this group's stages are done; it keeps meeting the barriers
+        if (kt + NSTG - 1 < KT) issue(kt + NSTG - 1);
+        compute(kt);
+    }
     }
 
     __syncthreads();  // every wavefront is done with the operand ring, which now holds the epilogue slices
@@ -1069,6 +1148,26 @@ void launch_gemm_grouped(const int8_t *A, const int8_t *B, const float *sxT, con
 #undef LFM2Q_GEMM
 }
 
+// bf16 activations quantized inside the GEMM (sx = their quant_rows scales): the tiles of at most 128 token rows
+template <int OUT>
+void launch_gemm_bf16a(const uint16_t *X, const int8_t *B, const float *sx, const float *sw, const uint16_t *bias,
+                       void *Y, int M, int N, int K, hipStream_t st) {
+    const TileCfg t = pick_tile(M, N, K, TILES_GROUPED);
+    const int sh = knob_int(KNOB_GEMM_SWZ, 2);
+    const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
+    const int8_t *Xv = reinterpret_cast<const int8_t *>(X);
+#define LFM2Q_GEMM(BM_, BN_)                                                                                        \
+    if (t.bm == BM_ && t.bn == BN_) {                                                                                \
+        gemm_i8_kernel<BM_, BN_, OUT, false, 3, 1, true><<<grid, GT, 0, st>>>(Xv, B, sx, sw, bias, Y, M, N, K, sh);  \
+        return;                                                                                                      \
+    }
+    LFM2Q_GEMM(128, 128)
+    LFM2Q_GEMM(128, 64)
+    LFM2Q_GEMM(64, 128)
+    LFM2Q_GEMM(64, 64)
+#undef LFM2Q_GEMM
+}
+
 template <int OUT>
 void launch_gemm_w8(const uint16_t *X, const int8_t *W, const float *sw, const uint16_t *bias, uint16_t *Y, int M,
                     int N, int K, hipStream_t st) {
@@ -1125,6 +1224,25 @@ extern "C" int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, 
     else
         launch_gemm<OUT_BF16>(A, B, sa, sb, bias, Y, M, N, K, (hipStream_t)stream);
     return launch_status("gemm_i8");
+}
+
+extern "C" int lfm2q_gemm_i8_bf16a(const lfm2q_bf16 *X, float *sa, const int8_t *B, const float *sb,
+                                   const lfm2q_bf16 *bias, lfm2q_bf16 *Y, int M, int N, int K, int gelu,
+                                   lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(X && sa && B && sb && Y, LFM2Q_ERR_ARG, "gemm_i8_bf16a: null pointer");
+    LFM2Q_REQUIRE(M >= 1 && N >= 1 && K >= 16 && K % 16 == 0, LFM2Q_ERR_SHAPE,
+                  "gemm_i8_bf16a: need M, N >= 1, K >= 16 and K %% 16 == 0 (M=%d N=%d K=%d)", M, N, K);
+    LFM2Q_REQUIRE((long)M * K * 2 < (1L << 31) && (long)N * K < (1L << 31), LFM2Q_ERR_SHAPE,
+                  "gemm_i8_bf16a: each operand must be smaller than 2 GiB (buffer offsets are 32-bit)");
+    LFM2Q_REQUIRE(aligned16(X) && aligned16(B) && ((uintptr_t)sa & 3) == 0, LFM2Q_ERR_ALIGN,
+                  "gemm_i8_bf16a: X and B must be 16-byte aligned");
+    const hipStream_t st = (hipStream_t)stream;
+    if (int e = launch_row_scales(X, sa, M, K, st)) return e;
+    if (gelu)
+        launch_gemm_bf16a<OUT_BF16_GELU>(X, B, sa, sb, bias, Y, M, N, K, st);
+    else
+        launch_gemm_bf16a<OUT_BF16>(X, B, sa, sb, bias, Y, M, N, K, st);
+    return launch_status("gemm_i8_bf16a");
 }
 
 extern "C" int lfm2q_gemm_i8_grouped(const int8_t *A, const float *saT, const int8_t *B, const float *sb,

@@ -100,6 +100,20 @@ __global__ __launch_bounds__(256) void quant_kernel(const uint16_t *__restrict__
     }
 }
 
+// Per-row scales only, s = max(amax, 1e-8) / 127 -- the s of quant_rows (a maximum does not depend on the order it
+// is taken in): the first pass of the bf16-activation GEMM, which quantizes the rows itself with these scales.
+__global__ __launch_bounds__(256) void row_scale_kernel(const uint16_t *__restrict__ x, float *__restrict__ s, int rows,
+                                                        int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = row_of_wave();
+    if (row >= rows) return;
+    const uint16_t *xr = x + (size_t)row * K;
+    float m = 0.f;
+    for (int c = lane; c < K / 8; c += 64) m = absmax8(ld16(xr + (size_t)c * 8), m);
+    m = wave_max(m);
+    if (lane == 0) s[row] = scale_of(m);
+}
+
 // ------------------------------------------------------------------------------------------------ producers
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
@@ -284,6 +298,12 @@ int check_rows(const char *name, int rows, int len, int grouped, int maxlen) {
 }
 
 }  // namespace
+
+int launch_row_scales(const uint16_t *x, float *s, int rows, int K, hipStream_t st) {
+    row_scale_kernel<<<(rows + 3) / 4, 256, 0, st>>>(x, s, rows, K);
+    return launch_status("row scales");
+}
+
 }  // namespace lfm2q
 
 using namespace lfm2q;

@@ -50,4 +50,7 @@ __device__ __forceinline__ float absmax8(v4i xv, float m) {
 
 __device__ __forceinline__ float scale_of(float amax) { return fmaxf(amax, 1e-8f) / 127.f; }
 
+// s[r] = quant_rows' scale of row r of x (bf16 [rows, K], K % 8 == 0), on `st` (quant.hip)
+int launch_row_scales(const uint16_t *x, float *s, int rows, int K, hipStream_t st);
+
 }  // namespace lfm2q

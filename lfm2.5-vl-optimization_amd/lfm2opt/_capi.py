@@ -41,6 +41,7 @@ SIGNATURES = {
     "lfm2q_silu_mul_q": [_P, _P, _P, _P, _I, _I, _I, _P],
     "lfm2q_gemm_i8": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_grouped": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "lfm2q_gemm_i8_bf16a": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_w8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_i32": [_P, _P, _P, _I, _I, _I, _P],

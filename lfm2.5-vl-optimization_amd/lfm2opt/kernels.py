@@ -272,6 +272,21 @@ class Int8Ops:
                    w.data_ptr(), sw.data_ptr(), _capi.ptr(bias), y.data_ptr(), M, N, K, int(bool(gelu)),
                    _capi.stream(xq))
 
+    def gemm_i8_bf16a(self, x, sx, w, sw, bias, y, gelu):
+        """The per-token pair quant_rows(x) + gemm_i8 as one call on bf16 activations x [M, K]: sx [M] receives the
+        scales quant_rows would write, the GEMM quantizes x inside (no int8 copy of x), and y is bit-identical to
+        the pair's. Reference pair: src/lfm2opt/int8.py:45-51 (quantize_rows, then gemm_i8)."""
+        _check_bf16(x, "x")
+        _check_t(sx, torch.float32, "sx")
+        K = x.size(-1)
+        M = x.numel() // K if K else 0
+        if sx.numel() != M:
+            raise RuntimeError("sx shape")
+        N = self._check_common(w, sw, bias, y, M, K)
+        _same_device(x, sx, w, sw, bias, y)
+        _capi.call("lfm2q_gemm_i8_bf16a", x.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias),
+                   y.data_ptr(), M, N, K, int(bool(gelu)), _capi.stream(x))
+
     def gemm_i8_q(self, xq, sxT, w, sw, bias, yq, ysT, gelu):
         """Grouped W8A8 writing the next W8A8 GEMM's input: (yq [M, N], ysT [N/64, M]) = quant_groups(the bf16 output
         gemm_i8 would write), bit-identical to that pair of calls. Reference: gemm_i8_q(), kernels/int8_gemm.cpp:53-69

@@ -106,6 +106,64 @@ def test_gemm_vs_oracle(E, M, K, N, bias, gelu):
     assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
 
 
+def _bf16a_vs_pair(E, x, w, sw, b, gelu):
+    """gemm_i8_bf16a(x) against quant_rows(x) + gemm_i8: the scales and every output bit for bit."""
+    M, K = x.shape
+    N = w.shape[0]
+    xq = torch.empty(M, K, device="cuda", dtype=torch.int8)
+    s = torch.empty(M, device="cuda")
+    y1 = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.quant_rows(x, xq, s)
+    E.gemm_i8(xq, s, w, sw, b, y1, gelu)
+    s2 = torch.full((M,), -1.0, device="cuda")
+    y2 = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8_bf16a(x, s2, w, sw, b, y2, gelu)
+    torch.cuda.synchronize()
+    assert torch.equal(s2, s), "scales differ from quant_rows'"
+    assert torch.equal(y2.view(torch.int16), y1.view(torch.int16)), \
+        f"{int((y2.view(torch.int16) != y1.view(torch.int16)).sum())} outputs differ from quant_rows + gemm_i8"
+
+
+@pytest.mark.parametrize("tile", [None, (128, 128), (128, 64), (64, 128), (64, 64)])
+@pytest.mark.parametrize("M,K,N,bias,gelu", [(70, 1152, 96, True, True), (129, 4304, 72, True, False),
+                                             (1, 16, 8, False, False), (300, 2048, 3072, False, False),
+                                             (513, 8192, 2048, False, False), (64, 64, 1000, True, True)])
+def test_gemm_bf16a_equals_quant_then_gemm(E, M, K, N, bias, gelu, tile, tune):
+    """bf16 activations quantized inside the GEMM: ragged M / N / K tails, every tile, K from one stage to 128
+    stages; activations ~N(0,1) with 0.1 % outliers at 20 sigma."""
+    if tile:
+        tune("LFM2Q_GEMM_BM", tile[0])
+        tune("LFM2Q_GEMM_BN", tile[1])
+    g = torch.Generator(device="cuda").manual_seed(M * 3 + K + N)
+    x = torch.randn(M, K, device="cuda", generator=g)
+    x = torch.where(torch.rand(M, K, device="cuda", generator=g) < 1e-3, 20.0 * torch.sign(x), x).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+    sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+    _bf16a_vs_pair(E, x, w, sw, b, gelu)
+
+
+def test_gemm_bf16a_division_traps(E):
+    """The golden rows whose values sit where x * (1/s) and x / s round to different integers: the in-GEMM
+    quantization takes the same IEEE-division branch as quant_rows."""
+    f = load("quant_rows_traps_k64")
+    x = dev_bf16(f["x"])
+    M, K = x.shape
+    g = torch.Generator(device="cuda").manual_seed(3)
+    w = torch.randint(-127, 128, (40, K), device="cuda", dtype=torch.int8, generator=g)
+    sw = torch.rand(40, device="cuda", generator=g) * 0.01 + 1e-3
+    _bf16a_vs_pair(E, x, w, sw, None, False)
+
+
+def test_gemm_bf16a_full_shape(E):
+    """The 4096 x 2048 x 16384 prefill w1|w3 shape (128 x 128 tiles, 32 stages) against the pair, every output."""
+    g = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn(4096, 2048, device="cuda", generator=g).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (16384, 2048), device="cuda", dtype=torch.int8, generator=g)
+    sw = torch.rand(16384, device="cuda", generator=g) * 0.01 + 1e-3
+    _bf16a_vs_pair(E, x, w, sw, None, False)
+
+
 @pytest.mark.parametrize("tile", [None, (256, 256), (128, 64)])
 def test_gemm_gelu_epilogue_over_its_input_range(E, tile, tune):
     """The GELU epilogue on ~1M distinct inputs: acc = 1 everywhere (one-hot A and B rows), so y[m, n] =
