@@ -651,6 +651,61 @@ def producer_results(reps):
     return res
 
 
+# every (tile, K split) configuration of the per-token W8A8 kernels (the cost model's candidates)
+GEMM_CONFIGS = [(256, 256, 1), (128, 256, 1), (128, 256, 2), (256, 128, 1), (256, 128, 2), (128, 128, 1),
+                (128, 128, 2), (128, 64, 1), (128, 64, 2), (128, 64, 4), (64, 128, 1), (64, 128, 2), (64, 128, 4),
+                (64, 64, 1), (64, 64, 2), (64, 64, 4)]
+
+
+def gemm_sweep(reps):
+    """The per-token W8A8 GEMM on the 13 shapes under every forced (tile, K split) and under the automatic choice,
+    timed as in w8a8_results (one call per rotated weight copy in a graph): how far the cost model's pick is from
+    the best configuration of each shape."""
+    from lfm2opt import _capi
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    knobs = ("LFM2Q_GEMM_BM", "LFM2Q_GEMM_BN", "LFM2Q_GEMM_KSPLIT")
+    out = []
+    for M, K, N, bias, gelu, name in W8A8_SHAPES:
+        log(f"sweep {name} {M}x{K}x{N}")
+        g = torch.Generator(device="cuda").manual_seed(M + K + N)
+        ncopy = max(2, -(-512 * 2 ** 20 // (N * K)))
+        Ws = [torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g) for _ in range(ncopy)]
+        sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+        b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+        xq = torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8, generator=g)
+        sx = torch.rand(M, device="cuda", generator=g) * 0.01 + 1e-3
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+
+        def fn():
+            for W in Ws:
+                E.gemm_i8(xq, sx, W, sw, b, y, gelu)
+
+        us = {}
+        try:
+            for cfg in [None] + GEMM_CONFIGS:
+                for k in knobs:
+                    _capi.set_tuning(k, None)
+                if cfg:
+                    for k, v in zip(knobs, cfg):
+                        _capi.set_tuning(k, v)
+                graph = capture(fn)
+                t = min(time_graph(graph, reps, 2)[0] for _ in range(2))
+                us["auto" if cfg is None else "%dx%d/%d" % cfg] = round(t * 1e3 / ncopy, 2)
+                del graph
+        finally:
+            for k in knobs:
+                _capi.set_tuning(k, None)
+        best = min((v, k) for k, v in us.items() if k != "auto")
+        out.append({"name": name, "M": M, "K": K, "N": N, "us": us, "best": best[1], "us_best": best[0],
+                    "us_auto": us["auto"]})
+        del Ws
+        torch.cuda.empty_cache()
+    return {"shapes": out, "us_auto_total": round(sum(r["us_auto"] for r in out), 1),
+            "us_best_total": round(sum(r["us_best"] for r in out), 1)}
+
+
 def mfma_rate(iters=20000):
     """The int8 matrix-core rate the chip sustains (lib/liblfm2q_calib.so: every SIMD issuing nothing but
     independent v_mfma_i32_32x32x32_i8, two wavefronts per SIMD) on random and on all-zero operand bytes, with the
@@ -707,6 +762,8 @@ def main():
                          "eagerly, for counter collection")
     ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
     ap.add_argument("--mfma-rate", action="store_true", help="only the sustained int8 matrix-core rate calibration")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="only the per-token W8A8 GEMM under every forced (tile, K split) on the 13 shapes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the library has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -715,6 +772,9 @@ def main():
 
     if args.eager_kind:
         eager_kind(args.eager_kind, int(args.batches.split(",")[0]), args.steps, args.wfmt)
+        return
+    if args.gemm_sweep:
+        print(json.dumps({"gemm_sweep": gemm_sweep(max(5, args.steps // 20))}))
         return
     if args.mfma_rate:
         print(json.dumps({"mfma_sustained": mfma_rate()}))
