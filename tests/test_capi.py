@@ -70,6 +70,12 @@ def test_status_codes_without_launch(L):
     assert "at most 128" in L.lfm2q_last_error().decode()
     assert L.lfm2q_gemv_chain_noalloc(ctypes.addressof(table), fake, 0, None, None) == 2
     assert L.lfm2q_gemv_chain_noalloc(ctypes.addressof(table), ctypes.c_void_p(0x1008), 1, None, None) == 3
+    # the W8A8 GEMM on bf16 activations: pointers, K % 16, alignment
+    assert L.lfm2q_gemm_i8_bf16a(None, fake, fake, fake, None, fake, 4, 8, 64, 0, None) == 1
+    assert L.lfm2q_gemm_i8_bf16a(fake, fake, fake, fake, None, fake, 4, 8, 72, 0, None) == 2
+    assert "K % 16 == 0" in L.lfm2q_last_error().decode()
+    assert L.lfm2q_gemm_i8_bf16a(fake, fake, fake, fake, None, fake, 0, 8, 64, 0, None) == 2
+    assert L.lfm2q_gemm_i8_bf16a(ctypes.c_void_p(0x1008), fake, fake, fake, None, fake, 4, 8, 64, 0, None) == 3
 
 
 def test_python_checks_match_reference_wording():
