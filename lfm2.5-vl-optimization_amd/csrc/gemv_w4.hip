@@ -554,7 +554,8 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
 // Launch shape from (weight rows, K, B) only -- a plain and a fused call over the same weights (w1|w3 as one
 // [2 S, K/8] matrix) then split K alike, which keeps the fused epilogues bit-identical:
 //   KS = 2 (8-row tiles) for batches up to 8 and at most 2048 weight rows; RT = 2 for 6144+ weight rows unless
-//   KS = 2, RT = 4 (at most 4 wavefronts) for 32768+ rows without SwiGLU (the lm_head, batch 8: 27.9 -> 26.6 us);
+//   KS = 2 or SwiGLU at batches up to 8, RT = 4 (at most 4 wavefronts) for 32768+ rows without SwiGLU (the lm_head,
+//   batch 8: 27.9 -> 26.6 us);
 //   NWK from the 256-k blocks per wavefront: 2 (4 when KS = 2, with at least 4 wavefronts past K = 2048), at most 8
 //   wavefronts for two-tile workgroups and 16 otherwise. INT4 costs twice the VALU work per weight byte
 //   of INT8, so its wavefronts take half the blocks (measured on MI355X at batches 2, 4 and 8). The
@@ -581,7 +582,9 @@ void launch_w4_mfma(const uint8_t *W, const void *S, const int32_t *Z, const uin
     const long wrows = EPI == EPI_SWIGLU ? 2L * N : N;
     const int nblk = (K + 255) / 256;
     int ks = (B <= 8 && wrows <= 2048) ? 2 : 1;
-    int rt = (ks == 1 && wrows >= 6144) ? 2 : 1;
+    // two row tiles per workgroup from 6144 weight rows, except w1|w3 + SwiGLU up to batch 8, where one tile per
+    // workgroup (twice the workgroups) measured faster: 8.4-8.9 -> 7.6-8.3 us at batches 2-8 (even at 16)
+    int rt = (ks == 1 && wrows >= 6144 && !(EPI == EPI_SWIGLU && B <= 8)) ? 2 : 1;
     if (EPI != EPI_SWIGLU && ks == 1 && wrows >= 32768) rt = 4;  // the lm_head: four tiles share each activation load
     const int bpw = ks == 2 ? 4 : 2;  // target blocks per wavefront
     int nwk = 1;
