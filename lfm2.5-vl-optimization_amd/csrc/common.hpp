@@ -14,19 +14,23 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
 
-// bf16 is carried as its raw 16-bit pattern everywhere (uint16_t); conversions are done by hand so that the
-// rounding mode is explicit: fp32 -> bf16 is round-to-nearest-even, NaN stays a quiet NaN.
+// bf16 is carried as its raw 16-bit pattern everywhere (uint16_t). fp32 -> bf16 is gfx950's v_cvt_pk_bf16_f32
+// (one instruction per pair of values): round to nearest even, and a NaN becomes the quiet NaN with its sign and
+// upper payload, i.e. for every fp32 pattern u the bits of the explicit formula
+//   NaN: (u >> 16) | 0x40,   otherwise: (u + 0x7fff + ((u >> 16) & 1)) >> 16
+// (checked on the device against that formula over 2^20 patterns spanning every exponent, with the NaN, denormal,
+// tie and overflow cases), which is how the CPU oracle rounds.
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 __device__ __forceinline__ float bf2f_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf2f_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-__device__ __forceinline__ uint32_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
+__device__ __forceinline__ uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }  // round to bf16 and back
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {  // lo in bits 0-15, hi in bits 16-31
+    const v2bf r = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, r);
+}
 
 // DPP lane permutations within a 16-lane row (no LDS traffic, unlike ds_bpermute).
 template <int CTRL>
@@ -138,25 +142,58 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(p));
 }
 
-// SiLU exactly as the decode path rounds it: silu(g) = g / (1 + exp(-g)) in fp32.
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.f + expf(-g)); }
+// SiLU as the reference computes it, silu(g) = g / (1 + exp(-g)) in fp32, on the hardware exp2 and reciprocal:
+// exp(-g) = 2^x, x = t log2(e) with t = -g, carried as x_hi + x_lo (the fma residual of the rounded product plus the
+// constant's own low part), 2^x_hi on v_exp_f32 times the first-order correction 1 + x_lo ln 2, then d = 1 + exp(-g)
+// rounded as the reference rounds it; the quotient g / d from v_rcp_f32 with one fma correction,
+// q - (q d - g) r. The edges, each without a branch:
+//  - t is clamped to [-128, 128] (v_med3): exp(-g) has rounded to 0 or inf well before, and past |t| ~ 2^24 x_lo is no
+//    longer small (the correction factor could turn the overflow negative, and t log2(e) itself overflows near
+//    FLT_MAX);
+//  - v_rcp_f32 flushes a denormal result, so past d = 2^64 (g < -44) the quotient is formed as (g 2^-64) / (d 2^-64)
+//    (exact scalings; the result stays a normal number down to where exp(-g) overflows);
+//  - once exp(-g) has overflowed, r = 1/inf = 0 and q = g x 0 = -0, the reference's g / inf; d is capped at 2^64 in
+//    the residual so that q d does not become 0 x inf (finite d never reaches the cap after the scaling). g = -inf
+//    gives NaN, as g / inf does;
+//  - the residual is written q d - g, not g - q d, so that g = -0 keeps its sign through the correction;
+//  - g = +inf is the one select (the residual is inf - inf there); the reference gives g / 1.
+// Contraction is off so that every rounding is the one written. About 20 VALU instructions against ~25 plus branches
+// for the math library's expf and the IEEE division. The callers all round g to bf16 first and the result to bf16
+// after; over all 65536 bf16 inputs the result equals the C library's g / (1 + expf(-g)) rounded to bf16.
+__device__ __forceinline__ float silu_f32(float g) {
+#pragma clang fp contract(off)
+    constexpr float L_HI = 1.44269502f, L_LO = 1.92596299e-8f;  // log2(e) = L_HI + L_LO
+    const float t = __builtin_amdgcn_fmed3f(-g, -128.f, 128.f);
+    const float xh = t * L_HI;
+    const float xl = __builtin_fmaf(t, L_LO, __builtin_fmaf(t, L_HI, -xh));
+    const float e = __builtin_amdgcn_exp2f(xh) * __builtin_fmaf(xl, 0.693147182f, 1.f);
+    const float d = 1.f + e;
+    const float sc = d > 0x1p64f ? 0x1p-64f : 1.f;
+    const float ds = d * sc, gs = g * sc;
+    const float r = __builtin_amdgcn_rcpf(ds);
+    const float q = gs * r;
+    const float rr = __builtin_fmaf(q, __builtin_fminf(ds, 0x1p64f), -gs);
+    const float res = __builtin_fmaf(-rr, r, q);
+    return g == __builtin_inff() ? g : res;
+}
 
-// GELU, tanh approximation, in fp32: 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
 // GELU, tanh form: 0.5 v (1 + tanh(u)), u = sqrt(2/pi) (v + 0.044715 v^3), with 1 + tanh(u) formed in fp32 as the
 // reference forms it (for large negative v that sum cancels, and the result follows it). tanh comes from the identity
 // tanh(a) = 1 - 2 / (e^{2a} + 1), a = |u|, sign restored afterwards: e^{2a} = 2^x, x = 2a log2(e) carried as
 // x_hi + x_lo (the fma residual of the rounded product plus the constant's own low part), 2^x_hi on v_exp_f32 times
-// the first-order correction 1 + x_lo ln 2, and v_rcp_f32 for the reciprocal (each within about an ulp). Near u = 0
-// the identity gives tanh only to ~1e-7 absolute -- not tanh's full relative accuracy there, but 1 + tanh(u) is all
-// the GELU uses, and that stays within an ulp or two. About 15 VALU instructions, against ~38 for the math
-// library's tanhf with its small-argument polynomial and range checks (the GELU epilogue dominated the GELU GEMMs).
+// the first-order correction 1 + x_lo ln 2, and v_rcp_f32 for the reciprocal (each within about an ulp). a is capped
+// at 16, where tanh already rounds to 1 in fp32: past |v| ~ 7e12 the cube overflows, u is inf and x_lo would be
+// inf - inf. Near u = 0 the identity gives tanh only to ~1e-7 absolute -- not tanh's full relative accuracy there,
+// but 1 + tanh(u) is all the GELU uses, and that stays within an ulp or two. About 16 VALU instructions, against ~38
+// for the math library's tanhf with its small-argument polynomial and range checks (the GELU epilogue dominated the
+// GELU GEMMs).
 __device__ __forceinline__ float gelu_tanh_f32(float v) {
     const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-    const float a = __builtin_fabsf(u);
+    const float a = __builtin_fminf(__builtin_fabsf(u), 16.f);
     constexpr float C_HI = 2.88539004f, C_LO = 3.85192598e-8f;  // 2 log2(e) = C_HI + C_LO
     const float xh = a * C_HI;
     const float xl = __builtin_fmaf(a, C_HI, -xh) + a * C_LO;
-    const float e = __builtin_amdgcn_exp2f(xh) * __builtin_fmaf(xl, 0.693147182f, 1.f);  // e^{2a}; inf past 2^128
+    const float e = __builtin_amdgcn_exp2f(xh) * __builtin_fmaf(xl, 0.693147182f, 1.f);  // e^{2a}
     const float t = __builtin_fmaf(-2.f, __builtin_amdgcn_rcpf(e + 1.f), 1.f);            // tanh(a)
     return 0.5f * v * (1.f + __builtin_copysignf(t, u));
 }

@@ -50,13 +50,6 @@ __device__ __forceinline__ float dequant(float facc, float, float sw, float b) {
     return v + b;
 }
 
-typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {  // round to nearest even (v_cvt_pk_bf16_f32)
-    v2bf_t r;
-    r[0] = (__bf16)lo;
-    r[1] = (__bf16)hi;
-    return __builtin_bit_cast(uint32_t, r);
-}
 
 // Workgroup -> output tile. Workgroups are dealt to the 8 XCDs round-robin (workgroup w runs on XCD w % 8), so the
 // tile sequence is split into 8 contiguous bands and band x is given to the workgroups of XCD x; inside the band

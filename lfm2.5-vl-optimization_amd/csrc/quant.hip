@@ -115,7 +115,6 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const uint16_t *__restri
 }
 
 // ------------------------------------------------------------------------------------------------ producers
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
 // row (+ residual) -> registers. ADD: h = bf16(h + y), written back. Lanes past the row get zeros.
 template <int CH>
@@ -131,7 +130,7 @@ __device__ __forceinline__ void load_row_add(uint16_t *__restrict__ hr, const ui
                 const v4i yv = ld16(yr + (size_t)i * 8);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    hv[c][j] = (int)pack2(bf2f_lo((uint32_t)hv[c][j]) + bf2f_lo((uint32_t)yv[j]),
+                    hv[c][j] = (int)pack_bf16x2(bf2f_lo((uint32_t)hv[c][j]) + bf2f_lo((uint32_t)yv[j]),
                                           bf2f_hi((uint32_t)hv[c][j]) + bf2f_hi((uint32_t)yv[j]));
                 *reinterpret_cast<v4i *>(hr + (size_t)i * 8) = hv[c];
             }
@@ -180,7 +179,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_q_kernel(uint16_t *__restrict
             const v4i wv = ld16(w + (size_t)i * 8);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                xv[c][j] = (int)pack2(bf2f_lo((uint32_t)wv[j]) * rbf(bf2f_lo((uint32_t)hv[c][j]) * rs),
+                xv[c][j] = (int)pack_bf16x2(bf2f_lo((uint32_t)wv[j]) * rbf(bf2f_lo((uint32_t)hv[c][j]) * rs),
                                       bf2f_hi((uint32_t)wv[j]) * rbf(bf2f_hi((uint32_t)hv[c][j]) * rs));
         }
     }
@@ -232,7 +231,7 @@ __global__ __launch_bounds__(256) void add_layernorm_q_kernel(uint16_t *__restri
             for (int j = 0; j < 4; ++j) {
                 const float lo = ((bf2f_lo((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_lo((uint32_t)wv[j]);
                 const float hi = ((bf2f_hi((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_hi((uint32_t)wv[j]);
-                xv[c][j] = (int)pack2(lo + bf2f_lo((uint32_t)bv[j]), hi + bf2f_hi((uint32_t)bv[j]));
+                xv[c][j] = (int)pack_bf16x2(lo + bf2f_lo((uint32_t)bv[j]), hi + bf2f_hi((uint32_t)bv[j]));
             }
         }
     }
@@ -258,7 +257,7 @@ __global__ __launch_bounds__(256) void silu_mul_q_kernel(const uint16_t *__restr
             const v4i av = ld_nt16(gr + (size_t)i * 8), uv = ld_nt16(gr + I + (size_t)i * 8);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                xv[c][j] = (int)pack2(rbf(silu_f32(bf2f_lo((uint32_t)av[j]))) * bf2f_lo((uint32_t)uv[j]),
+                xv[c][j] = (int)pack_bf16x2(rbf(silu_f32(bf2f_lo((uint32_t)av[j]))) * bf2f_lo((uint32_t)uv[j]),
                                       rbf(silu_f32(bf2f_hi((uint32_t)av[j]))) * bf2f_hi((uint32_t)uv[j]));
         }
     }
