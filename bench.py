@@ -651,10 +651,11 @@ def producer_results(reps):
     return res
 
 
-# every (tile, K split) configuration of the per-token W8A8 kernels (the cost model's candidates)
-GEMM_CONFIGS = [(256, 256, 1), (128, 256, 1), (128, 256, 2), (256, 128, 1), (256, 128, 2), (128, 128, 1),
-                (128, 128, 2), (128, 64, 1), (128, 64, 2), (128, 64, 4), (64, 128, 1), (64, 128, 2), (64, 128, 4),
-                (64, 64, 1), (64, 64, 2), (64, 64, 4)]
+# every (tile, K split) configuration of the per-token W8A8 kernels (the cost model's candidates); 256 x 256 and
+# the first 256 x 128 are the persistent kernels, "256x128/1g" the one-tile-per-workgroup 256 x 128 kernel
+GEMM_CONFIGS = [(256, 256, 1), (128, 256, 1), (128, 256, 2), (256, 128, 1), (256, 128, 1, 0), (256, 128, 2),
+                (128, 128, 1), (128, 128, 2), (128, 64, 1), (128, 64, 2), (128, 64, 4), (64, 128, 1), (64, 128, 2),
+                (64, 128, 4), (64, 64, 1), (64, 64, 2), (64, 64, 4)]
 
 
 def gemm_sweep(reps):
@@ -665,7 +666,7 @@ def gemm_sweep(reps):
     from lfm2opt.kernels import int8_ext
 
     E = int8_ext()
-    knobs = ("LFM2Q_GEMM_BM", "LFM2Q_GEMM_BN", "LFM2Q_GEMM_KSPLIT")
+    knobs = ("LFM2Q_GEMM_BM", "LFM2Q_GEMM_BN", "LFM2Q_GEMM_KSPLIT", "LFM2Q_GEMM_BIGP")
     out = []
     for M, K, N, bias, gelu, name in W8A8_SHAPES:
         log(f"sweep {name} {M}x{K}x{N}")
@@ -692,7 +693,8 @@ def gemm_sweep(reps):
                         _capi.set_tuning(k, v)
                 graph = capture(fn)
                 t = min(time_graph(graph, reps, 2)[0] for _ in range(2))
-                us["auto" if cfg is None else "%dx%d/%d" % cfg] = round(t * 1e3 / ncopy, 2)
+                label = "auto" if cfg is None else "%dx%d/%d" % cfg[:3] + ("g" if len(cfg) > 3 else "")
+                us[label] = round(t * 1e3 / ncopy, 2)
                 del graph
         finally:
             for k in knobs:

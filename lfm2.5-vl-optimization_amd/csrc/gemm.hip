@@ -793,27 +793,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                           smem + wave * stage_bytes<TN>());
 }
 
-// Persistent form of the 256 x 256 kernel (128-byte stages, two ring slots): one workgroup per CU walks the tiles
-// w, w + grid, ... (same XCD bands as tile_of). When a tile's K loop ends, the next tile's first stage and its
+// Persistent form of the 256 x BN kernels (BN = 256 or 128; 128-byte stages, two ring slots; 8 wavefronts as 4 x 2
+// blocks of 64 x BN/2): one workgroup per CU walks the tiles w, w + grid, ... (same XCD bands as tile_of). The
+// 256 x 128 tile gives the shapes whose 256 x 256 tiles leave CUs idle (w2 at 4096 tokens: 128 tiles) one tile per
+// CU at the same per-wavefront MFMA : LDS-read ratio as the generic kernels' best. When a tile's K loop ends, the next tile's first stage and its
 // epilogue operands (the 256 token scales, 256 weight scales and 256 bias values, by direct loads into a second
 // small LDS buffer) are issued before the epilogue runs, so their latency hides behind the dequant and the stores,
 // and the stores drain while the next tile's first stage computes: the stage-0 wait leaves exactly the wavefront's
 // SST staged stores outstanding. Staged stores are buffer stores whose out-of-range lanes get an offset past the
 // buffer (dropped by the range check), so every wavefront issues the same number; the staging area is the ring
-// slot the last stage used, 32 rows x 256 bytes per wavefront with 16-byte granule g of row r at g ^ (r % 16).
+// slot the last stage used, 32 rows x BN bytes per wavefront with 16-byte granule g of row r at g ^ (r % (BN / 16)).
 // bf16 output only, with N % 8 == 0, 16-byte aligned Y, 4-byte aligned bias (its dword loads) and M N 2 < 2^31
 // (the launcher checks): the epilogue then issues no vector memory loads, so nothing but the staged stores is
 // outstanding when the next tile's first stage is waited for.
-template <int OUT>
+template <int OUT, int BN>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_bigp_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K) {
     static_assert(OUT == OUT_BF16 || OUT == OUT_BF16_GELU, "bf16 output only");
-    constexpr int BM = 256, BN = 256, BKT = 128, WMt = 64, WNt = 128, TM = 2, TN = 4;
-    constexpr int CPR = BKT / 16, RPI = 64 / CPR, IL = BM / RPI / 8, KS = BKT / 32;
-    constexpr int SLOT = 2 * BM * BKT;             // one stage of both operands (64 KiB)
-    constexpr int EOP = 4 * BM + 4 * BN + 2 * BN;  // one tile's epilogue operands: sx, sw, bias (2.5 KiB)
-    constexpr int SST = TM * 32 / 4;               // staged stores per wavefront per tile (4 rows per store)
+    static_assert(BN == 256 || BN == 128, "256 x 256 or 256 x 128 tiles");
+    constexpr int BM = 256, BKT = 128, WMt = 64, WNt = BN / 2, TM = 2, TN = WNt / 32;
+    constexpr int CPR = BKT / 16, RPI = 64 / CPR, ILX = BM / RPI / 8, ILW = BN / RPI / 8, KS = BKT / 32;
+    constexpr int SLOT = (BM + BN) * BKT;          // one stage of both operands (64 / 48 KiB)
+    constexpr int EOP = 4 * BM + 4 * BN + 2 * BN;  // one tile's epilogue operands: sx, sw, bias (2.5 / 2 KiB)
+    constexpr int G = WNt / 8;                     // 16-byte granules per staged output row (2 WNt bytes)
+    constexpr int RPS = 64 / G;                    // staged rows per store instruction
+    constexpr int SST = TM * 32 / RPS;             // staged stores per wavefront per tile
     static_assert(8 * 32 * 2 * WNt <= SLOT, "epilogue staging exceeds a ring slot");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SLOT + 2 * EOP];
 
@@ -824,10 +829,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     int t = blockIdx.x;
     if (t >= T) return;  // the launch sizes the grid to at most T; uniform per workgroup
 
-    uint32_t off[IL];
-    int cb[IL];
+    uint32_t off[ILX];
+    int cb[ILX];
 #pragma unroll
-    for (int j = 0; j < IL; ++j) {
+    for (int j = 0; j < ILX; ++j) {
         const int row = RPI * (8 * j + wave) + lane / CPR;
         cb[j] = swzb<CPR>(row, lane % CPR) - row * BKT;
         off[j] = (uint32_t)row * K + cb[j];
@@ -848,13 +853,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         const uint32_t sX = lbase + slot * SLOT, sW = sX + BM * BKT;
         const int k0 = kt * BKT;
 #pragma unroll
-        for (int j = 0; j < IL; ++j) {
+        for (int j = 0; j < ILX; ++j) {
             const bool in = k0 + cb[j] < K;
             lds_dma16(rx, in ? off[j] + k0 : 0xfffffff0u, sX + 1024 * (8 * j + wbase));
-            lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, sW + 1024 * (8 * j + wbase));
+            if (j < ILW) lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, sW + 1024 * (8 * j + wbase));
         }
     };
-    // the tile's token scales (waves 0-3, 64 each), weight scales (waves 4-7) and bias (waves 0-1) into LDS
+    // the tile's token scales (waves 0-3, 64 each), weight scales (waves 4 .. 4 + BN / 64 - 1) and bias (waves
+    // 0 .. BN / 128 - 1, 128 each) into LDS: sx at 0, sw at 4 BM, bias at 4 BM + 4 BN
     const v4i rsx = make_desc(sx, (uint32_t)M * 4), rsw = make_desc(sw, (uint32_t)N * 4);
     const v4i rb = make_desc(bias, bias ? (uint32_t)N * 2 : 0u);
     auto issue_eop = [&](int e) {
@@ -864,9 +870,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         asm volatile("" : "+v"(l));
         if (wbase < 4) {
             lds_dma4(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
-            if (wbase < 2 && bias) lds_dma4(rb, (uint32_t)(n0 + 128 * wbase + 2 * l) * 2, eb + 2048 + 256 * wbase);
-        } else {
-            lds_dma4(rsw, (uint32_t)(n0 + 64 * (wbase - 4) + l) * 4, eb + 1024 + 256 * (wbase - 4));
+            if (wbase < BN / 128 && bias)
+                lds_dma4(rb, (uint32_t)(n0 + 128 * wbase + 2 * l) * 2, eb + 4 * BM + 4 * BN + 256 * wbase);
+        } else if (wbase < 4 + BN / 64) {
+            lds_dma4(rsw, (uint32_t)(n0 + 64 * (wbase - 4) + l) * 4, eb + 4 * BM + 256 * (wbase - 4));
         }
     };
     const rsrc_t ry = make_rsrc(Y, (uint32_t)((size_t)M * N * 2));
@@ -931,9 +938,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         {
             const uint8_t *eb = smem + 2 * SLOT + (it & 1) * EOP;
             const float *sxs = reinterpret_cast<const float *>(eb);
-            const float *sws = reinterpret_cast<const float *>(eb + 1024);
-            const uint16_t *bs = reinterpret_cast<const uint16_t *>(eb + 2048);
-            uint8_t *stage = smem + ((g - 1) & 1) * SLOT + wave * 8192;
+            const float *sws = reinterpret_cast<const float *>(eb + 4 * BM);
+            const uint16_t *bs = reinterpret_cast<const uint16_t *>(eb + 4 * BM + 4 * BN);
+            uint8_t *stage = smem + ((g - 1) & 1) * SLOT + wave * (32 * 2 * WNt);
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const float s_m = sxs[wm * WMt + 32 * j + lr];
@@ -957,14 +964,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                         if (out_gelu(OUT))
 #pragma unroll
                             for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f32(v[e]);
-                        *reinterpret_cast<uint2 *>(stage + lr * 256 + (((4 * i + q) ^ (lr & 15)) << 4) + 8 * lh) =
-                            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                        *reinterpret_cast<uint2 *>(stage + lr * (2 * WNt) + (((4 * i + q) ^ (lr & (G - 1))) << 4) +
+                                                   8 * lh) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                     }
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                for (int rr = 0; rr < 32; rr += 4) {
-                    const int r = rr + (lane >> 4), c = lane & 15;
-                    const v4i v = *reinterpret_cast<const v4i *>(stage + r * 256 + ((c ^ (r & 15)) << 4));
+                for (int rr = 0; rr < 32; rr += RPS) {
+                    const int r = rr + lane / G, c = lane % G;
+                    const v4i v = *reinterpret_cast<const v4i *>(stage + r * (2 * WNt) + ((c ^ (r & (G - 1))) << 4));
                     const int mo = mb + 32 * j + r, no = nb + 8 * c;
                     const uint32_t o = (mo < M && no < N) ? (uint32_t)(((size_t)mo * N + no) * 2) : 0xfffffff0u;
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), ry, (int)o, 0, 0);
@@ -985,7 +992,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 struct TileCfg {
     int bm, bn, resident;
     double a, b;
-    int ksp = 1;  // wavefront groups splitting K inside the workgroup (per-token path)
+    int ksp = 1;   // wavefront groups splitting K inside the workgroup (per-token path)
+    int pers = 0;  // the persistent 256 x BN kernel (per-token bf16 output, where its conditions hold)
 };
 
 // Tile sets: per-token (all seven), grouped (the four tiles whose fp32 accumulators fit beside the int32 ones), and
@@ -1024,31 +1032,35 @@ inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
 }
 
 // Per-token path: the seven tiles, each also with K split over 2 (and, for the small tiles, 4) wavefront groups,
-// fitted like the table above to MI355X timings of every (tile, split) on the 13 LFM2 prefill / SigLIP2 shapes
-// (`resident` = workgroups one CU holds at that split). The LFM2Q_GEMM_BM / _BN knobs force a tile,
-// LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced).
+// and the persistent 256 x 128 kernel, fitted like the table above to MI355X timings of every (tile, split) on the
+// 13 LFM2 prefill / SigLIP2 shapes (`resident` = workgroups one CU holds at that split). The LFM2Q_GEMM_BM / _BN
+// knobs force a tile, LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced); 256 x 128 forced means the
+// persistent kernel unless LFM2Q_GEMM_BIGP is 0.
 inline TileCfg pick_tile_pt(int M, int N, int K) {
     const int force_bm = knob_int(KNOB_GEMM_BM, 0), force_bn = knob_int(KNOB_GEMM_BN, 0);
     const int force_ks = knob_int(KNOB_GEMM_KSPLIT, 0);
+    const bool pers_ok = knob_int(KNOB_GEMM_BIGP, 1) != 0;
     static const TileCfg opts[] = {
-        {256, 256, 1, 0.1582, 10.87, 1}, {128, 256, 2, 0.2912, 7.604, 1}, {128, 256, 1, 0.2721, 10.14, 2},
+        {256, 256, 1, 0.1582, 10.87, 1, 1}, {256, 128, 1, 0.2632, 3.586, 1, 1},
+        {128, 256, 2, 0.2912, 7.604, 1}, {128, 256, 1, 0.2721, 10.14, 2},
         {256, 128, 2, 0.2911, 7.455, 1}, {256, 128, 1, 0.2572, 10.95, 2}, {128, 128, 3, 0.3494, 5.003, 1},
         {128, 128, 1, 0.3449, 5.533, 2}, {128, 64, 4, 0.4546, 3.930, 1},  {128, 64, 2, 0.4729, 2.456, 2},
         {128, 64, 1, 0.5114, 3.760, 4},  {64, 128, 4, 0.4555, 3.970, 1},  {64, 128, 2, 0.4864, 2.494, 2},
         {64, 128, 1, 0.5502, 3.505, 4},  {64, 64, 6, 0.5660, 3.086, 1},   {64, 64, 3, 0.6101, 0.836, 2},
         {64, 64, 1, 0.7027, 2.256, 4}};
+    const auto usable = [&](const TileCfg &o) { return pers_ok || !o.pers || o.bn == 256; };
     if (force_bm && force_bn) {
         const int ks = force_ks == 4 ? 4 : force_ks == 2 ? 2 : 1;
         for (const TileCfg &o : opts)
-            if (o.bm == force_bm && o.bn == force_bn && o.ksp == ks) return o;
+            if (o.bm == force_bm && o.bn == force_bn && o.ksp == ks && usable(o)) return o;
         for (const TileCfg &o : opts)
-            if (o.bm == force_bm && o.bn == force_bn && o.ksp == 1) return o;
+            if (o.bm == force_bm && o.bn == force_bn && o.ksp == 1 && usable(o)) return o;
     }
     const long cus = device_cus();
     double best = 1e300;
-    TileCfg bestc = opts[5];
+    TileCfg bestc = opts[6];
     for (const TileCfg &o : opts) {
-        if (force_ks && o.ksp != force_ks) continue;
+        if ((force_ks && o.ksp != force_ks) || !usable(o)) continue;
         const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
         const long per = (tiles + cus - 1) / cus;
         const double t = o.a * (double)per * o.bm * o.bn * (double)K * 1e-6 + o.b * (double)((per + o.resident - 1) / o.resident);
@@ -1066,16 +1078,21 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
     const TileCfg t = pick_tile_pt(M, N, K);
     const int sh = knob_int(KNOB_GEMM_SWZ, 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
-    if (t.bm == 256 && t.bn == 256) {
+    if (t.pers) {
         if constexpr (OUT == OUT_BF16 || OUT == OUT_BF16_GELU) {
             // persistent form: one workgroup per CU (its LDS allows no second), at most one per tile
             if (knob_int(KNOB_GEMM_BIGP, 1) && K > 0 && (N & 7) == 0 && ((uintptr_t)Y & 15) == 0 &&
                 ((uintptr_t)bias & 3) == 0 && (size_t)M * N * 2 < 0x80000000ull) {
                 const int pgrid = (int)std::min<long>((long)grid.x, device_cus());
-                gemm_i8_bigp_kernel<OUT><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                if (t.bn == 256)
+                    gemm_i8_bigp_kernel<OUT, 256><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                else
+                    gemm_i8_bigp_kernel<OUT, 128><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 return;
             }
         }
+    }
+    if (t.bm == 256 && t.bn == 256) {
         // ring shape (K bytes per stage x stages); the LFM2Q_GEMM_RING knob (1282 / 644 / 645) forces one
         switch (knob_int(KNOB_GEMM_RING, 1282)) {
         case 644: gemm_i8_big_kernel<OUT, 64, 4><<<grid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K); break;
