@@ -793,10 +793,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                           smem + wave * stage_bytes<TN>());
 }
 
-// Persistent form of the 256 x BN kernels (BN = 256 or 128; 128-byte stages, two ring slots; 8 wavefronts as 4 x 2
-// blocks of 64 x BN/2): one workgroup per CU walks the tiles w, w + grid, ... (same XCD bands as tile_of). The
-// 256 x 128 tile gives the shapes whose 256 x 256 tiles leave CUs idle (w2 at 4096 tokens: 128 tiles) one tile per
-// CU at the same per-wavefront MFMA : LDS-read ratio as the generic kernels' best. When a tile's K loop ends, the next tile's first stage and its
+// Persistent form of the BM x BN kernels (256 x 256, 256 x 128, 128 x 128; 128-byte stages, two ring slots; 8
+// wavefronts as 4 x 2 blocks of BM/4 x BN/2): one workgroup per CU walks the tiles w, w + grid, ... (same XCD bands
+// as tile_of). The smaller tiles give the shapes whose 256 x 256 tiles leave CUs idle (w2 at 4096 tokens: 128
+// tiles of 256 x 256, 256 of 256 x 128; at 2048 tokens 256 of 128 x 128) one tile per CU. When a tile's K loop ends, the next tile's first stage and its
 // epilogue operands (the 256 token scales, 256 weight scales and 256 bias values, by direct loads into a second
 // small LDS buffer) are issued before the epilogue runs, so their latency hides behind the dequant and the stores,
 // and the stores drain while the next tile's first stage computes: the stage-0 wait leaves exactly the wavefront's
@@ -806,21 +806,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 // bf16 output only, with N % 8 == 0, 16-byte aligned Y, 4-byte aligned bias (its dword loads) and M N 2 < 2^31
 // (the launcher checks): the epilogue then issues no vector memory loads, so nothing but the staged stores is
 // outstanding when the next tile's first stage is waited for.
-template <int OUT, int BN>
+template <int OUT, int BM, int BN, int NSLOT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_bigp_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K) {
     static_assert(OUT == OUT_BF16 || OUT == OUT_BF16_GELU, "bf16 output only");
-    static_assert(BN == 256 || BN == 128, "256 x 256 or 256 x 128 tiles");
-    constexpr int BM = 256, BKT = 128, WMt = 64, WNt = BN / 2, TM = 2, TN = WNt / 32;
+    static_assert((BM == 256 && (BN == 256 || BN == 128)) || (BM == 128 && BN == 128), "tile shape");
+    constexpr int BKT = 128, WMt = BM / 4, WNt = BN / 2, TM = WMt / 32, TN = WNt / 32;
     constexpr int CPR = BKT / 16, RPI = 64 / CPR, ILX = BM / RPI / 8, ILW = BN / RPI / 8, KS = BKT / 32;
     constexpr int SLOT = (BM + BN) * BKT;          // one stage of both operands (64 / 48 KiB)
     constexpr int EOP = 4 * BM + 4 * BN + 2 * BN;  // one tile's epilogue operands: sx, sw, bias (2.5 / 2 KiB)
     constexpr int G = WNt / 8;                     // 16-byte granules per staged output row (2 WNt bytes)
     constexpr int RPS = 64 / G;                    // staged rows per store instruction
     constexpr int SST = TM * 32 / RPS;             // staged stores per wavefront per tile
+    constexpr int LPS = ILX + ILW;                 // operand loads per wavefront per stage
     static_assert(8 * 32 * 2 * WNt <= SLOT, "epilogue staging exceeds a ring slot");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SLOT + 2 * EOP];
+    static_assert(NSLOT >= 2 && NSLOT <= 4 && NSLOT * SLOT + 2 * EOP <= 160 * 1024, "LDS ring");
+    static_assert((NSLOT - 2) * LPS + SST < 64, "vmcnt holds 6 bits");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSLOT * SLOT + 2 * EOP];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
@@ -859,17 +862,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             if (j < ILW) lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, sW + 1024 * (8 * j + wbase));
         }
     };
-    // the tile's token scales (waves 0-3, 64 each), weight scales (waves 4 .. 4 + BN / 64 - 1) and bias (waves
-    // 0 .. BN / 128 - 1, 128 each) into LDS: sx at 0, sw at 4 BM, bias at 4 BM + 4 BN
+    // the tile's token scales (waves 0 .. BM / 64 - 1, 64 each), weight scales (waves 4 .. 4 + BN / 64 - 1) and bias
+    // (waves 0 .. BN / 128 - 1, 128 each) into LDS: sx at 0, sw at 4 BM, bias at 4 BM + 4 BN
     const v4i rsx = make_desc(sx, (uint32_t)M * 4), rsw = make_desc(sw, (uint32_t)N * 4);
     const v4i rb = make_desc(bias, bias ? (uint32_t)N * 2 : 0u);
     auto issue_eop = [&](int e) {
-        const uint32_t eb = lbase + 2 * SLOT + e * EOP;
+        const uint32_t eb = lbase + NSLOT * SLOT + e * EOP;
         // recomputed here rather than kept live across the K loop (register pressure)
         int l = lane;
         asm volatile("" : "+v"(l));
         if (wbase < 4) {
-            lds_dma4(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
+            if (wbase < BM / 64) lds_dma4(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
             if (wbase < BN / 128 && bias)
                 lds_dma4(rb, (uint32_t)(n0 + 128 * wbase + 2 * l) * 2, eb + 4 * BM + 4 * BN + 256 * wbase);
         } else if (wbase < 4 + BN / 64) {
@@ -879,10 +882,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     const rsrc_t ry = make_rsrc(Y, (uint32_t)((size_t)M * N * 2));
 
     at_tile(t);
-    issue(0, 0);
+#pragma unroll
+    for (int p = 0; p < NSLOT - 1; ++p)
+        if (p < KT) issue(p, p);
     issue_eop(0);
     const int lr = lane & 31, lh = lane >> 5;
-    int g = 0;  // ring stage counter across tiles: stage g sits in slot g & 1
+    int g = 0;  // ring stage counter across tiles: stage g sits in slot g % NSLOT
     for (int it = 0;; ++it) {
         v16i acc[TN][TM];
 #pragma unroll
@@ -892,15 +897,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
         for (int kt = 0; kt < KT; ++kt, ++g) {
-            // stage kt has landed once this wavefront's loads are done; at a tile's first stage the previous
-            // epilogue's staged stores, issued after those loads, may still be in flight
-            if (kt == 0 && it > 0)
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(SST));
-            else
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            asm volatile("s_barrier" ::: "memory");  // every wavefront's loads of stage kt landed; slot g + 1 is free
-            if (kt + 1 < KT) issue(kt + 1, (g + 1) & 1);
-            const uint8_t *x_s = smem + (g & 1) * SLOT, *w_s = x_s + BM * BKT;
+            // stage kt has landed once at most the loads of the f stages issued after it remain outstanding (and,
+            // at a tile's first stage, the previous epilogue's staged stores, issued after those loads); the next
+            // tile's epilogue-operand loads sit between its stages and the stores, so the counts only wait longer
+            const int f = min(NSLOT - 2, KT - 1 - kt);
+            if (kt == 0 && it > 0) {
+                if (NSLOT >= 4 && f == 2)
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPS + SST));
+                else if (NSLOT >= 3 && f == 1)
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPS + SST));
+                else
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(SST));
+            } else {
+                if (NSLOT >= 4 && f == 2)
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPS));
+                else if (NSLOT >= 3 && f == 1)
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPS));
+                else
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            }
+            asm volatile("s_barrier" ::: "memory");  // every wavefront's loads of stage kt landed; slot g - 1 is free
+            if (kt + NSLOT - 1 < KT) issue(kt + NSLOT - 1, (g + NSLOT - 1) % NSLOT);
+            const uint8_t *x_s = smem + (g % NSLOT) * SLOT, *w_s = x_s + BM * BKT;
             v4i wf[2][TN], xf[2][TM];
             auto rd = [&](int set, int kk) {
                 const int c = 2 * kk + lh;
@@ -924,23 +942,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        // the next tile's first stage (slot g & 1, free since the barrier of this tile's last stage) and epilogue
-        // operands go out before this tile's epilogue
+        // the next tile's first NSLOT - 1 stages (slots g .. g + NSLOT - 2, every slot but the last stage's: free
+        // since the barrier of this tile's last stage) and epilogue operands go out before this tile's epilogue
         const int tnext = t + (int)gridDim.x;
         const int pm0 = m0, pn0 = n0;
         if (tnext < T) {
             at_tile(tnext);
-            issue(0, g & 1);
+#pragma unroll
+            for (int p = 0; p < NSLOT - 1; ++p)
+                if (p < KT) issue(p, (g + p) % NSLOT);
             issue_eop((it + 1) & 1);
         }
         asm volatile("s_barrier" ::: "memory");  // every wavefront is done with the last stage's slot
         const int mb = pm0 + wm * WMt, nb = pn0 + wn * WNt;
         {
-            const uint8_t *eb = smem + 2 * SLOT + (it & 1) * EOP;
+            const uint8_t *eb = smem + NSLOT * SLOT + (it & 1) * EOP;
             const float *sxs = reinterpret_cast<const float *>(eb);
             const float *sws = reinterpret_cast<const float *>(eb + 4 * BM);
             const uint16_t *bs = reinterpret_cast<const uint16_t *>(eb + 4 * BM + 4 * BN);
-            uint8_t *stage = smem + ((g - 1) & 1) * SLOT + wave * (32 * 2 * WNt);
+            uint8_t *stage = smem + ((g + NSLOT - 1) % NSLOT) * SLOT + wave * (32 * 2 * WNt);
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const float s_m = sxs[wm * WMt + 32 * j + lr];
@@ -993,7 +1013,7 @@ struct TileCfg {
     int bm, bn, resident;
     double a, b;
     int ksp = 1;   // wavefront groups splitting K inside the workgroup (per-token path)
-    int pers = 0;  // the persistent 256 x BN kernel (per-token bf16 output, where its conditions hold)
+    int pers = 0;  // the persistent BM x BN kernel (per-token bf16 output, where its conditions hold)
 };
 
 // Tile sets: per-token (all seven), grouped (the four tiles whose fp32 accumulators fit beside the int32 ones), and
@@ -1032,23 +1052,23 @@ inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
 }
 
 // Per-token path: the seven tiles, each also with K split over 2 (and, for the small tiles, 4) wavefront groups,
-// and the persistent 256 x 128 kernel, fitted like the table above to MI355X timings of every (tile, split) on the
+// and the persistent 256 x 128 and 128 x 128 kernels, fitted like the table above to MI355X timings of every (tile, split) on the
 // 13 LFM2 prefill / SigLIP2 shapes (`resident` = workgroups one CU holds at that split). The LFM2Q_GEMM_BM / _BN
-// knobs force a tile, LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced); 256 x 128 forced means the
-// persistent kernel unless LFM2Q_GEMM_BIGP is 0.
+// knobs force a tile, LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced); 256 x 128 or 128 x 128 forced
+// means the persistent kernel unless LFM2Q_GEMM_BIGP is 0.
 inline TileCfg pick_tile_pt(int M, int N, int K) {
     const int force_bm = knob_int(KNOB_GEMM_BM, 0), force_bn = knob_int(KNOB_GEMM_BN, 0);
     const int force_ks = knob_int(KNOB_GEMM_KSPLIT, 0);
     const bool pers_ok = knob_int(KNOB_GEMM_BIGP, 1) != 0;
     static const TileCfg opts[] = {
-        {256, 256, 1, 0.1582, 10.87, 1, 1}, {256, 128, 1, 0.2632, 3.586, 1, 1},
+        {256, 256, 1, 0.1582, 10.87, 1, 1}, {256, 128, 1, 0.2030, 5.781, 1, 1}, {128, 128, 1, 0.2880, 2.877, 1, 1},
         {128, 256, 2, 0.2912, 7.604, 1}, {128, 256, 1, 0.2721, 10.14, 2},
         {256, 128, 2, 0.2911, 7.455, 1}, {256, 128, 1, 0.2572, 10.95, 2}, {128, 128, 3, 0.3494, 5.003, 1},
         {128, 128, 1, 0.3449, 5.533, 2}, {128, 64, 4, 0.4546, 3.930, 1},  {128, 64, 2, 0.4729, 2.456, 2},
         {128, 64, 1, 0.5114, 3.760, 4},  {64, 128, 4, 0.4555, 3.970, 1},  {64, 128, 2, 0.4864, 2.494, 2},
         {64, 128, 1, 0.5502, 3.505, 4},  {64, 64, 6, 0.5660, 3.086, 1},   {64, 64, 3, 0.6101, 0.836, 2},
         {64, 64, 1, 0.7027, 2.256, 4}};
-    const auto usable = [&](const TileCfg &o) { return pers_ok || !o.pers || o.bn == 256; };
+    const auto usable = [&](const TileCfg &o) { return pers_ok || !o.pers || (o.bm == 256 && o.bn == 256); };
     if (force_bm && force_bn) {
         const int ks = force_ks == 4 ? 4 : force_ks == 2 ? 2 : 1;
         for (const TileCfg &o : opts)
@@ -1058,7 +1078,7 @@ inline TileCfg pick_tile_pt(int M, int N, int K) {
     }
     const long cus = device_cus();
     double best = 1e300;
-    TileCfg bestc = opts[6];
+    TileCfg bestc = opts[7];
     for (const TileCfg &o : opts) {
         if ((force_ks && o.ksp != force_ks) || !usable(o)) continue;
         const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
@@ -1084,10 +1104,18 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
             if (knob_int(KNOB_GEMM_BIGP, 1) && K > 0 && (N & 7) == 0 && ((uintptr_t)Y & 15) == 0 &&
                 ((uintptr_t)bias & 3) == 0 && (size_t)M * N * 2 < 0x80000000ull) {
                 const int pgrid = (int)std::min<long>((long)grid.x, device_cus());
-                if (t.bn == 256)
-                    gemm_i8_bigp_kernel<OUT, 256><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                // LDS ring: as many slots as LDS holds (2, 3, 4); LFM2Q_GEMM_STAGES = 2 forces two
+                const bool two = knob_int(KNOB_GEMM_STAGES, 0) == 2;
+                if (t.bm == 256 && t.bn == 256)
+                    gemm_i8_bigp_kernel<OUT, 256, 256, 2><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                else if (t.bm == 256 && two)
+                    gemm_i8_bigp_kernel<OUT, 256, 128, 2><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                else if (t.bm == 256)
+                    gemm_i8_bigp_kernel<OUT, 256, 128, 3><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                else if (two)
+                    gemm_i8_bigp_kernel<OUT, 128, 128, 2><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 else
-                    gemm_i8_bigp_kernel<OUT, 128><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                    gemm_i8_bigp_kernel<OUT, 128, 128, 4><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 return;
             }
         }

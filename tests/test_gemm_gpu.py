@@ -257,15 +257,15 @@ def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, tune):
         assert int(ulp_dist(host_bits(y), oracle.gemm_i8_epilogue(acc, sx, sw, b)).max()) == 0, f"bf16 K={K}"
 
 
-@pytest.mark.parametrize("bn", [256, 128])
+@pytest.mark.parametrize("bm,bn", [(256, 256), (256, 128), (128, 128)])
 @pytest.mark.parametrize("bias,gelu", [(False, False), (True, True)])
-def test_gemm_persistent_big_tiles(E, bias, gelu, bn, tune):
-    """The persistent 256 x 256 and 256 x 128 kernels with more tiles than workgroups (17 x 17 or 17 x 33 tiles on
-    one workgroup per CU, so workgroups take further tiles whose first stage and epilogue operands load during the
-    previous tile's epilogue), with M, N and K tails: bf16 output against the oracle's epilogue of the exact int32
-    product (bit-exact, <= 1 ulp with GELU) and bit-identical to the one-tile-per-workgroup kernel of the same tile
-    (LFM2Q_GEMM_BIGP=0)."""
-    tune("LFM2Q_GEMM_BM", "256")
+def test_gemm_persistent_big_tiles(E, bias, gelu, bm, bn, tune):
+    """The persistent 256 x 256, 256 x 128 and 128 x 128 kernels with more tiles than workgroups (17 x 17, 17 x 33 or
+    33 x 33 tiles on one workgroup per CU, so workgroups take further tiles whose first stage and epilogue operands
+    load during the previous tile's epilogue), with M, N and K tails: bf16 output against the oracle's epilogue of
+    the exact int32 product (bit-exact, <= 1 ulp with GELU) and bit-identical to the one-tile-per-workgroup kernel
+    of the same tile (LFM2Q_GEMM_BIGP=0)."""
+    tune("LFM2Q_GEMM_BM", str(bm))
     tune("LFM2Q_GEMM_BN", str(bn))
     M, K, N = 4100, 272, 4104
     xq, sx, wq, sw, b = _operands(M + N + int(gelu), M, K, N, bias)
@@ -281,12 +281,12 @@ def test_gemm_persistent_big_tiles(E, bias, gelu, bn, tune):
     assert np.array_equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("bn", [256, 128])
-def test_gemm_big_tiles_unaligned_operands(E, bn, tune):
-    """256 x 256 and 256 x 128 tiles with a bias view 2 bytes off a 4-byte boundary and an output view 8 bytes off a
-    16-byte one: the launcher leaves the persistent kernel (dword bias loads, 16-byte staged stores) for the
+@pytest.mark.parametrize("bm,bn", [(256, 256), (256, 128), (128, 128)])
+def test_gemm_big_tiles_unaligned_operands(E, bm, bn, tune):
+    """Tiles of the persistent kernels with a bias view 2 bytes off a 4-byte boundary and an output view 8 bytes off
+    a 16-byte one: the launcher leaves the persistent kernel (dword bias loads, 16-byte staged stores) for the
     one-tile-per-workgroup kernel's predicated path; bf16 output still bit-exact against the oracle."""
-    tune("LFM2Q_GEMM_BM", "256")
+    tune("LFM2Q_GEMM_BM", str(bm))
     tune("LFM2Q_GEMM_BN", str(bn))
     M, K, N = 520, 128, 520
     xq, sx, wq, sw, b = _operands(11, M, K, N, True)
