@@ -652,10 +652,12 @@ def producer_results(reps):
 
 
 # every (tile, K split) configuration of the per-token W8A8 kernels (the cost model's candidates); 256 x 256 and
-# the first 256 x 128 and 128 x 128 are the persistent kernels, "…/1g" the one-tile-per-workgroup kernels
+# the first 256 x 128 and 128 x 128 are the persistent kernels, "…/1g" the one-tile-per-workgroup kernels, "…sN"
+# the persistent kernels with K cut into N slices over workgroups
 GEMM_CONFIGS = [(256, 256, 1), (128, 256, 1), (128, 256, 2), (256, 128, 1), (256, 128, 1, 0), (256, 128, 2),
                 (128, 128, 1), (128, 128, 1, 0), (128, 128, 2), (128, 64, 1), (128, 64, 2), (128, 64, 4), (64, 128, 1),
-                (64, 128, 2), (64, 128, 4), (64, 64, 1), (64, 64, 2), (64, 64, 4)]
+                (64, 128, 2), (64, 128, 4), (64, 64, 1), (64, 64, 2), (64, 64, 4), (256, 128, 1, 1, 2),
+                (256, 128, 1, 1, 4), (128, 128, 1, 1, 2), (128, 128, 1, 1, 4), (128, 128, 1, 1, 8)]
 
 
 def gemm_sweep(reps):
@@ -666,7 +668,7 @@ def gemm_sweep(reps):
     from lfm2opt.kernels import int8_ext
 
     E = int8_ext()
-    knobs = ("LFM2Q_GEMM_BM", "LFM2Q_GEMM_BN", "LFM2Q_GEMM_KSPLIT", "LFM2Q_GEMM_BIGP")
+    knobs = ("LFM2Q_GEMM_BM", "LFM2Q_GEMM_BN", "LFM2Q_GEMM_KSPLIT", "LFM2Q_GEMM_BIGP", "LFM2Q_GEMM_SPLITK")
     out = []
     for M, K, N, bias, gelu, name in W8A8_SHAPES:
         log(f"sweep {name} {M}x{K}x{N}")
@@ -693,7 +695,8 @@ def gemm_sweep(reps):
                         _capi.set_tuning(k, v)
                 graph = capture(fn)
                 t = min(time_graph(graph, reps, 2)[0] for _ in range(2))
-                label = "auto" if cfg is None else "%dx%d/%d" % cfg[:3] + ("g" if len(cfg) > 3 else "")
+                label = "auto" if cfg is None else "%dx%d/%d" % cfg[:3] + (
+                    "g" if len(cfg) == 4 else "s%d" % cfg[4] if len(cfg) > 4 else "")
                 us[label] = round(t * 1e3 / ncopy, 2)
                 del graph
         finally:

@@ -47,7 +47,7 @@ const char *lfm2q_version(void);
  * name (read once, at the first launch) and is read with one atomic load per launch. Results may differ in the last
  * bits between configurations where a kernel's summation order depends on them (the GEMV launch shapes); the W8A8
  * int32 paths are exact whatever the configuration. Knob names: LFM2Q_GEMV_{WPC, PERSIST, R, VALU, MFMA, CHUNK},
- * LFM2Q_W4_{WPC, ONESHOT, MFMA, B1_MFMA}, LFM2Q_GEMM_{BM, BN, KSPLIT, SWZ, BIGP, RING, STAGES}.
+ * LFM2Q_W4_{WPC, ONESHOT, MFMA, B1_MFMA}, LFM2Q_GEMM_{BM, BN, KSPLIT, SWZ, BIGP, RING, STAGES, SPLITK}.
  * Replaces the reference's implementation switches: set_gemv_impl() (kernels/lfm2_decode.cu:662-663, bound at
  * kernels/lfm2_decode.cpp:166) and the LFM2_INT8_BM tile override (kernels/int8_gemm.cu:691). */
 int lfm2q_set_tuning(const char *name, const char *value);
@@ -188,6 +188,19 @@ int lfm2q_silu_mul_q(const lfm2q_bf16 *g, int8_t *q, float *s, lfm2q_bf16 *x, in
  * kernels/int8_gemm.cpp:39-50, which also requires N % 8 == 0). */
 int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
                   lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream);
+
+/* lfm2q_gemm_i8 with a workspace: where the output tiles are fewer than the CUs (few tokens, narrow N) the
+ * persistent 256 x 128 / 128 x 128 kernels may also cut K into 2..8 slices over workgroups; each slice's int32
+ * accumulators go to the workspace and the last workgroup of a tile adds them (exact) before the epilogue, so Y is
+ * bit-identical to lfm2q_gemm_i8's. ws: lfm2q_gemm_workspace_bytes() of device memory (or at least 64 KiB: a
+ * smaller one only limits the slices), 256-byte aligned, zero-filled before its first use; every call that returns
+ * 0 leaves its counters zero again. Calls sharing a workspace must not overlap (one stream, or ordered); ws NULL is
+ * lfm2q_gemm_i8. No counterpart in the reference (added for the K split). */
+int lfm2q_gemm_i8_ex(const int8_t *A, const float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
+                     lfm2q_bf16 *Y, int M, int N, int K, int gelu, void *ws, size_t ws_bytes, lfm2q_stream_t stream);
+
+/* Bytes of the lfm2q_gemm_i8_ex workspace (64 MiB + 64 KiB). */
+size_t lfm2q_gemm_workspace_bytes(void);
 
 /* W8A8 GEMM on bf16 activations, quantized per token inside the GEMM: a first pass writes sa fp32 [M], the
  * scales lfm2q_quant_rows would write for X, and the GEMM quantizes each stage of X bf16 [M, K] on its way into

@@ -806,10 +806,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 // bf16 output only, with N % 8 == 0, 16-byte aligned Y, 4-byte aligned bias (its dword loads) and M N 2 < 2^31
 // (the launcher checks): the epilogue then issues no vector memory loads, so nothing but the staged stores is
 // outstanding when the next tile's first stage is waited for.
-template <int OUT, int BM, int BN, int NSLOT>
+// SPL: K is also cut into SK slices, a work unit being (tile, slice) (unit = tile SK + slice); a slice's unit stores
+// its int32 accumulator registers to the workspace (register r of thread i at word (unit NREG + r) 512 + i, so every
+// store instruction writes 2 KiB contiguous) with device-coherent stores, waits for them, and adds one to the tile's
+// arrival counter (workspace word `tile`); the unit that sees SK - 1 earlier arrivals loads the other slices'
+// registers, adds them to its own (int32: exact in any order), sets the counter back to 0 and runs the epilogue.
+// Nothing waits on another workgroup. The counters must be 0 when a call starts (a zero-filled workspace; every
+// completed call leaves them 0).
+constexpr uint32_t SPLIT_CNT_WORDS = 16384;                  // tile counters at the workspace start
+constexpr size_t GEMM_WS_BYTES = 4 * SPLIT_CNT_WORDS + (64u << 20);  // + partial accumulators
+
+template <int OUT, int BM, int BN, int NSLOT, bool SPL = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_bigp_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
-    const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K) {
+    const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
+    uint32_t *__restrict__ ws = nullptr, int SK = 1) {
     static_assert(OUT == OUT_BF16 || OUT == OUT_BF16_GELU, "bf16 output only");
     static_assert((BM == 256 && (BN == 256 || BN == 128)) || (BM == 128 && BN == 128), "tile shape");
     constexpr int BKT = 128, WMt = BM / 4, WNt = BN / 2, TM = WMt / 32, TN = WNt / 32;
@@ -827,9 +838,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
-    const int tm_n = (M + BM - 1) / BM, tn_n = (N + BN - 1) / BN, T = tm_n * tn_n;
-    const int KT = (K + BKT - 1) / BKT;
-    int t = blockIdx.x;
+    const int tm_n = (M + BM - 1) / BM, tn_n = (N + BN - 1) / BN, T = tm_n * tn_n * (SPL ? SK : 1);
+    const int KTT = (K + BKT - 1) / BKT;                  // stages of the whole K
+    const int SPS = SPL ? (KTT + SK - 1) / SK : KTT;      // stages per slice
+    int t = blockIdx.x;                                   // work unit
     if (t >= T) return;  // the launch sizes the grid to at most T; uniform per workgroup
 
     uint32_t off[ILX];
@@ -840,13 +852,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         cb[j] = swzb<CPR>(row, lane % CPR) - row * BKT;
         off[j] = (uint32_t)row * K + cb[j];
     }
-    int m0 = 0, n0 = 0;
+    int m0 = 0, n0 = 0, kb = 0, KT = KTT;  // the unit's tile corner and its stages kb .. kb + KT - 1
     v4i rx, rw;
     auto at_tile = [&](int tt) {
         int tm, tn;
-        tile_of(tt, tm_n, tn_n, tm, tn);
+        tile_of(SPL ? tt / SK : tt, tm_n, tn_n, tm, tn);
         m0 = tm * BM;
         n0 = tn * BN;
+        if (SPL) {
+            kb = (tt % SK) * SPS;
+            KT = max(0, min(KTT - kb, SPS));
+        }
         rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
         rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
     };
@@ -854,7 +870,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     const uint32_t lbase = lds_addr(smem), wbase = __builtin_amdgcn_readfirstlane(wave);
     auto issue = [&](int kt, int slot) {
         const uint32_t sX = lbase + slot * SLOT, sW = sX + BM * BKT;
-        const int k0 = kt * BKT;
+        const int k0 = (kb + kt) * BKT;
 #pragma unroll
         for (int j = 0; j < ILX; ++j) {
             const bool in = k0 + cb[j] < K;
@@ -945,7 +961,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         // the next tile's first NSLOT - 1 stages (slots g .. g + NSLOT - 2, every slot but the last stage's: free
         // since the barrier of this tile's last stage) and epilogue operands go out before this tile's epilogue
         const int tnext = t + (int)gridDim.x;
-        const int pm0 = m0, pn0 = n0;
+        const int pm0 = m0, pn0 = n0, pt = t;
         if (tnext < T) {
             at_tile(tnext);
 #pragma unroll
@@ -955,7 +971,44 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
         asm volatile("s_barrier" ::: "memory");  // every wavefront is done with the last stage's slot
         const int mb = pm0 + wm * WMt, nb = pn0 + wn * WNt;
-        {
+        bool epi = true;
+        if constexpr (SPL) {
+            constexpr int NREG = TN * TM * 16;
+            constexpr int SC1 = 16;  // buffer cache policy: device-scope coherent
+            const int ptile = pt / SK, pslice = pt % SK;
+            const rsrc_t pr = make_rsrc(ws + SPLIT_CNT_WORDS, 0x7ffffff0u);
+            auto word = [&](int unit, int r) { return (uint32_t)(((unit * NREG + r) * 512 + tid) * 4); };
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)acc[i][j][e], pr, (int)word(pt, (i * TM + j) * 16 + e), 0, SC1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
+            __shared__ uint32_t arrived;
+            __syncthreads();
+            if (tid == 0) arrived = __hip_atomic_fetch_add(ws + ptile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            epi = arrived == (uint32_t)(SK - 1);  // uniform over the workgroup
+            if (epi) {
+                for (int s2 = 0; s2 < SK; ++s2) {
+                    if (s2 == pslice) continue;
+                    int v[NREG];
+#pragma unroll
+                    for (int r = 0; r < NREG; ++r)
+                        v[r] = (int)__builtin_amdgcn_raw_buffer_load_b32(pr, (int)word(ptile * SK + s2, r), 0, SC1);
+#pragma unroll
+                    for (int i = 0; i < TN; ++i)
+#pragma unroll
+                        for (int j = 0; j < TM; ++j)
+#pragma unroll
+                            for (int e = 0; e < 16; ++e) acc[i][j][e] += v[(i * TM + j) * 16 + e];
+                }
+                if (tid == 0) __hip_atomic_store(ws + ptile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (epi) {
             const uint8_t *eb = smem + NSLOT * SLOT + (it & 1) * EOP;
             const float *sxs = reinterpret_cast<const float *>(eb);
             const float *sws = reinterpret_cast<const float *>(eb + 4 * BM);
@@ -1014,6 +1067,7 @@ struct TileCfg {
     double a, b;
     int ksp = 1;   // wavefront groups splitting K inside the workgroup (per-token path)
     int pers = 0;  // the persistent BM x BN kernel (per-token bf16 output, where its conditions hold)
+    int sk = 1;    // K slices over workgroups (persistent 256 x 128 / 128 x 128 with a workspace)
 };
 
 // Tile sets: per-token (all seven), grouped (the four tiles whose fp32 accumulators fit beside the int32 ones), and
@@ -1056,9 +1110,20 @@ inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
 // 13 LFM2 prefill / SigLIP2 shapes (`resident` = workgroups one CU holds at that split). The LFM2Q_GEMM_BM / _BN
 // knobs force a tile, LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced); 256 x 128 or 128 x 128 forced
 // means the persistent kernel unless LFM2Q_GEMM_BIGP is 0.
-inline TileCfg pick_tile_pt(int M, int N, int K) {
+// With a workspace the persistent 256 x 128 and 128 x 128 kernels are also candidates with K cut into SK = 2..8
+// slices over workgroups (at most two units per CU, partials within the workspace), costed as their tiles on
+// SK x the tiles with K / SK each plus SPLIT_US for the partial round trip; LFM2Q_GEMM_SPLITK forces SK.
+constexpr double SPLIT_US = 4.0;
+
+inline int split_fits(const TileCfg &o, long tiles, int sk, int K, size_t ws_bytes) {
+    const long cus = device_cus();
+    return o.pers && o.bm * o.bn <= 256 * 128 && tiles * sk <= 2 * cus && sk <= (K + 127) / 128 &&
+           tiles <= (long)SPLIT_CNT_WORDS && 4 * (size_t)SPLIT_CNT_WORDS + (size_t)tiles * sk * o.bm * o.bn * 4 <= ws_bytes;
+}
+
+inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0) {
     const int force_bm = knob_int(KNOB_GEMM_BM, 0), force_bn = knob_int(KNOB_GEMM_BN, 0);
-    const int force_ks = knob_int(KNOB_GEMM_KSPLIT, 0);
+    const int force_ks = knob_int(KNOB_GEMM_KSPLIT, 0), force_sk = knob_int(KNOB_GEMM_SPLITK, 0);
     const bool pers_ok = knob_int(KNOB_GEMM_BIGP, 1) != 0;
     static const TileCfg opts[] = {
         {256, 256, 1, 0.1582, 10.87, 1, 1}, {256, 128, 1, 0.2030, 5.781, 1, 1}, {128, 128, 1, 0.2880, 2.877, 1, 1},
@@ -1072,7 +1137,12 @@ inline TileCfg pick_tile_pt(int M, int N, int K) {
     if (force_bm && force_bn) {
         const int ks = force_ks == 4 ? 4 : force_ks == 2 ? 2 : 1;
         for (const TileCfg &o : opts)
-            if (o.bm == force_bm && o.bn == force_bn && o.ksp == ks && usable(o)) return o;
+            if (o.bm == force_bm && o.bn == force_bn && o.ksp == ks && usable(o)) {
+                TileCfg r = o;
+                const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
+                if (force_sk > 1 && split_fits(o, tiles, force_sk, K, ws_bytes)) r.sk = force_sk;
+                return r;
+            }
         for (const TileCfg &o : opts)
             if (o.bm == force_bm && o.bn == force_bn && o.ksp == 1 && usable(o)) return o;
     }
@@ -1088,14 +1158,26 @@ inline TileCfg pick_tile_pt(int M, int N, int K) {
             best = t;
             bestc = o;
         }
+        if (ws_bytes && force_sk != 1)
+            for (int sk = 2; sk <= 8; ++sk) {
+                if ((force_sk && sk != force_sk) || !split_fits(o, tiles, sk, K, ws_bytes)) continue;
+                const long sper = (tiles * sk + cus - 1) / cus;
+                const double ts = o.a * (double)sper * o.bm * o.bn * (double)((K + sk - 1) / sk) * 1e-6 +
+                                  o.b * (double)sper + SPLIT_US;
+                if (ts < best) {
+                    best = ts;
+                    bestc = o;
+                    bestc.sk = sk;
+                }
+            }
     }
     return bestc;
 }
 
 template <int OUT>
 void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float *sw, const uint16_t *bias, void *Y,
-                 int M, int N, int K, hipStream_t st) {
-    const TileCfg t = pick_tile_pt(M, N, K);
+                 int M, int N, int K, hipStream_t st, void *ws = nullptr, size_t ws_bytes = 0) {
+    const TileCfg t = pick_tile_pt(M, N, K, (OUT == OUT_BF16 || OUT == OUT_BF16_GELU) && ws ? ws_bytes : 0);
     const int sh = knob_int(KNOB_GEMM_SWZ, 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
     if (t.pers) {
@@ -1106,6 +1188,17 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
                 const int pgrid = (int)std::min<long>((long)grid.x, device_cus());
                 // LDS ring: as many slots as LDS holds (2, 3, 4); LFM2Q_GEMM_STAGES = 2 forces two
                 const bool two = knob_int(KNOB_GEMM_STAGES, 0) == 2;
+                if (t.sk > 1) {
+                    const int sgrid = (int)std::min<long>((long)grid.x * t.sk, device_cus());
+                    uint32_t *w = static_cast<uint32_t *>(ws);
+                    if (t.bm == 256)
+                        gemm_i8_bigp_kernel<OUT, 256, 128, 3, true><<<sgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K,
+                                                                                           w, t.sk);
+                    else
+                        gemm_i8_bigp_kernel<OUT, 128, 128, 4, true><<<sgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K,
+                                                                                           w, t.sk);
+                    return;
+                }
                 if (t.bm == 256 && t.bn == 256)
                     gemm_i8_bigp_kernel<OUT, 256, 256, 2><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 else if (t.bm == 256 && two)
@@ -1261,6 +1354,22 @@ extern "C" int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, 
         launch_gemm<OUT_BF16_GELU>(A, B, sa, sb, bias, Y, M, N, K, (hipStream_t)stream);
     else
         launch_gemm<OUT_BF16>(A, B, sa, sb, bias, Y, M, N, K, (hipStream_t)stream);
+    return launch_status("gemm_i8");
+}
+
+extern "C" size_t lfm2q_gemm_workspace_bytes(void) { return GEMM_WS_BYTES; }
+
+extern "C" int lfm2q_gemm_i8_ex(const int8_t *A, const float *sa, const int8_t *B, const float *sb,
+                                const lfm2q_bf16 *bias, lfm2q_bf16 *Y, int M, int N, int K, int gelu, void *ws,
+                                size_t ws_bytes, lfm2q_stream_t stream) {
+    if (int st = check_gemm("gemm_i8", A, B, Y, M, N, K)) return st;
+    LFM2Q_REQUIRE(sa && sb, LFM2Q_ERR_ARG, "gemm_i8: sx and sw are required");
+    LFM2Q_REQUIRE(!ws || (((uintptr_t)ws & 255) == 0 && ws_bytes >= 4 * (size_t)SPLIT_CNT_WORDS), LFM2Q_ERR_ARG,
+                  "gemm_i8_ex: workspace must be 256-byte aligned and at least %zu bytes", 4 * (size_t)SPLIT_CNT_WORDS);
+    if (gelu)
+        launch_gemm<OUT_BF16_GELU>(A, B, sa, sb, bias, Y, M, N, K, (hipStream_t)stream, ws, ws_bytes);
+    else
+        launch_gemm<OUT_BF16>(A, B, sa, sb, bias, Y, M, N, K, (hipStream_t)stream, ws, ws_bytes);
     return launch_status("gemm_i8");
 }
 

@@ -24,7 +24,7 @@ class GemvOp(ctypes.Structure):
 
 
 # entry points that return something other than an int status
-RESTYPES = {"lfm2q_gemv_chain_workspace_bytes": ctypes.c_size_t}
+RESTYPES = {"lfm2q_gemv_chain_workspace_bytes": ctypes.c_size_t, "lfm2q_gemm_workspace_bytes": ctypes.c_size_t}
 
 # name -> argument types (every entry point returns an int status unless listed in RESTYPES)
 SIGNATURES = {
@@ -40,6 +40,8 @@ SIGNATURES = {
     "lfm2q_add_layernorm_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _P],
     "lfm2q_silu_mul_q": [_P, _P, _P, _P, _I, _I, _I, _P],
     "lfm2q_gemm_i8": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "lfm2q_gemm_i8_ex": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "lfm2q_gemm_workspace_bytes": [],
     "lfm2q_gemm_i8_grouped": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_bf16a": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
@@ -99,3 +101,20 @@ def stream(t):
 
 def ptr(t):
     return None if t is None else t.data_ptr()
+
+
+_workspaces = {}
+
+
+def workspace(t):
+    """The GEMM workspace of torch's current stream on t's device: lfm2q_gemm_workspace_bytes() of device memory,
+    zero-filled (by a fill kernel on that stream) when first used and kept for the process. Calls on one stream are
+    ordered, so they share it; another stream gets its own. A graph captured on a stream uses that stream's
+    workspace, so graphs captured on one stream must not be replayed concurrently with each other."""
+    s = torch.cuda.current_stream(t.device)
+    key = (t.device.index, s.cuda_stream)
+    w = _workspaces.get(key)
+    if w is None:
+        w = torch.zeros(lib().lfm2q_gemm_workspace_bytes(), dtype=torch.uint8, device=t.device)
+        _workspaces[key] = w
+    return w

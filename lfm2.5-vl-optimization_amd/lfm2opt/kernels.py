@@ -268,9 +268,14 @@ class Int8Ops:
             raise RuntimeError("sx shape")
         N = self._check_common(w, sw, bias, y, M, K)
         _same_device(xq, sx, w, sw, bias, y)
-        _capi.call("lfm2q_gemm_i8_grouped" if grouped else "lfm2q_gemm_i8", xq.data_ptr(), sx.data_ptr(),
-                   w.data_ptr(), sw.data_ptr(), _capi.ptr(bias), y.data_ptr(), M, N, K, int(bool(gelu)),
-                   _capi.stream(xq))
+        if grouped:
+            _capi.call("lfm2q_gemm_i8_grouped", xq.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(),
+                       _capi.ptr(bias), y.data_ptr(), M, N, K, int(bool(gelu)), _capi.stream(xq))
+        else:  # per-token: with the stream's workspace (the K split for shapes with fewer tiles than CUs)
+            ws = _capi.workspace(xq)
+            _capi.call("lfm2q_gemm_i8_ex", xq.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(),
+                       _capi.ptr(bias), y.data_ptr(), M, N, K, int(bool(gelu)), ws.data_ptr(), ws.numel(),
+                       _capi.stream(xq))
 
     def gemm_i8_bf16a(self, x, sx, w, sw, bias, y, gelu):
         """The per-token pair quant_rows(x) + gemm_i8 as one call on bf16 activations x [M, K]: sx [M] receives the

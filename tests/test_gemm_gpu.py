@@ -300,6 +300,57 @@ def test_gemm_big_tiles_unaligned_operands(E, bm, bn, tune):
         assert int(ulp_dist(host_bits(y), ref).max()) == 0
 
 
+def _gemm_plain(xq, sx, wq, sw, b, y, gelu):
+    """lfm2q_gemm_i8 (no workspace: never a K split across workgroups)."""
+    from lfm2opt import _capi
+
+    M, K = xq.shape
+    _capi.call("lfm2q_gemm_i8", xq.data_ptr(), sx.data_ptr(), wq.data_ptr(), sw.data_ptr(), _capi.ptr(b), y.data_ptr(),
+               M, wq.shape[0], K, int(gelu), _capi.stream(xq))
+
+
+@pytest.mark.parametrize("bm,bn", [(128, 128), (256, 128)])
+@pytest.mark.parametrize("sk", [2, 3, 4, 8])
+def test_gemm_split_k_across_workgroups(E, bm, bn, sk, tune):
+    """The persistent kernels with K cut into SK slices over workgroups (forced through LFM2Q_GEMM_SPLITK), the
+    partial int32 tiles summed through the stream's workspace by the last workgroup of each tile: bit-identical to
+    the same tile without a workspace, and to the oracle's epilogue of the exact product, on M / N / K tails (K of
+    35 stages: slices of unequal length), with and without bias / GELU; three calls in a row on one workspace (the
+    arrival counters must be back at 0 after each)."""
+    tune("LFM2Q_GEMM_BM", str(bm))
+    tune("LFM2Q_GEMM_BN", str(bn))
+    for i, (M, K, N, bias, gelu) in enumerate([(300, 4432, 520, True, False), (131, 1104, 264, False, True),
+                                               (300, 4432, 520, True, False)]):
+        xq, sx, wq, sw, b = _operands(bm + bn + sk + i, M, K, N, bias)
+        ref = oracle.gemm_i8_epilogue(oracle.gemm_i8_i32(xq, wq), sx, sw, b, gelu)
+        args = [dev(xq), dev(sx), dev(wq), dev(sw), None if b is None else dev_bf16(b)]
+        y0 = torch.full((M, N), 7.0, device="cuda", dtype=torch.bfloat16)
+        _gemm_plain(*args, y0, gelu)
+        tune("LFM2Q_GEMM_SPLITK", str(sk))
+        y1 = torch.full((M, N), 9.0, device="cuda", dtype=torch.bfloat16)
+        E.gemm_i8(*args, y1, gelu)
+        tune("LFM2Q_GEMM_SPLITK", None)
+        assert torch.equal(y0, y1), f"split {sk} differs from the unsplit kernel (call {i})"
+        assert int(ulp_dist(host_bits(y1), ref).max()) <= (1 if gelu else 0)
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 3072), (512, 8192, 2048), (300, 8192, 2048)])
+def test_gemm_split_k_automatic(E, M, K, N):
+    """Shapes whose tiles leave CUs idle, where the automatic choice cuts K over workgroups: the library's call with
+    the stream's workspace is bit-identical to the call without one, and the int32 product is exact."""
+    xq, sx, wq, sw, b = _operands(M + K + N, M, K, N, True)
+    args = [dev(xq), dev(sx), dev(wq), dev(sw), dev_bf16(b)]
+    y0 = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    y1 = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    _gemm_plain(*args, y0, False)
+    E.gemm_i8(*args, y1, False)
+    E.gemm_i8(*args, y1, False)  # again, after the first call reset the counters
+    assert torch.equal(y0, y1)
+    rows = np.arange(0, M, 37)
+    ref = oracle.gemm_i8_epilogue(oracle.gemm_i8_i32(xq[rows], wq), sx[rows], sw, b, False)
+    assert int(ulp_dist(host_bits(y1)[rows], ref).max()) == 0
+
+
 # ------------------------------------------------------------------------------------------------ errors
 def test_gemm_argument_errors(E):
     xq = torch.zeros(4, 64, device="cuda", dtype=torch.int8)
