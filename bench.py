@@ -762,6 +762,7 @@ def main():
     ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 GEMM shapes")
     ap.add_argument("--w4-batches", default="1,8", help="INT4 decode batch sizes ('' to skip)")
     ap.add_argument("--only-w8a8", action="store_true", help="W8A8 shapes only (no decode step, no CPU baseline)")
+    ap.add_argument("--only-w8a16", action="store_true", help="W8A16 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--eager-kind", default=None,
                     help="run one decode kind (e.g. 'w1|w3+swiglu'), 'gemm:M,K,N', 'gemmg:M,K,N' (grouped scales) or 'copy' "
                          "eagerly, for counter collection")
@@ -786,6 +787,9 @@ def main():
         return
     if args.only_w8a8:
         print(json.dumps({"w8a8_shapes": w8a8_results(max(5, args.steps // 10))}))
+        return
+    if args.only_w8a16:
+        print(json.dumps({"w8a16_shapes": w8a16_results(max(5, args.steps // 10))}))
         return
     batches = [int(b) for b in args.batches.split(",")]
     res1 = decode_results(batches[0], args.steps, args.warmup)

@@ -199,7 +199,7 @@ int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, const float
 int lfm2q_gemm_i8_ex(const int8_t *A, const float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
                      lfm2q_bf16 *Y, int M, int N, int K, int gelu, void *ws, size_t ws_bytes, lfm2q_stream_t stream);
 
-/* Bytes of the lfm2q_gemm_i8_ex workspace (64 MiB + 64 KiB). */
+/* Bytes of the lfm2q_gemm_i8_ex / lfm2q_gemm_w8_ex workspace (64 MiB + 64 KiB). */
 size_t lfm2q_gemm_workspace_bytes(void);
 
 /* W8A8 GEMM on bf16 activations, quantized per token inside the GEMM: a first pass writes sa fp32 [M], the
@@ -232,6 +232,15 @@ int lfm2q_gemm_i8_q(const int8_t *A, const float *saT, const int8_t *B, const fl
  * kernels/int8_gemm.cu:762-771 (binding gemm_w8(), kernels/int8_gemm.cpp:72-79). */
 int lfm2q_gemm_w8(const lfm2q_bf16 *X, const int8_t *W, const float *sw, const lfm2q_bf16 *bias, lfm2q_bf16 *Y, int M,
                   int N, int K, int gelu, lfm2q_stream_t stream);
+
+/* lfm2q_gemm_w8 with a workspace (the lfm2q_gemm_i8_ex one: lfm2q_gemm_workspace_bytes(), zero-filled before its
+ * first use, left with its counters zero by every call that returns 0, not shared by overlapping calls): where the
+ * tiles leave more than half the CUs idle, K is also cut into up to 8 slices over workgroups and the last workgroup
+ * of each tile sums the slices' fp32 tiles in slice order (so the result does not depend on which came last; its
+ * last bits differ from lfm2q_gemm_w8's, within the same tolerance). ws NULL is lfm2q_gemm_w8. No counterpart in the
+ * reference (added for the K split). */
+int lfm2q_gemm_w8_ex(const lfm2q_bf16 *X, const int8_t *W, const float *sw, const lfm2q_bf16 *bias, lfm2q_bf16 *Y,
+                     int M, int N, int K, int gelu, void *ws, size_t ws_bytes, lfm2q_stream_t stream);
 
 /* The exact int32 accumulators of the W8A8 GEMM: C[m, n] = sum_k A[m, k] B[n, k], C int32 [M, N]. No counterpart
  * entry point in the reference (whose tests use torch._int_mm for this, tests/test_int8_gemm.py:236). */

@@ -68,6 +68,10 @@ __device__ __forceinline__ void tile_of(int w, int tm_n, int tn_n, int &tm, int 
 }
 
 constexpr int STAGES = 3;  // LDS ring depth: stage s computes while s + 1 and s + 2 are loading
+// The workspace of the K split across workgroups (lfm2q_gemm_i8_ex / lfm2q_gemm_w8_ex): one arrival counter per
+// output tile, then the partial accumulator tiles.
+constexpr uint32_t SPLIT_CNT_WORDS = 16384;
+constexpr size_t GEMM_WS_BYTES = 4 * SPLIT_CNT_WORDS + (64u << 20);
 
 // s_waitcnt immediate for vmcnt(n) with the other counters at their maximum (gfx9: vmcnt bits 3:0 and 15:14)
 constexpr int vmcnt_imm(int n) { return 0x3f70 | (n & 15) | ((n >> 4) << 14); }
@@ -557,10 +561,16 @@ __device__ __forceinline__ v8bf w8x8_to_bf16(uint32_t d0, uint32_t d1) {
     return __builtin_bit_cast(v8bf, r);
 }
 
-template <int BM, int BN, int OUT, int KSP = 1>
+// SPL: K is also cut into SK slices over workgroups (workgroup SK t + s takes slice s of tile t); after its own
+// groups are summed, a slice's workgroup stores its fp32 accumulator registers to the workspace (register r of
+// thread i at word (unit NREG + r) 256 + i), waits for them and adds one to the tile's arrival counter; the one that
+// sees SK - 1 earlier arrivals sums the SK slices' registers in slice order (its own reloaded, so the order does
+// not depend on which workgroup came last), resets the counter and runs the epilogue. Nothing waits.
+template <int BM, int BN, int OUT, int KSP = 1, bool SPL = false>
 __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(2))) void gemm_w8_kernel(
     const uint16_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sw,
-    const uint16_t *__restrict__ bias, uint16_t *__restrict__ Y, int M, int N, int K) {
+    const uint16_t *__restrict__ bias, uint16_t *__restrict__ Y, int M, int N, int K, uint32_t *__restrict__ ws = nullptr,
+    int SK = 1) {
     constexpr int BKE = 64;                       // k per stage
     constexpr int WMt = BM / 2, WNt = BN / 2, TM = WMt / 32, TN = WNt / 32;
     constexpr int IX = BM / 32, IW = BN / 64;     // direct loads per wavefront per stage: X 8 rows, W 16 rows each
@@ -580,10 +590,14 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(2))) v
     uint8_t(*sX)[XS] = reinterpret_cast<uint8_t(*)[XS]>(smem + grp * RING);
     uint8_t(*sW)[WS] = reinterpret_cast<uint8_t(*)[WS]>(smem + grp * RING + STAGES * XS);
     int tm, tn;
-    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+    const int unit = blockIdx.x, tile = SPL ? unit / SK : unit;
+    tile_of(tile, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int KTall = (K + BKE - 1) / BKE, KTg = (KTall + KSP - 1) / KSP;
-    const int kt0 = grp * KTg, KT = max(0, min(KTall, kt0 + KTg) - kt0);  // this group's stages kt0 .. kt0 + KT - 1
+    // the workgroup's stages s0 .. s0 + SKT - 1 (all of K without SPL), split over its KSP groups
+    const int KTall = (K + BKE - 1) / BKE, SPS = SPL ? (KTall + SK - 1) / SK : KTall;
+    const int s0 = SPL ? (unit % SK) * SPS : 0, SKT = max(0, min(KTall, s0 + SPS) - s0);
+    const int KTg = (SKT + KSP - 1) / KSP;
+    const int kt0 = s0 + grp * KTg, KT = max(0, min(s0 + SKT, kt0 + KTg) - kt0);  // this group's stages kt0 .. + KT - 1
     const v4i rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K * 2, 0x7fffffffL));
     const v4i rw = make_desc(W + (size_t)n0 * K, (uint32_t)std::min<long>((long)(N - n0) * K, 0x7fffffffL));
     // X: instruction j of wavefront w fills rows 8 (4 j + w) .. + 7; lane i -> row + i / 8, slot i % 8
@@ -682,6 +696,38 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(2))) v
                         }
         __syncthreads();  // the partials are read before group 0's epilogue slices overwrite them
         if (grp > 0) return;
+    }
+    if constexpr (SPL) {
+        constexpr int NREG = TN * TM * 16;
+        constexpr int SC1 = 16;  // buffer cache policy: device-scope coherent
+        const rsrc_t pr = make_rsrc(ws + SPLIT_CNT_WORDS, 0x7ffffff0u);
+        auto word = [&](int u, int r) { return (uint32_t)(((u * NREG + r) * 256 + (tid & 255)) * 4); };
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), pr, (int)word(unit, (i * TM + j) * 16 + e), 0, SC1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
+        __shared__ uint32_t arrived;
+        __syncthreads();
+        if (tid == 0) arrived = __hip_atomic_fetch_add(ws + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (arrived != (uint32_t)(SK - 1)) return;  // uniform over the workgroup
+        for (int s2 = 0; s2 < SK; ++s2) {
+            float v[NREG];
+#pragma unroll
+            for (int r = 0; r < NREG; ++r)
+                v[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, (int)word(tile * SK + s2, r), 0, SC1));
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[i][j][e] = s2 == 0 ? v[(i * TM + j) * 16 + e] : acc[i][j][e] + v[(i * TM + j) * 16 + e];
+        }
+        if (tid == 0) __hip_atomic_store(ws + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     epilogue<TM, TN, OUT>(acc, nullptr, sw, bias, Y, nullptr, M, N, m0 + wm * WMt, n0 + wn * WNt, lane,
                           smem + wave * stage_bytes<TN>());
@@ -813,8 +859,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 // registers, adds them to its own (int32: exact in any order), sets the counter back to 0 and runs the epilogue.
 // Nothing waits on another workgroup. The counters must be 0 when a call starts (a zero-filled workspace; every
 // completed call leaves them 0).
-constexpr uint32_t SPLIT_CNT_WORDS = 16384;                  // tile counters at the workspace start
-constexpr size_t GEMM_WS_BYTES = 4 * SPLIT_CNT_WORDS + (64u << 20);  // + partial accumulators
 
 template <int OUT, int BM, int BN, int NSLOT, bool SPL = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_bigp_kernel(
@@ -1301,16 +1345,48 @@ void launch_gemm_bf16a(const uint16_t *X, const int8_t *B, const float *sx, cons
 
 template <int OUT>
 void launch_gemm_w8(const uint16_t *X, const int8_t *W, const float *sw, const uint16_t *bias, uint16_t *Y, int M,
-                    int N, int K, hipStream_t st) {
+                    int N, int K, hipStream_t st, void *ws = nullptr, size_t ws_bytes = 0) {
     const TileCfg t = pick_tile(M, N, K, TILES_GROUPED);
-    const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
+    const long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+    const int KT = (K + 63) / 64;
+    // With a workspace, K slices over workgroups where the tiles leave more than half the CUs idle: SK = CUs / tiles,
+    // at most 8 and with at least 2048 k per slice (shorter slices lost to the unsplit kernel on MI355X: w1|w3 at 64
+    // tokens 14.4 -> 15.8 us split in two, against w2 at 64 tokens 33.7 -> 15.3 us in four); LFM2Q_GEMM_SPLITK
+    // forces SK (1 = none).
+    int sk = 1;
+    if (ws) {
+        const long cus = device_cus();
+        sk = (int)std::min<long>(8, std::min<long>(cus / tiles, K / 2048));
+        if (const int f = knob_int(KNOB_GEMM_SPLITK, 0)) sk = std::min(f, std::max(1, KT));
+        while (sk > 1 && 4 * (size_t)SPLIT_CNT_WORDS + (size_t)tiles * sk * t.bm * t.bn * 4 > ws_bytes) --sk;
+        if (tiles > (long)SPLIT_CNT_WORDS || sk < 2) sk = 1;
+    }
+    const dim3 grid(tiles * sk);
     // K split inside the workgroup where the tiles leave at most one workgroup per CU (a lone workgroup of 4
     // wavefronts is bound by its LDS -> convert -> MFMA chain): 4 groups for 64 x 64 tiles, 2 for the others (LDS).
     // The LFM2Q_GEMM_KSPLIT knob (1 / 2 / 4) forces it (4 only for 64 x 64).
-    const int KT = (K + 63) / 64;
     const bool s64 = t.bm == 64 && t.bn == 64;
-    int ksp = ((long)grid.x <= device_cus() && KT >= 8) ? (s64 ? 4 : 2) : 1;
+    int ksp = ((long)grid.x <= device_cus() && KT / sk >= 8) ? (s64 ? 4 : 2) : 1;
     if (const int f = knob_int(KNOB_GEMM_KSPLIT, 0)) ksp = f == 4 && s64 ? 4 : f == 2 ? 2 : 1;
+    uint32_t *const w = static_cast<uint32_t *>(ws);
+    if (sk > 1) {
+#define LFM2Q_GEMM(BM_, BN_)                                                                                        \
+    if (t.bm == BM_ && t.bn == BN_) {                                                                                \
+        if (ksp == 4 && BM_ == 64 && BN_ == 64)                                                                      \
+            gemm_w8_kernel<BM_, BN_, OUT, (BM_ == 64 && BN_ == 64 ? 4 : 1), true><<<grid, 4 * GT, 0, st>>>(          \
+                X, W, sw, bias, Y, M, N, K, w, sk);                                                                  \
+        else if (ksp == 2)                                                                                           \
+            gemm_w8_kernel<BM_, BN_, OUT, 2, true><<<grid, 2 * GT, 0, st>>>(X, W, sw, bias, Y, M, N, K, w, sk);     \
+        else                                                                                                         \
+            gemm_w8_kernel<BM_, BN_, OUT, 1, true><<<grid, GT, 0, st>>>(X, W, sw, bias, Y, M, N, K, w, sk);         \
+        return;                                                                                                      \
+    }
+        LFM2Q_GEMM(128, 128)
+        LFM2Q_GEMM(128, 64)
+        LFM2Q_GEMM(64, 128)
+        LFM2Q_GEMM(64, 64)
+#undef LFM2Q_GEMM
+    }
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
         if (ksp == 4 && BM_ == 64 && BN_ == 64)                                                                      \
@@ -1435,6 +1511,24 @@ extern "C" int lfm2q_gemm_w8(const lfm2q_bf16 *X, const int8_t *W, const float *
         launch_gemm_w8<OUT_BF16_GELU>(X, W, sw, bias, Y, M, N, K, (hipStream_t)stream);
     else
         launch_gemm_w8<OUT_BF16>(X, W, sw, bias, Y, M, N, K, (hipStream_t)stream);
+    return launch_status("gemm_w8");
+}
+
+extern "C" int lfm2q_gemm_w8_ex(const lfm2q_bf16 *X, const int8_t *W, const float *sw, const lfm2q_bf16 *bias,
+                                lfm2q_bf16 *Y, int M, int N, int K, int gelu, void *ws, size_t ws_bytes,
+                                lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(X && W && sw && Y, LFM2Q_ERR_ARG, "gemm_w8: null pointer");
+    LFM2Q_REQUIRE(M >= 1 && N >= 1 && K >= 16 && K % 16 == 0, LFM2Q_ERR_SHAPE,
+                  "gemm_w8: need M, N >= 1 and K %% 16 == 0 (M=%d N=%d K=%d)", M, N, K);
+    LFM2Q_REQUIRE((long)M * K * 2 < (1L << 31) && (long)N * K < (1L << 31), LFM2Q_ERR_SHAPE,
+                  "gemm_w8: each operand must be smaller than 2 GiB (buffer offsets are 32-bit)");
+    LFM2Q_REQUIRE(aligned16(X) && aligned16(W), LFM2Q_ERR_ALIGN, "gemm_w8: x and w must be 16-byte aligned");
+    LFM2Q_REQUIRE(!ws || (((uintptr_t)ws & 255) == 0 && ws_bytes >= 4 * (size_t)SPLIT_CNT_WORDS), LFM2Q_ERR_ARG,
+                  "gemm_w8_ex: workspace must be 256-byte aligned and at least %zu bytes", 4 * (size_t)SPLIT_CNT_WORDS);
+    if (gelu)
+        launch_gemm_w8<OUT_BF16_GELU>(X, W, sw, bias, Y, M, N, K, (hipStream_t)stream, ws, ws_bytes);
+    else
+        launch_gemm_w8<OUT_BF16>(X, W, sw, bias, Y, M, N, K, (hipStream_t)stream, ws, ws_bytes);
     return launch_status("gemm_w8");
 }
 

@@ -324,8 +324,9 @@ class Int8Ops:
         M = x.numel() // K if K else 0
         N = self._check_common(w, sw, bias, y, M, K)
         _same_device(x, w, sw, bias, y)
-        _capi.call("lfm2q_gemm_w8", x.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias), y.data_ptr(), M, N, K,
-                   int(bool(gelu)), _capi.stream(x))
+        ws = _capi.workspace(x)  # the K split across workgroups for shapes with few tiles
+        _capi.call("lfm2q_gemm_w8_ex", x.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias), y.data_ptr(), M, N,
+                   K, int(bool(gelu)), ws.data_ptr(), ws.numel(), _capi.stream(x))
 
     def gemm_i8_i32(self, xq, w, c):
         """The exact int32 accumulators c [M, N] = xq [M, K] . w [N, K]^T (the torch._int_mm analogue)."""

@@ -106,3 +106,33 @@ def test_int8_linear_w8a16(cuda):
     ref = torch.empty(28, 192, device="cuda", dtype=torch.bfloat16)
     int8_ext().gemm_w8(x.reshape(28, 1152), lin.q, lin.s, b, ref, True)
     assert torch.equal(y.reshape(28, 192), ref)
+
+
+@pytest.mark.parametrize("tile", ["128x128", "64x64"])
+@pytest.mark.parametrize("sk", [2, 3, 8])
+def test_gemm_w8_split_k_across_workgroups(E, tile, sk, tune):
+    """K cut into SK slices over workgroups (LFM2Q_GEMM_SPLITK), the fp32 partial tiles summed in slice order through
+    the stream's workspace by the last workgroup of each tile: against the oracle as every W8A16 call, on ragged
+    shapes with K of 69 stages (unequal slices) and 9 stages (some slices empty at SK = 8); two calls in a row give
+    the same bits (the sum order does not depend on which workgroup finishes last, and the counters are back at 0)."""
+    bm, bn = tile.split("x")
+    tune("LFM2Q_GEMM_BM", bm)
+    tune("LFM2Q_GEMM_BN", bn)
+    tune("LFM2Q_GEMM_SPLITK", str(sk))
+    for M, K, N, bias, gelu in [(70, 4416, 136, True, False), (33, 576, 264, False, True)]:
+        x, W, sw, b = operands(M + K + N + sk, M, K, N, bias)
+        y1 = run(E, x, W, sw, b, gelu)
+        y2 = run(E, x, W, sw, b, gelu)
+        assert np.array_equal(y1, y2), "two split calls differ"
+        assert_close_bf16(y1, oracle.gemm_w8(x, W, sw, b, gelu), what=f"gemm_w8 split {sk} {tile} {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 8192, 2048), (64, 8192, 2048)])
+def test_gemm_w8_split_k_automatic(E, M, K, N):
+    """The decode-batch shapes whose tiles leave most CUs idle (w2: N = 2048, K = 8192), where the automatic choice
+    cuts K over workgroups: 64 sampled rows against the oracle; repeated calls bit-identical."""
+    x, W, sw, b = operands(M + K + N, M, K, N, False)
+    y1 = run(E, x, W, sw, b, False)
+    assert np.array_equal(y1, run(E, x, W, sw, b, False))
+    rows = np.sort(np.random.default_rng(3).permutation(M)[:64])
+    assert_close_bf16(y1[rows], oracle.gemm_w8(x[rows], W, sw, b, False), what=f"gemm_w8 auto split {M}x{K}x{N}")
