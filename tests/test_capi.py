@@ -76,6 +76,15 @@ def test_status_codes_without_launch(L):
     assert "K % 16 == 0" in L.lfm2q_last_error().decode()
     assert L.lfm2q_gemm_i8_bf16a(fake, fake, fake, fake, None, fake, 0, 8, 64, 0, None) == 2
     assert L.lfm2q_gemm_i8_bf16a(ctypes.c_void_p(0x1008), fake, fake, fake, None, fake, 4, 8, 64, 0, None) == 3
+    # the workspace forms: the plain entry point's checks, then a 256-byte aligned workspace of at least 64 KiB
+    assert L.lfm2q_gemm_i8_ex(fake, fake, fake, fake, None, fake, 4, 8, 72, 0, None, 0, None) == 2
+    assert L.lfm2q_gemm_i8_ex(fake, fake, fake, fake, None, fake, 4, 8, 64, 0, ctypes.c_void_p(0x1108), 1 << 20,
+                              None) == 1
+    assert "256-byte aligned" in L.lfm2q_last_error().decode()
+    assert L.lfm2q_gemm_i8_ex(fake, fake, fake, fake, None, fake, 4, 8, 64, 0, fake, 4096, None) == 1
+    assert L.lfm2q_gemm_w8_ex(fake, fake, fake, None, fake, 4, 8, 64, 0, ctypes.c_void_p(0x1108), 1 << 20, None) == 1
+    assert L.lfm2q_gemm_w8_ex(None, fake, fake, None, fake, 4, 8, 64, 0, None, 0, None) == 1
+    assert L.lfm2q_gemm_workspace_bytes() == 4 * 16384 + (64 << 20)
 
 
 def test_python_checks_match_reference_wording():
