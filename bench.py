@@ -652,12 +652,13 @@ def producer_results(reps):
 
 
 # every (tile, K split) configuration of the per-token W8A8 kernels (the cost model's candidates); 256 x 256 and
-# the first 256 x 128 and 128 x 128 are the persistent kernels, "…/1g" the one-tile-per-workgroup kernels, "…sN"
+# the first 256 x 128, 128 x 128 and 128 x 64 are the persistent kernels, "…/1g" the one-tile-per-workgroup kernels, "…sN"
 # the persistent kernels with K cut into N slices over workgroups
 GEMM_CONFIGS = [(256, 256, 1), (128, 256, 1), (128, 256, 2), (256, 128, 1), (256, 128, 1, 0), (256, 128, 2),
                 (128, 128, 1), (128, 128, 1, 0), (128, 128, 2), (128, 64, 1), (128, 64, 2), (128, 64, 4), (64, 128, 1),
                 (64, 128, 2), (64, 128, 4), (64, 64, 1), (64, 64, 2), (64, 64, 4), (256, 128, 1, 1, 2),
-                (256, 128, 1, 1, 4), (128, 128, 1, 1, 2), (128, 128, 1, 1, 4), (128, 128, 1, 1, 8)]
+                (256, 128, 1, 1, 4), (128, 128, 1, 1, 2), (128, 128, 1, 1, 4), (128, 128, 1, 1, 8), (128, 64, 1, 0),
+                (128, 64, 1, 1, 2)]
 
 
 def gemm_sweep(reps):

@@ -866,17 +866,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
     uint32_t *__restrict__ ws = nullptr, int SK = 1) {
     static_assert(OUT == OUT_BF16 || OUT == OUT_BF16_GELU, "bf16 output only");
-    static_assert((BM == 256 && (BN == 256 || BN == 128)) || (BM == 128 && BN == 128), "tile shape");
+    static_assert((BM == 256 && (BN == 256 || BN == 128)) || (BM == 128 && (BN == 128 || BN == 64)), "tile shape");
     constexpr int BKT = 128, WMt = BM / 4, WNt = BN / 2, TM = WMt / 32, TN = WNt / 32;
     constexpr int CPR = BKT / 16, RPI = 64 / CPR, ILX = BM / RPI / 8, ILW = BN / RPI / 8, KS = BKT / 32;
     constexpr int SLOT = (BM + BN) * BKT;          // one stage of both operands (64 / 48 KiB)
-    constexpr int EOP = 4 * BM + 4 * BN + 2 * BN;  // one tile's epilogue operands: sx, sw, bias (2.5 / 2 KiB)
+    constexpr int EOP = 4 * BM + 4 * BN + (BN >= 128 ? 2 * BN : 256);  // one tile's sx, sw, bias (bias: 128+)
     constexpr int G = WNt / 8;                     // 16-byte granules per staged output row (2 WNt bytes)
     constexpr int RPS = 64 / G;                    // staged rows per store instruction
     constexpr int SST = TM * 32 / RPS;             // staged stores per wavefront per tile
     constexpr int LPS = ILX + ILW;                 // operand loads per wavefront per stage
     static_assert(8 * 32 * 2 * WNt <= SLOT, "epilogue staging exceeds a ring slot");
-    static_assert(NSLOT >= 2 && NSLOT <= 4 && NSLOT * SLOT + 2 * EOP <= 160 * 1024, "LDS ring");
+    static_assert(NSLOT >= 2 && NSLOT <= 6 && NSLOT * SLOT + 2 * EOP <= 160 * 1024, "LDS ring");
     static_assert((NSLOT - 2) * LPS + SST < 64, "vmcnt holds 6 bits");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSLOT * SLOT + 2 * EOP];
 
@@ -923,7 +923,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
     };
     // the tile's token scales (waves 0 .. BM / 64 - 1, 64 each), weight scales (waves 4 .. 4 + BN / 64 - 1) and bias
-    // (waves 0 .. BN / 128 - 1, 128 each) into LDS: sx at 0, sw at 4 BM, bias at 4 BM + 4 BN
+    // (waves 0 .. max(1, BN / 128) - 1, 128 each: a 64-column tile reads its 64 and the next tile's) into LDS: sx at
+    // 0, sw at 4 BM, bias at 4 BM + 4 BN
     const v4i rsx = make_desc(sx, (uint32_t)M * 4), rsw = make_desc(sw, (uint32_t)N * 4);
     const v4i rb = make_desc(bias, bias ? (uint32_t)N * 2 : 0u);
     auto issue_eop = [&](int e) {
@@ -933,7 +934,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         asm volatile("" : "+v"(l));
         if (wbase < 4) {
             if (wbase < BM / 64) lds_dma4(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
-            if (wbase < BN / 128 && bias)
+            if (wbase < (BN >= 128 ? BN / 128 : 1) && bias)
                 lds_dma4(rb, (uint32_t)(n0 + 128 * wbase + 2 * l) * 2, eb + 4 * BM + 4 * BN + 256 * wbase);
         } else if (wbase < 4 + BN / 64) {
             lds_dma4(rsw, (uint32_t)(n0 + 64 * (wbase - 4) + l) * 4, eb + 4 * BM + 256 * (wbase - 4));
@@ -961,21 +962,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             // at a tile's first stage, the previous epilogue's staged stores, issued after those loads); the next
             // tile's epilogue-operand loads sit between its stages and the stores, so the counts only wait longer
             const int f = min(NSLOT - 2, KT - 1 - kt);
-            if (kt == 0 && it > 0) {
-                if (NSLOT >= 4 && f == 2)
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPS + SST));
-                else if (NSLOT >= 3 && f == 1)
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPS + SST));
-                else
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(SST));
-            } else {
-                if (NSLOT >= 4 && f == 2)
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPS));
-                else if (NSLOT >= 3 && f == 1)
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPS));
-                else
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            }
+            const bool st = kt == 0 && it > 0;
+#define LFM2Q_WAIT_STAGE(F_)                                                                                       \
+    do {                                                                                                            \
+        if (st)                                                                                                     \
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((F_) * LPS + SST));                                                \
+        else                                                                                                        \
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((F_) * LPS));                                                      \
+    } while (0)
+            if (NSLOT >= 6 && f == 4)
+                LFM2Q_WAIT_STAGE(4);
+            else if (NSLOT >= 5 && f == 3)
+                LFM2Q_WAIT_STAGE(3);
+            else if (NSLOT >= 4 && f == 2)
+                LFM2Q_WAIT_STAGE(2);
+            else if (NSLOT >= 3 && f == 1)
+                LFM2Q_WAIT_STAGE(1);
+            else
+                LFM2Q_WAIT_STAGE(0);
+#undef LFM2Q_WAIT_STAGE
             asm volatile("s_barrier" ::: "memory");  // every wavefront's loads of stage kt landed; slot g - 1 is free
             if (kt + NSLOT - 1 < KT) issue(kt + NSLOT - 1, (g + NSLOT - 1) % NSLOT);
             const uint8_t *x_s = smem + (g % NSLOT) * SLOT, *w_s = x_s + BM * BKT;
@@ -1150,11 +1155,11 @@ inline TileCfg pick_tile(int M, int N, int K, int set = TILES_ALL) {
 }
 
 // Per-token path: the seven tiles, each also with K split over 2 (and, for the small tiles, 4) wavefront groups,
-// and the persistent 256 x 128 and 128 x 128 kernels, fitted like the table above to MI355X timings of every (tile, split) on the
+// and the persistent 256 x 128, 128 x 128 and 128 x 64 kernels, fitted like the table above to MI355X timings of every (tile, split) on the
 // 13 LFM2 prefill / SigLIP2 shapes (`resident` = workgroups one CU holds at that split). The LFM2Q_GEMM_BM / _BN
-// knobs force a tile, LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced); 256 x 128 or 128 x 128 forced
-// means the persistent kernel unless LFM2Q_GEMM_BIGP is 0.
-// With a workspace the persistent 256 x 128 and 128 x 128 kernels are also candidates with K cut into SK = 2..8
+// knobs force a tile, LFM2Q_GEMM_KSPLIT its split (default 1 when a tile is forced); 256 x 128, 128 x 128 or 128 x 64
+// forced means the persistent kernel unless LFM2Q_GEMM_BIGP is 0.
+// With a workspace the persistent 256 x 128, 128 x 128 and 128 x 64 kernels are also candidates with K cut into SK = 2..8
 // slices over workgroups (at most two units per CU, partials within the workspace), costed as their tiles on
 // SK x the tiles with K / SK each plus SPLIT_US for the partial round trip; LFM2Q_GEMM_SPLITK forces SK.
 constexpr double SPLIT_US = 4.0;
@@ -1170,7 +1175,8 @@ inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0) {
     const int force_ks = knob_int(KNOB_GEMM_KSPLIT, 0), force_sk = knob_int(KNOB_GEMM_SPLITK, 0);
     const bool pers_ok = knob_int(KNOB_GEMM_BIGP, 1) != 0;
     static const TileCfg opts[] = {
-        {256, 256, 1, 0.1582, 10.87, 1, 1}, {256, 128, 1, 0.2030, 5.781, 1, 1}, {128, 128, 1, 0.2880, 2.877, 1, 1},
+        {256, 256, 1, 0.1582, 10.87, 1, 1}, {256, 128, 1, 0.2033, 5.808, 1, 1}, {128, 128, 1, 0.2894, 2.859, 1, 1},
+        {128, 64, 1, 0.4104, 1.750, 1, 1},
         {128, 256, 2, 0.2912, 7.604, 1}, {128, 256, 1, 0.2721, 10.14, 2},
         {256, 128, 2, 0.2911, 7.455, 1}, {256, 128, 1, 0.2572, 10.95, 2}, {128, 128, 3, 0.3494, 5.003, 1},
         {128, 128, 1, 0.3449, 5.533, 2}, {128, 64, 4, 0.4546, 3.930, 1},  {128, 64, 2, 0.4729, 2.456, 2},
@@ -1192,7 +1198,7 @@ inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0) {
     }
     const long cus = device_cus();
     double best = 1e300;
-    TileCfg bestc = opts[7];
+    TileCfg bestc = opts[8];
     for (const TileCfg &o : opts) {
         if ((force_ks && o.ksp != force_ks) || !usable(o)) continue;
         const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
@@ -1238,6 +1244,9 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
                     if (t.bm == 256)
                         gemm_i8_bigp_kernel<OUT, 256, 128, 3, true><<<sgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K,
                                                                                            w, t.sk);
+                    else if (t.bn == 64)
+                        gemm_i8_bigp_kernel<OUT, 128, 64, 6, true><<<sgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K,
+                                                                                          w, t.sk);
                     else
                         gemm_i8_bigp_kernel<OUT, 128, 128, 4, true><<<sgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K,
                                                                                            w, t.sk);
@@ -1249,6 +1258,8 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
                     gemm_i8_bigp_kernel<OUT, 256, 128, 2><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 else if (t.bm == 256)
                     gemm_i8_bigp_kernel<OUT, 256, 128, 3><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
+                else if (t.bn == 64)
+                    gemm_i8_bigp_kernel<OUT, 128, 64, 6><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 else if (two)
                     gemm_i8_bigp_kernel<OUT, 128, 128, 2><<<pgrid, 512, 0, st>>>(A, B, sx, sw, bias, Y, M, N, K);
                 else

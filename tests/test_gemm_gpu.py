@@ -257,12 +257,12 @@ def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, tune):
         assert int(ulp_dist(host_bits(y), oracle.gemm_i8_epilogue(acc, sx, sw, b)).max()) == 0, f"bf16 K={K}"
 
 
-@pytest.mark.parametrize("bm,bn", [(256, 256), (256, 128), (128, 128)])
+@pytest.mark.parametrize("bm,bn", [(256, 256), (256, 128), (128, 128), (128, 64)])
 @pytest.mark.parametrize("bias,gelu", [(False, False), (True, True)])
 def test_gemm_persistent_big_tiles(E, bias, gelu, bm, bn, tune):
-    """The persistent 256 x 256, 256 x 128 and 128 x 128 kernels with more tiles than workgroups (17 x 17, 17 x 33 or
-    33 x 33 tiles on one workgroup per CU, so workgroups take further tiles whose first stage and epilogue operands
-    load during the previous tile's epilogue), with M, N and K tails: bf16 output against the oracle's epilogue of
+    """The persistent 256 x 256, 256 x 128, 128 x 128 and 128 x 64 kernels with more tiles than workgroups (17 x 17,
+    17 x 33, 33 x 33 or 33 x 65 tiles on one workgroup per CU, so workgroups take further tiles whose first stage and
+    epilogue operands load during the previous tile's epilogue), with M, N and K tails: bf16 output against the oracle's epilogue of
     the exact int32 product (bit-exact, <= 1 ulp with GELU) and bit-identical to the one-tile-per-workgroup kernel
     of the same tile (LFM2Q_GEMM_BIGP=0)."""
     tune("LFM2Q_GEMM_BM", str(bm))
@@ -281,7 +281,7 @@ def test_gemm_persistent_big_tiles(E, bias, gelu, bm, bn, tune):
     assert np.array_equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("bm,bn", [(256, 256), (256, 128), (128, 128)])
+@pytest.mark.parametrize("bm,bn", [(256, 256), (256, 128), (128, 128), (128, 64)])
 def test_gemm_big_tiles_unaligned_operands(E, bm, bn, tune):
     """Tiles of the persistent kernels with a bias view 2 bytes off a 4-byte boundary and an output view 8 bytes off
     a 16-byte one: the launcher leaves the persistent kernel (dword bias loads, 16-byte staged stores) for the
@@ -309,7 +309,7 @@ def _gemm_plain(xq, sx, wq, sw, b, y, gelu):
                M, wq.shape[0], K, int(gelu), _capi.stream(xq))
 
 
-@pytest.mark.parametrize("bm,bn", [(128, 128), (256, 128)])
+@pytest.mark.parametrize("bm,bn", [(128, 128), (256, 128), (128, 64)])
 @pytest.mark.parametrize("sk", [2, 3, 4, 8])
 def test_gemm_split_k_across_workgroups(E, bm, bn, sk, tune):
     """The persistent kernels with K cut into SK slices over workgroups (forced through LFM2Q_GEMM_SPLITK), the
