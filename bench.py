@@ -837,12 +837,12 @@ def main():
         big = next(r for r in shapes if r["M"] == 4096 and r["N"] == 16384)
         out["w8a8"] = {"unit": "TOPS", "peak": INT8_PEAK_TOPS,
                        "roofline": {"bound": "mfma",
-                                    "kernel": "gemm_i8_bigp_kernel<0> (4096 x 2048 x 16384, persistent 256 x 256 tiles)",
+                                    "kernel": "gemm_i8_bigp_kernel<0, 256, 256, 2, false> (4096 x 2048 x 16384, persistent 256 x 256 tiles)",
                                     "achieved": big["tops_gemm"], "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                                     "frac": round(big["tops_gemm"] / INT8_PEAK_TOPS, 4)},
                        # the same layer as the workload specifies it: bf16 activations quantized per token
                        # (quant_rows) and then multiplied
-                       "roofline_with_quant": {"bound": "mfma", "kernels": "quant_kernel + gemm_i8_bigp_kernel<0>",
+                       "roofline_with_quant": {"bound": "mfma", "kernels": "quant_kernel + gemm_i8_bigp_kernel<0, 256, 256, 2, false>",
                                                "achieved": big["tops_quant_gemm"], "peak": INT8_PEAK_TOPS,
                                                "unit": "TOPS",
                                                "frac": round(big["tops_quant_gemm"] / INT8_PEAK_TOPS, 4)},
