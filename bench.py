@@ -764,6 +764,8 @@ def main():
     ap.add_argument("--w4-batches", default="1,8", help="INT4 decode batch sizes ('' to skip)")
     ap.add_argument("--only-w8a8", action="store_true", help="W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--only-w8a16", action="store_true", help="W8A16 shapes only (no decode step, no CPU baseline)")
+    ap.add_argument("--only-w8a8-grouped", action="store_true",
+                    help="grouped-64 W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--eager-kind", default=None,
                     help="run one decode kind (e.g. 'w1|w3+swiglu'), 'gemm:M,K,N', 'gemmg:M,K,N' (grouped scales) or 'copy' "
                          "eagerly, for counter collection")
@@ -791,6 +793,9 @@ def main():
         return
     if args.only_w8a16:
         print(json.dumps({"w8a16_shapes": w8a16_results(max(5, args.steps // 10))}))
+        return
+    if args.only_w8a8_grouped:
+        print(json.dumps({"w8a8_grouped": grouped_results(max(5, args.steps // 10))}))
         return
     batches = [int(b) for b in args.batches.split(",")]
     res1 = decode_results(batches[0], args.steps, args.warmup)

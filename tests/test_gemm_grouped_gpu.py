@@ -65,6 +65,30 @@ def test_gemm_grouped_every_tile(E, tile, tune):
     assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
 
 
+@pytest.mark.skip(reason="a persistent grouped-64 kernel (two groups per 128-byte stage, scale ring in LDS) faulted "
+                         "the GPU on this case, its first run with more tiles than workgroups (128 x 64 tiles, "
+                         "1100 x 320 x 2056); the cause was not found and the kernel was taken out, so the grouped "
+                         "path runs the one-tile-per-workgroup kernels and this case stays off the GPU")
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64"])
+@pytest.mark.parametrize("gelu", [False, True])
+def test_gemm_grouped_persistent_many_tiles(E, tile, gelu, tune):
+    """The persistent grouped kernels with more tiles than workgroups (one workgroup per CU takes several tiles, the
+    next tile's first stages and scale slots loading during the previous tile's epilogue), M / N tails and K of 5
+    groups: bit-exact against the oracle's fold (<= 1 ulp with GELU) and bit-identical to the one-tile-per-workgroup
+    grouped kernel of the same tile where there is one."""
+    bm, bn = tile.split("x")
+    tune("LFM2Q_GEMM_BM", bm)
+    tune("LFM2Q_GEMM_BN", bn)
+    M, K, N = 1100, 320, 2056
+    xq, sxT, wq, sw, b = operands(11 + int(gelu), M, K, N, True)
+    y = host_bits(run_grouped(E, xq, sxT, wq, sw, b, gelu))
+    ref = oracle.gemm_i8_grouped(xq, sxT, wq, sw, b, gelu)
+    assert int(ulp_dist(y, ref).max()) <= (1 if gelu else 0)
+    if bm == "128":
+        tune("LFM2Q_GEMM_BIGP", "0")
+        assert np.array_equal(y, host_bits(run_grouped(E, xq, sxT, wq, sw, b, gelu)))
+
+
 @pytest.mark.parametrize("M,K,N", [(2048, 2048, 16384), (4096, 8192, 2048)])
 def test_gemm_grouped_full_shape_error_rule(E, M, K, N):
     """Full LFM2 prefill shapes: against the exact fp64 per-group sum on the GPU, the reference's rule (relative
