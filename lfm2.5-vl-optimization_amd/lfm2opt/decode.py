@@ -44,8 +44,10 @@ from .quant import GROUP, quantize_int4, quantize_int8
 MODES = ("cublas", "bf16", "int8", "int4")
 GEMV_MAX_BATCH = 16      # quantized weights: the GEMV beat F.linear and W8A16 at every LFM2 shape up to this batch
 BF16_GEMV_MAX_BATCH = 8  # BF16 weights (16 when K < 8192)
-W8A16_MIN_ROWS = 8192    # INT8 weights with this many output rows go to W8A16 above batch 24
-HEAD_ROWS = 32768        # ... and above batch 16 with this many
+W8A16_MIN_ROWS = 8192    # INT8 weights with this many output rows (or K >= 8192) leave the GEMV above batch 16
+GEMV_MAX_BATCH_NARROW = 32  # ... the others above batch 32
+W8A16_MAX_BATCH = 256    # above this many rows a kept BF16 copy (F.linear) beats W8A16 ...
+HEAD_ROWS = 32768        # ... and above 128 rows for weights with this many output rows
 
 
 def linear_path(mode, fmt, B, N, K, has_bf16):
@@ -62,13 +64,13 @@ def linear_path(mode, fmt, B, N, K, has_bf16):
     if B <= GEMV_MAX_BATCH:
         return "gemv"
     if fmt == "int8":
-        if N >= HEAD_ROWS:
-            return "w8a16"
-        if N >= W8A16_MIN_ROWS:
-            return "gemv" if B <= 24 else "w8a16"
-        if K >= 8192:
-            return "linear" if has_bf16 else ("gemv" if B <= 48 else "w8a16")
-        return "gemv" if B <= 32 else ("linear" if has_bf16 else "w8a16")
+        if K >= 8192 and B <= 24 and has_bf16:
+            return "linear"
+        if N < W8A16_MIN_ROWS and K < 8192 and B <= GEMV_MAX_BATCH_NARROW:
+            return "gemv"
+        if has_bf16 and B > (W8A16_MAX_BATCH // 2 if N >= HEAD_ROWS else W8A16_MAX_BATCH):
+            return "linear"
+        return "w8a16"
     return "linear" if has_bf16 else "gemv"
 
 

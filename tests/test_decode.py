@@ -24,22 +24,25 @@ def test_quantized_gemv_up_to_16(fmt, shape, B):
 
 
 def test_int8_above_16():
-    # the lm_head: W8A16 whether or not a BF16 copy is kept
+    # the lm_head (32768+ rows): W8A16 up to 128 rows, then the kept BF16 copy
     for B in (17, 24, 64, 128):
         assert linear_path("int8", "int8", B, *HEAD, True) == "w8a16"
-        assert linear_path("int8", "int8", B, *HEAD, False) == "w8a16"
-    # w1|w3-sized: the GEMV up to 24 rows, then W8A16
-    for kept in (True, False):
-        assert [linear_path("int8", "int8", B, *W13, kept) for B in (17, 24, 25, 64)] == \
+    assert [linear_path("int8", "int8", B, *HEAD, True) for B in (129, 512)] == ["linear", "linear"]
+    assert [linear_path("int8", "int8", B, *HEAD, False) for B in (17, 129, 4096)] == ["w8a16"] * 3
+    # w1|w3-sized weights (8192+ rows): W8A16 from batch 17 up to 256 rows
+    assert [linear_path("int8", "int8", B, *W13, True) for B in (17, 24, 25, 256, 257)] == \
+        ["w8a16", "w8a16", "w8a16", "w8a16", "linear"]
+    assert [linear_path("int8", "int8", B, *W13, False) for B in (17, 257, 1024)] == ["w8a16"] * 3
+    # narrow, K = 2048: the GEMV up to 32 rows, W8A16 up to 256, then the kept BF16 copy
+    for shape in (QKV, IN, OUT):
+        assert [linear_path("int8", "int8", B, *shape, True) for B in (17, 32, 33, 256, 257)] == \
+            ["gemv", "gemv", "w8a16", "w8a16", "linear"]
+        assert [linear_path("int8", "int8", B, *shape, False) for B in (17, 32, 33, 300)] == \
             ["gemv", "gemv", "w8a16", "w8a16"]
-    # narrow, K = 2048: the GEMV up to 32 rows, then the kept BF16 copy or W8A16
-    assert [linear_path("int8", "int8", B, *QKV, True) for B in (17, 32, 33, 300)] == \
-        ["gemv", "gemv", "linear", "linear"]
-    assert [linear_path("int8", "int8", B, *QKV, False) for B in (17, 32, 33)] == ["gemv", "gemv", "w8a16"]
-    # w2 (K = 8192): the kept BF16 copy, or the GEMV up to 48 rows and W8A16 beyond
-    assert [linear_path("int8", "int8", B, *W2, True) for B in (17, 64)] == ["linear", "linear"]
-    assert [linear_path("int8", "int8", B, *W2, False) for B in (17, 48, 49, 128)] == \
-        ["gemv", "gemv", "w8a16", "w8a16"]
+    # w2 (K = 8192): the kept BF16 copy up to 24 rows, W8A16 up to 256, the BF16 copy beyond; W8A16 without one
+    assert [linear_path("int8", "int8", B, *W2, True) for B in (17, 24, 25, 256, 257)] == \
+        ["linear", "linear", "w8a16", "w8a16", "linear"]
+    assert [linear_path("int8", "int8", B, *W2, False) for B in (17, 48, 49, 1024)] == ["w8a16"] * 4
 
 
 def test_int4_above_16():
@@ -52,7 +55,8 @@ def test_int4_above_16():
 def test_int8_weights_in_int4_mode():
     """w4_keep_int8 kinds are stored in INT8 under mode "int4" and follow the INT8 rules."""
     assert linear_path("int4", "int8", 24, *HEAD, True) == "w8a16"
-    assert linear_path("int4", "int8", 40, *QKV, True) == "linear"
+    assert linear_path("int4", "int8", 40, *QKV, True) == "w8a16"
+    assert linear_path("int4", "int8", 300, *QKV, True) == "linear"
 
 
 def test_bf16_weights():

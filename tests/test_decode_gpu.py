@@ -100,9 +100,16 @@ def test_linear_drop_bf16(weights):
     assert not D.lin_bf16
     paths = {(key, B): check_linear(D, key, B, B + 3) for key in SHAPES for B in (24, 40, 72)}
     assert paths[(("qkv", 0), 24)] == "gemv" and paths[(("qkv", 0), 40)] == "w8a16"
-    assert paths[(("w2", 0), 40)] == "gemv" and paths[(("w2", 0), 72)] == "w8a16"
+    assert paths[(("w2", 0), 24)] == "w8a16" and paths[(("w2", 0), 72)] == "w8a16"
     assert paths[(("head", 0), 24)] == "w8a16"
-    assert paths[(("w13", 1), 24)] == "gemv" and paths[(("w13", 1), 40)] == "w8a16"
+    assert paths[(("w13", 1), 24)] == "w8a16" and paths[(("w13", 0), 24)] == "gemv"
+
+
+def test_linear_int8_large_batches(weights):
+    """INT8 weights with a kept BF16 copy: W8A16 up to 256 rows (128 for 32768+ weight rows), F.linear beyond."""
+    D = make(weights, "int8")
+    assert check_linear(D, ("head", 0), 128, 7) == "w8a16" and check_linear(D, ("head", 0), 136, 8) == "linear"
+    assert check_linear(D, ("qkv", 0), 256, 9) == "w8a16" and check_linear(D, ("qkv", 0), 264, 10) == "linear"
 
 
 def test_keep_int8_kinds(weights):
