@@ -1,16 +1,24 @@
-// W8A8 GEMM for gfx950: Y[M, N] = epilogue( Xq[M, K] . Wq[N, K]^T ), int8 x int8 -> exact int32 on the matrix
-// cores (v_mfma_i32_32x32x32_i8), then either the int32 accumulators themselves or the per-token / per-channel
-// dequant epilogue y = bf16( gelu?( ((float)acc * sx[m]) * sw[n] + b[n] ) ) with three separately rounded fp32 ops.
+// W8A8 GEMM for gfx950 and its W8A16 sibling: Y[M, N] = epilogue( Xq[M, K] . Wq[N, K]^T ), int8 x int8 -> exact
+// int32 on the matrix cores (v_mfma_i32_32x32x32_i8), then either the int32 accumulators themselves or the
+// per-token / per-channel dequant epilogue y = bf16( gelu?( ((float)acc * sx[m]) * sw[n] + b[n] ) ) with three
+// separately rounded fp32 ops (grouped-64 activation scales: the per-group fold of gemm_i8_kernel's GRP form; INT8
+// output: requantized per 64 columns for the next GEMM).
 //
-// Tiling: a 256-thread workgroup (4 wavefronts as 2 x 2) owns a BM x BN output tile; each wavefront a
-// (BM/2) x (BN/2) block of 32 x 32 MFMA tiles. K advances in 64-byte stages through two LDS buffers: the global
-// loads of stage s + 1 are in flight (in registers) while the MFMAs of stage s run, then land in the other buffer.
-// LDS rows are 64 bytes (4 chunks of 16); chunk c of row r is stored at slot c ^ ((r >> 1) & 3), so the 8 rows a
-// ds_read_b128 phase reads at one logical chunk, and the 8 chunks a ds_write_b128 phase writes, fall in 8 distinct
-// 16-byte bank groups. M, N and K tails are zero-filled at load time (K % 16 == 0); stores are predicated.
+// Kernels:
+// - gemm_i8_kernel: one BM x BN tile per 256-thread workgroup (4 wavefronts as 2 x 2); operands go global -> LDS
+//   directly (buffer_load ... lds) through an NSTG-deep ring of 64-byte stages; optionally K split over KSP
+//   wavefront groups (exact int32 partials summed in LDS), the grouped fold (GRP), INT8 output, or bf16 activations
+//   quantized on their way into LDS (XBF).
+// - gemm_i8_big_kernel: 256 x 256 tiles on 8 wavefronts with BKT-byte stages.
+// - gemm_i8_bigp_kernel: the persistent form (one workgroup per CU walks its tiles; the next tile's first stage and
+//   epilogue operands load during the current tile's epilogue) in 256 x 256, 256 x 128, 128 x 128 and 128 x 64
+//   tiles with 2-6 ring slots of 128-byte stages, optionally with K cut across workgroups through a workspace.
+// - gemm_w8_kernel: W8A16, bf16 activations x int8 weights on the bf16 matrix cores.
+// Which kernel and tile run is decided by the cost models of the dispatch section at the end of the file.
 //
-// Activation quantization is its own memory-bound kernel (quant.hip): quantizing inside the GEMM's main loop would
-// redo the per-element VALU work once per N tile, about twice the MFMA time of the tile.
+// M, N and K tails are zero-filled at load time by the buffer range check (K % 16 == 0); stores are predicated.
+// Activation quantization is normally its own memory-bound kernel (quant.hip): the XBF form, which quantizes inside
+// the main loop, redoes that per-element work once per N tile and measured 3-6x slower on the LFM2 / SigLIP2 shapes.
 //
 // Reference: kernels/int8_gemm.cu:125-297 (gemm_i8_kernel, per-token path), :93-115 (store_tile epilogue),
 // :690-702 (pick_bm); bound as gemm_i8 in kernels/int8_gemm.cpp.
@@ -839,10 +847,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                           smem + wave * stage_bytes<TN>());
 }
 
-// Persistent form of the BM x BN kernels (256 x 256, 256 x 128, 128 x 128; 128-byte stages, two ring slots; 8
-// wavefronts as 4 x 2 blocks of BM/4 x BN/2): one workgroup per CU walks the tiles w, w + grid, ... (same XCD bands
-// as tile_of). The smaller tiles give the shapes whose 256 x 256 tiles leave CUs idle (w2 at 4096 tokens: 128
-// tiles of 256 x 256, 256 of 256 x 128; at 2048 tokens 256 of 128 x 128) one tile per CU. When a tile's K loop ends, the next tile's first stage and its
+// Persistent form of the BM x BN kernels (256 x 256, 256 x 128, 128 x 128, 128 x 64; 128-byte stages in an
+// NSLOT-deep LDS ring, NSLOT - 1 of them in flight; 8 wavefronts as 4 x 2 blocks of BM/4 x BN/2): one workgroup per
+// CU walks the tiles w, w + grid, ... (same XCD bands as tile_of). The smaller tiles give the shapes whose 256 x 256
+// tiles leave CUs idle (w2 at 4096 tokens: 128 tiles of 256 x 256, 256 of 256 x 128; at 2048 tokens 256 of
+// 128 x 128; qkv at 512 tokens 192 of 128 x 64) a tile per CU, and their smaller ring slots room for deeper rings
+// (the launcher uses 3 slots for 256 x 128, 4 for 128 x 128, 6 for 128 x 64). When a tile's K loop ends, the next tile's first stage and its
 // epilogue operands (the 256 token scales, 256 weight scales and 256 bias values, by direct loads into a second
 // small LDS buffer) are issued before the epilogue runs, so their latency hides behind the dequant and the stores,
 // and the stores drain while the next tile's first stage computes: the stage-0 wait leaves exactly the wavefront's

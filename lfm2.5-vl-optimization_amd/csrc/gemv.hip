@@ -6,6 +6,8 @@
 //                     of each row with non-temporal loads (a wavefront load = 1 KiB contiguous of one row), all of
 //                     a lane's chunks are in flight before the first FMA. int8 -> fp32 is one SDWA convert per
 //                     weight; the row sums of a wavefront's rows are reduced together (fold_sum). No LDS.
+//   gemv_b1p_kernel   batch 1 on very tall matrices (131072+ rows at the default 8 wavefronts per CU): a persistent
+//                     grid walks the rows, each wavefront's next row in flight while the current one is reduced.
 //   gemv_bn_kernel    batch 2 with rows of at most 128 chunks: the batch-1 kernel over both batch rows, each weight
 //                     chunk converted once.
 //   gemv_mfma_kernel  batch 2..64. A workgroup owns RT tiles of 16 output rows (8 when the K run is split in two
