@@ -16,13 +16,12 @@ w1|w3 16384 x 2048, w2 2048 x 8192, lm_head 65536 x 2048):
   INT8 and INT4 weights, batch <= 16: the GEMV (e.g. INT8 w1|w3 9.8 us at batch 16 against 18 us for W8A16 and for
                BF16 F.linear); its fused SwiGLU and residual epilogues run at every batch size, where the reference
                fuses at batch 1 only (_epi_ok);
-  INT8, batch > 16: the GEMV reads each weight once for up to 64 batch rows, W8A16 splits K inside its workgroups
-               when the tiles are few. The lm_head (32768+ rows) takes W8A16 (35 us against 43 us for the GEMV at 24
-               rows); w1|w3-sized weights (8192+ rows) the GEMV up to 24 rows (11.9 us against 13.4) and W8A16
-               beyond (14.3 us at 64 rows against 22.3); narrow weights with K = 2048 the GEMV up to 32 rows, then the
-               kept BF16 copy or W8A16 (qkv ~11-12 us either way, GEMV 12.9 at 64 rows); w2 (K = 8192) the kept BF16
-               copy (13.9 us at 24 rows against 19.0), or without one the GEMV up to 48 rows and W8A16 beyond (33.7
-               us at 64 rows against 37.7);
+  INT8, batch > 16: W8A16, whose K split across workgroups keeps every CU busy from 17 rows on (w1|w3 12.3 us at
+               17 rows against 13.5 for the GEMV, lm_head 33 against 37), except: narrow weights with K = 2048 keep
+               the GEMV up to 32 rows (qkv 7.2 us against 10.9); w2 (K = 8192) takes the kept BF16 copy up to 24
+               rows (13.9 us against 15.0); and with a kept BF16 copy F.linear takes over above 256 rows (128 for the
+               lm_head, 32768+ rows: 77 us against 88 at 192 rows), where W8A16's per-tile weight conversion costs
+               more than hipBLASLt's BF16 GEMM;
   INT4, batch > 16: the kept BF16 copy through F.linear, or without one the GEMV in 16-row chunks (no INT4 GEMM);
   BF16 weights: the GEMV up to batch 8, and up to 16 for K < 8192 (qkv 6.6 us against 11.3 us for F.linear at
                batch 16; w2 18.5 against 13.1), F.linear beyond.

@@ -1,0 +1,101 @@
+"""The decode runtime (lfm2opt.runtime) on the CPU: its step math against transformers' own LFM2 forward, its weight
+keys against the reference's, and the on-disk decode-weight format.
+
+The step is checked with an F.linear stand-in for DecodeLinears (the library's kernels need a GPU), in fp32, feeding
+a token sequence one position per step: the logits at every position must equal transformers' Lfm2ForCausalLM
+forward over the whole sequence (its causal attention, RMSNorms, rotary embedding and short conv) to fp32 rounding.
+This pins the restated non-matmul ops -- a rotary embedding at the wrong position, a cache slot written or masked
+wrongly, a conv state shifted the wrong way, a norm weight dropped -- at every layer type and position."""
+
+import pytest
+import torch
+
+from lfm2_tiny import TorchLinears, reference_logits, step_logits, tiny_lfm2
+
+from lfm2opt.runtime import (StaticDecoder, decode_weight_modules, decode_weights, load_decode_weights,
+                             save_decode_weights)
+
+
+def rel_err(a, b):
+    return float((a - b).abs().max() / b.abs().max())
+
+
+@pytest.mark.parametrize("conv_bias", [False, True])
+def test_step_matches_transformers_forward(conv_bias):
+    net = tiny_lfm2(seed=3, conv_bias=conv_bias)
+    dec = StaticDecoder(net, bucket=16, keep_logits=True, linears=TorchLinears(decode_weights(net)))
+    ids = torch.randint(0, net.config.vocab_size, (2, 21), generator=torch.Generator().manual_seed(4))
+    got, want = step_logits(dec, ids), reference_logits(net, ids)
+    assert rel_err(got, want) < 1e-5
+
+
+def test_step_catches_a_planted_mistake():
+    """The comparison above fails when the restated math is wrong: the rotary embedding taken at position 0 for
+    every step (a cache-position bug) moves the logits far beyond the bar."""
+    net = tiny_lfm2(seed=5)
+    dec = StaticDecoder(net, bucket=16, keep_logits=True, linears=TorchLinears(decode_weights(net)))
+    ids = torch.randint(0, net.config.vocab_size, (1, 9), generator=torch.Generator().manual_seed(6))
+    want = reference_logits(net, ids)
+    dec.inv_freq = dec.inv_freq * 0  # every position rotated as position 0
+    assert rel_err(step_logits(dec, ids), want) > 1e-2
+
+
+def test_generate_is_greedy_decoding_of_the_forward():
+    """generate(): the prompt through the step, then greedy tokens; each new token is the argmax of transformers'
+    forward over everything before it (EOS masked, as the fixed-length default asks)."""
+    net = tiny_lfm2(seed=7)
+    dec = StaticDecoder(net, bucket=16, linears=TorchLinears(decode_weights(net)))
+    ids = torch.randint(3, net.config.vocab_size, (2, 6), generator=torch.Generator().manual_seed(8))
+    out = dec.generate(ids, 5, graph=False)
+    assert out.shape == (2, 11) and torch.equal(out[:, :6], ids)
+    for t in range(6, 11):
+        logits = reference_logits(net, out[:, :t])[:, -1]
+        logits[:, dec.eos] = float("-inf")
+        assert torch.equal(out[:, t], logits.argmax(-1))
+
+
+def test_generate_requests():
+    net = tiny_lfm2(seed=9, layer_types=("conv", "full_attention"))
+    dec = StaticDecoder(net, bucket=8, linears=TorchLinears(decode_weights(net)))
+    ids = torch.randint(3, net.config.vocab_size, (1, 4), generator=torch.Generator().manual_seed(1))
+    assert dec.generate(ids, 1, graph=False).shape == (1, 5)
+    a = dec.generate(ids, 6, graph=False)
+    assert torch.equal(dec.generate(ids, 6, graph=False), a)  # state reset between requests
+    with pytest.raises(ValueError, match="padded"):
+        dec.prefill(ids, 2, attention_mask=torch.tensor([[0, 1, 1, 1]]), graph=False)
+    with pytest.raises(ValueError, match="at least one"):
+        dec.prefill(ids[:, :0], 2, graph=False)
+
+
+def test_weight_keys_match_the_reference():
+    """Keys and stacking order of the reference's StaticDecoder.lin (runtime.py:159-171, gptq.py:239-256)."""
+    net = tiny_lfm2(seed=1, layer_types=("conv", "full_attention"))
+    keys = decode_weight_modules(net)
+    assert list(keys) == [("in", 0), ("out", 0), ("w13", 0), ("w2", 0), ("qkv", 1), ("o", 1), ("w13", 1), ("w2", 1),
+                          ("head", 0)]
+    assert keys[("qkv", 1)] == [f"model.layers.1.self_attn.{s}_proj" for s in "qkv"]
+    assert keys[("w13", 0)] == ["model.layers.0.feed_forward.w1", "model.layers.0.feed_forward.w3"]
+    w = decode_weights(net)
+    a = net.model.layers[1].self_attn
+    assert torch.equal(w[("qkv", 1)], torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]))
+    f = net.model.layers[0].feed_forward
+    assert torch.equal(w[("w13", 0)], torch.cat([f.w1.weight, f.w3.weight]))
+    assert w[("head", 0)] is net.lm_head.weight
+
+
+def test_decode_weight_file_round_trip(tmp_path):
+    g = torch.Generator().manual_seed(2)
+    pre = {("w13", 0): (torch.randint(0, 255, (64, 32), dtype=torch.uint8, generator=g), torch.rand(64, 1)),
+           ("head", 0): (torch.randint(0, 255, (8, 32), dtype=torch.uint8, generator=g), torch.rand(8, 1),
+                         torch.rand(64))}
+    save_decode_weights(tmp_path / "w.pt", pre)
+    back = load_decode_weights(tmp_path / "w.pt", device="cpu")
+    assert set(back) == set(pre)
+    for k in pre:
+        assert all(torch.equal(a, b) for a, b in zip(back[k], pre[k]))
+    torch.save({"w13": (torch.zeros(1),)}, tmp_path / "bad.pt")
+    with pytest.raises(ValueError, match="not \\(kind, layer\\)"):
+        load_decode_weights(tmp_path / "bad.pt", device="cpu")
+    torch.save([torch.zeros(1)], tmp_path / "list.pt")
+    with pytest.raises(ValueError, match="expected a dict"):
+        load_decode_weights(tmp_path / "list.pt", device="cpu")
