@@ -556,6 +556,55 @@ def grouped_results(reps):
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
+def lfm2_1p2b(device="cuda"):
+    """transformers' Lfm2ForCausalLM with the LFM2-1.2B shapes (hidden 2048, 16 layers in LAYER_TYPES order, 32 query
+    / 8 KV heads of 64, FFN 8192 after the config's 2/3 adjustment, vocab 65536, tied head), random weights, bf16."""
+    from transformers import Lfm2Config, Lfm2ForCausalLM
+
+    cfg = Lfm2Config(vocab_size=VOCAB, hidden_size=H, intermediate_size=12288, num_hidden_layers=len(LAYER_TYPES),
+                     num_attention_heads=32, num_key_value_heads=8,
+                     layer_types=["full_attention" if c == "A" else "conv" for c in LAYER_TYPES],
+                     max_position_embeddings=128000, norm_eps=1e-5, conv_bias=False, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    with torch.device(device):
+        net = Lfm2ForCausalLM(cfg)
+    return net.to(torch.bfloat16).eval()
+
+
+def decode_e2e_results(steps, prompt=128):
+    """Whole decode steps of LFM2-1.2B through lfm2opt.runtime.StaticDecoder: the library's linears plus the PyTorch
+    non-matmul ops (norms, rotary embedding, attention over the static cache, short conv, argmax), one HIP graph per
+    step, after a `prompt`-token prompt; random weights. "cublas" runs every linear through F.linear (hipBLASLt), the
+    reference's baseline mode."""
+    from lfm2opt.runtime import StaticDecoder
+
+    net = lfm2_1p2b()
+    ids = torch.randint(3, VOCAB, (8, prompt), generator=torch.Generator().manual_seed(1)).cuda()
+    out = {}
+    for mode, batches in (("int8", (1, 8)), ("int4", (1,)), ("bf16", (1,)), ("cublas", (1, 8))):
+        dec = StaticDecoder(net, gemv=mode)
+        for B in batches:
+            _, s = dec.prefill(ids[:B], steps + 1)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                s["graph"].replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            out[f"{mode}.{B}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(B * 1e3 / ms, 1)}
+            log(f"decode e2e {mode} batch {B}: {ms:.4f} ms per step")
+        dec.graphs.clear()
+        del dec, s
+        torch.cuda.empty_cache()
+    del net
+    torch.cuda.empty_cache()
+    return {"workload": f"LFM2-1.2B (random weights) greedy decode, prompt {prompt} tokens, {steps} timed steps, "
+                        "cache bucket 256; whole step (linears + PyTorch non-matmul ops) as one HIP graph",
+            "results": out}
+
+
 def w8a16_results(reps):
     """W8A16 gemm_w8 (the large-batch decode fallback and a vision layer), each call on its own weights."""
     from lfm2opt.kernels import int8_ext
@@ -764,6 +813,9 @@ def main():
     ap.add_argument("--w4-batches", default="1,8", help="INT4 decode batch sizes ('' to skip)")
     ap.add_argument("--only-w8a8", action="store_true", help="W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--only-w8a16", action="store_true", help="W8A16 shapes only (no decode step, no CPU baseline)")
+    ap.add_argument("--only-e2e", action="store_true",
+                    help="only whole LFM2-1.2B decode steps through the decode runtime (lfm2opt.runtime)")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the whole-decode-step runtime leg")
     ap.add_argument("--only-w8a8-grouped", action="store_true",
                     help="grouped-64 W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--eager-kind", default=None,
@@ -793,6 +845,9 @@ def main():
         return
     if args.only_w8a16:
         print(json.dumps({"w8a16_shapes": w8a16_results(max(5, args.steps // 10))}))
+        return
+    if args.only_e2e:
+        print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4))}))
         return
     if args.only_w8a8_grouped:
         print(json.dumps({"w8a8_grouped": grouped_results(max(5, args.steps // 10))}))
@@ -831,6 +886,10 @@ def main():
     w4b = [int(b) for b in args.w4_batches.split(",") if b]
     if w4b:
         out["decode_w4"] = {str(B): decode_results(B, max(20, args.steps // 2), args.warmup, "int4") for B in w4b}
+    if not args.no_e2e:
+        log("decode e2e (runtime)")
+        out["decode_e2e"] = decode_e2e_results(max(16, args.steps // 4))
+        out["decode_e2e"]["gemv_only_step_ms_int8_b1"] = round(res1["ms_per_step"], 4)
     if not args.no_w8a8:
         shapes = w8a8_results(max(5, args.steps // 10))
         ops = sum(2.0 * r["M"] * r["N"] * r["K"] for r in shapes)
