@@ -49,6 +49,13 @@ def test_decode_dispatch_through_binding(ns):
     assert linear_path("int8", "int8", 64, 65536, 2048, True) == "w8a16"
 
 
+def test_runtime_through_binding(ns):
+    """The decode runtime of the integration section resolves under the bound name, its imports included."""
+    from lfm2q_ops.runtime import StaticDecoder, decode_weight_modules, load_decode_weights  # noqa: F401
+
+    assert StaticDecoder.generate.__qualname__ == "StaticDecoder.generate"
+
+
 @pytest.mark.gpu
 def test_binding_runs_decode_linears(ns, cuda):
     """DecodeLinears built through the bound name quantizes and runs the SwiGLU and residual GEMVs at batch 1, the
