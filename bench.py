@@ -605,6 +605,55 @@ def decode_e2e_results(steps, prompt=128):
             "results": out}
 
 
+def prefill_e2e_results(reps=5):
+    """Whole-prompt prefill of LFM2-1.2B through lfm2opt.runtime (random weights, batch 1): "int8" = every GEMM but the
+    head on W8A8 with the fused quantizing producers (prefill_int8; activation scales per 64-channel group, the
+    default), "int8_per_token" = the same with one scale per token (LFM2_INT8_GROUP=0), "bf16" = the same pass on
+    hipBLASLt BF16 GEMMs (fused_prefill in "cublas" mode); attention over the prompt in fp32 in all. Median of `reps`
+    eager passes."""
+    from lfm2opt.runtime import StaticDecoder
+
+    net = lfm2_1p2b()
+    out = {}
+    for name, kw, group in (("int8", dict(gemv="int8", prefill_int8=True), None),
+                            ("int8_per_token", dict(gemv="int8", prefill_int8=True), "0"),
+                            ("bf16", dict(gemv="cublas", fused_prefill=True), None)):
+        saved = os.environ.get("LFM2_INT8_GROUP")
+        if group is not None:
+            os.environ["LFM2_INT8_GROUP"] = group  # read when the W8A8 layers are built
+        try:
+            dec = StaticDecoder(net, **kw)
+        finally:
+            if group is not None:
+                if saved is None:
+                    os.environ.pop("LFM2_INT8_GROUP")
+                else:
+                    os.environ["LFM2_INT8_GROUP"] = saved
+        for T in (512, 2048):
+            ids = torch.randint(3, VOCAB, (1, T), generator=torch.Generator().manual_seed(T)).cuda()
+            s = dec.state(1, T + 1, 1, graph=False)
+            times = []
+            for r in range(reps + 1):
+                dec._reset(s)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                dec._prefill_batched(ids, s)
+                e1.record()
+                torch.cuda.synchronize()
+                if r:
+                    times.append(e0.elapsed_time(e1))
+            ms = sorted(times)[len(times) // 2]
+            out[f"{name}.{T}"] = {"ms": round(ms, 3), "tokens_per_s": round(T * 1e3 / ms, 1)}
+            log(f"prefill e2e {name} {T} tokens: {ms:.3f} ms")
+        del dec
+        torch.cuda.empty_cache()
+    del net
+    torch.cuda.empty_cache()
+    return {"workload": "LFM2-1.2B (random weights) prefill of one prompt of 512 / 2048 tokens in one pass "
+                        "(16 layers + the head on the last position), eager", "results": out}
+
+
 def w8a16_results(reps):
     """W8A16 gemm_w8 (the large-batch decode fallback and a vision layer), each call on its own weights."""
     from lfm2opt.kernels import int8_ext
@@ -847,7 +896,8 @@ def main():
         print(json.dumps({"w8a16_shapes": w8a16_results(max(5, args.steps // 10))}))
         return
     if args.only_e2e:
-        print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4))}))
+        print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4)),
+                          "prefill_e2e": prefill_e2e_results()}))
         return
     if args.only_w8a8_grouped:
         print(json.dumps({"w8a8_grouped": grouped_results(max(5, args.steps // 10))}))
@@ -890,6 +940,8 @@ def main():
         log("decode e2e (runtime)")
         out["decode_e2e"] = decode_e2e_results(max(16, args.steps // 4))
         out["decode_e2e"]["gemv_only_step_ms_int8_b1"] = round(res1["ms_per_step"], 4)
+        log("prefill e2e (runtime)")
+        out["prefill_e2e"] = prefill_e2e_results()
     if not args.no_w8a8:
         shapes = w8a8_results(max(5, args.steps // 10))
         ops = sum(2.0 * r["M"] * r["N"] * r["K"] for r in shapes)

@@ -19,6 +19,7 @@ from lfm2_tiny import reference_logits, step_logits, tiny_lfm2
 pytestmark = pytest.mark.gpu
 
 TOL = 4e-2
+PREFILL_TOL = 1e-1
 
 
 @pytest.fixture(scope="module")
@@ -121,3 +122,60 @@ def test_drop_bf16_frees_the_module_weights(cuda):
             mods[n].weight = torch.nn.Parameter(W[r0:r0 + rows].clone(), requires_grad=False)
             r0 += rows
     assert rel_err(got, reference_logits(ref_net, ids)) <= TOL
+
+
+def prefill_oracle(gpu_net, dec, B, w8a8):
+    """fp32 CPU copy of the GPU model with the weights the batched prefill's GEMMs read (the dequantized INT8 weights
+    for W8A8, the BF16 ones for F.linear) and, for the head, what its decode call at batch B reads."""
+    from lfm2opt.runtime import decode_weight_modules
+
+    ref = copy.deepcopy(gpu_net).to("cpu", torch.float32)
+    mods = dict(ref.named_modules())
+    for key, names in decode_weight_modules(ref).items():
+        if key[0] == "head":
+            W = path_weight(dec.lin, key, B)
+        elif w8a8:
+            W = (dec.lin.lin[key].float() * dec.lin.lin_scale[key].float()[:, None]).cpu()
+        else:
+            W = dec.lin._bf16_weight(key).float().cpu()
+        r0 = 0
+        for n in names:
+            rows = mods[n].weight.shape[0]
+            mods[n].weight = torch.nn.Parameter(W[r0:r0 + rows].clone(), requires_grad=False)
+            r0 += rows
+    return ref
+
+
+@pytest.mark.parametrize("mode,flags,group", [("int8", {"prefill_int8": True}, "64"),
+                                              ("int8", {"prefill_int8": True}, "0"),
+                                              ("int8", {"fused_prefill": True}, "64"),
+                                              ("cublas", {"fused_prefill": True}, "64")])
+def test_batched_prefill(nets, mode, flags, group, monkeypatch):
+    """The whole prompt in one pass (W8A8 with the fused quantizing producers, or BF16 GEMMs): the last position's
+    logits against transformers' forward on the weights the GEMMs read (bar PREFILL_TOL: the W8A8 form also
+    quantizes every GEMM input to int8), and the k / v rows and conv states it leaves in the static buffers against
+    the ones the per-token prefill leaves (same bar: a row at the wrong position or head is off by ~100 %); then
+    decoding continues from that state."""
+    from lfm2opt.runtime import StaticDecoder
+
+    _, gnet = nets
+    B, T = 2, 21
+    ids = torch.randint(3, gnet.config.vocab_size, (B, T), generator=torch.Generator().manual_seed(11))
+    monkeypatch.setenv("LFM2_INT8_GROUP", group)  # W8A8 activation scales per 64-channel group, or per token
+    dec = StaticDecoder(gnet, bucket=32, keep_logits=True, gemv=mode, **flags)
+    print(f"batched prefill {mode} {flags} group {group}", flush=True)
+    first, s = dec.prefill(ids, 6)
+    want = reference_logits(prefill_oracle(gnet, dec, B, "prefill_int8" in flags), ids)[:, -1]
+    err = rel_err(dec.last_prefill_logits.cpu(), want)
+    step = StaticDecoder(gnet, bucket=32, gemv=mode)
+    _, s2 = step.prefill(ids, 6, graph=False)
+    errs = {f"k{i}": rel_err(s["k"][i][:, :, :T].float().cpu(), s2["k"][i][:, :, :T].float().cpu()) for i in s["k"]}
+    errs.update({f"v{i}": rel_err(s["v"][i][:, :, :T].float().cpu(), s2["v"][i][:, :, :T].float().cpu())
+                 for i in s["v"]})
+    errs.update({f"conv{i}": rel_err(s["conv"][i].float().cpu(), s2["conv"][i].float().cpu()) for i in s["conv"]})
+    print(f"batched prefill {mode} {flags} group {group}: logits {err:.2e}, state {max(errs.values()):.2e}")
+    assert err <= PREFILL_TOL
+    assert max(errs.values()) <= PREFILL_TOL, errs
+    assert int(s["pos"]) == T and int(s["step"]) == 1 and torch.equal(s["tok"].view(-1), first)
+    out = dec.generate(ids, 6)
+    assert out.shape == (B, T + 6) and torch.equal(out[:, T], first.cpu())
