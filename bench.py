@@ -571,17 +571,21 @@ def lfm2_1p2b(device="cuda"):
     return net.to(torch.bfloat16).eval()
 
 
-def decode_e2e_results(steps, prompt=128):
-    """Whole decode steps of LFM2-1.2B through lfm2opt.runtime.StaticDecoder: the library's linears plus the PyTorch
-    non-matmul ops (norms, rotary embedding, attention over the static cache, short conv, argmax), one HIP graph per
-    step, after a `prompt`-token prompt; random weights. "cublas" runs every linear through F.linear (hipBLASLt), the
-    reference's baseline mode."""
+def decode_e2e_results(steps, prompt=128, only=None):
+    """Whole decode steps of LFM2-1.2B through lfm2opt.runtime.StaticDecoder: the library's linears and RMSNorms
+    (add_rmsnorm_q) plus the PyTorch non-matmul ops (rotary embedding, attention over the static cache, short conv,
+    argmax), one HIP graph per step, after a `prompt`-token prompt; random weights. "cublas" runs every linear
+    through F.linear (hipBLASLt), the reference's baseline mode. only = "mode.batch" runs that one configuration."""
     from lfm2opt.runtime import StaticDecoder
 
     net = lfm2_1p2b()
-    ids = torch.randint(3, VOCAB, (8, prompt), generator=torch.Generator().manual_seed(1)).cuda()
+    ids = torch.randint(3, VOCAB, (64, prompt), generator=torch.Generator().manual_seed(1)).cuda()
     out = {}
-    for mode, batches in (("int8", (1, 8)), ("int4", (1,)), ("bf16", (1,)), ("cublas", (1, 8))):
+    for mode, batches in (("int8", (1, 8, 64)), ("int4", (1,)), ("bf16", (1,)), ("cublas", (1, 8, 64))):
+        if only is not None:
+            batches = [B for B in batches if f"{mode}.{B}" == only]
+            if not batches:
+                continue
         dec = StaticDecoder(net, gemv=mode)
         for B in batches:
             _, s = dec.prefill(ids[:B], steps + 1)
@@ -865,6 +869,8 @@ def main():
     ap.add_argument("--only-e2e", action="store_true",
                     help="only whole LFM2-1.2B decode steps through the decode runtime (lfm2opt.runtime)")
     ap.add_argument("--no-e2e", action="store_true", help="skip the whole-decode-step runtime leg")
+    ap.add_argument("--e2e-mode", default=None,
+                    help="with --only-e2e: one decode configuration 'mode.batch' (e.g. int8.1) and no prefill leg")
     ap.add_argument("--only-w8a8-grouped", action="store_true",
                     help="grouped-64 W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--eager-kind", default=None,
@@ -896,8 +902,11 @@ def main():
         print(json.dumps({"w8a16_shapes": w8a16_results(max(5, args.steps // 10))}))
         return
     if args.only_e2e:
-        print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4)),
-                          "prefill_e2e": prefill_e2e_results()}))
+        if args.e2e_mode:
+            print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4), only=args.e2e_mode)}))
+        else:
+            print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4)),
+                              "prefill_e2e": prefill_e2e_results()}))
         return
     if args.only_w8a8_grouped:
         print(json.dumps({"w8a8_grouped": grouped_results(max(5, args.steps // 10))}))

@@ -116,26 +116,39 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const uint16_t *__restri
 
 // ------------------------------------------------------------------------------------------------ producers
 
-// row (+ residual) -> registers. ADD: h = bf16(h + y), written back. Lanes past the row get zeros.
+// row (+ residual) -> registers. ADD: h = bf16(h + y), written back. Lanes past the row get zeros. Every load is
+// issued before the first use -- a lane past the row reads the row's last chunk and drops it -- so the row costs one
+// memory round trip whatever CH (a row per wavefront is latency-bound when there are few rows, as in decoding).
 template <int CH>
 __device__ __forceinline__ void load_row_add(uint16_t *__restrict__ hr, const uint16_t *__restrict__ yr, int C,
                                              int lane, v4i (&hv)[CH]) {
+    v4i yv[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const size_t o = (size_t)min(c * 64 + lane, C - 1) * 8;
+        hv[c] = ld16(hr + o);
+        if (yr) yv[c] = ld16(yr + o);
+    }
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int i = c * 64 + lane;
-        hv[c] = v4i{0, 0, 0, 0};
-        if (i < C) {
-            hv[c] = ld16(hr + (size_t)i * 8);
-            if (yr) {
-                const v4i yv = ld16(yr + (size_t)i * 8);
+        if (i >= C) {
+            hv[c] = v4i{0, 0, 0, 0};
+        } else if (yr) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    hv[c][j] = (int)pack_bf16x2(bf2f_lo((uint32_t)hv[c][j]) + bf2f_lo((uint32_t)yv[j]),
-                                          bf2f_hi((uint32_t)hv[c][j]) + bf2f_hi((uint32_t)yv[j]));
-                *reinterpret_cast<v4i *>(hr + (size_t)i * 8) = hv[c];
-            }
+            for (int j = 0; j < 4; ++j)
+                hv[c][j] = (int)pack_bf16x2(bf2f_lo((uint32_t)hv[c][j]) + bf2f_lo((uint32_t)yv[c][j]),
+                                      bf2f_hi((uint32_t)hv[c][j]) + bf2f_hi((uint32_t)yv[c][j]));
+            *reinterpret_cast<v4i *>(hr + (size_t)i * 8) = hv[c];
         }
     }
+}
+
+// a per-column parameter vector (norm weight / bias) of the row's layout, loaded up front like the row
+template <int CH>
+__device__ __forceinline__ void load_params(const uint16_t *__restrict__ p, int C, int lane, v4i (&pv)[CH]) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) pv[c] = ld16(p + (size_t)min(c * 64 + lane, C - 1) * 8);
 }
 
 template <int CH>
@@ -157,7 +170,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_q_kernel(uint16_t *__restrict
     const int row = row_of_wave();
     if (row >= rows) return;
     const int C = H / 8;
-    v4i hv[CH];
+    v4i wv[CH], hv[CH];
+    load_params<CH>(w, C, lane, wv);  // in flight with the row, used after the reduction
     load_row_add<CH>(h + (size_t)row * H, y ? y + (size_t)row * H : nullptr, C, lane, hv);
     float ss = 0.f;
 #pragma unroll
@@ -176,11 +190,10 @@ __global__ __launch_bounds__(256) void add_rmsnorm_q_kernel(uint16_t *__restrict
         const int i = c * 64 + lane;
         xv[c] = v4i{0, 0, 0, 0};
         if (i < C) {
-            const v4i wv = ld16(w + (size_t)i * 8);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                xv[c][j] = (int)pack_bf16x2(bf2f_lo((uint32_t)wv[j]) * rbf(bf2f_lo((uint32_t)hv[c][j]) * rs),
-                                      bf2f_hi((uint32_t)wv[j]) * rbf(bf2f_hi((uint32_t)hv[c][j]) * rs));
+                xv[c][j] = (int)pack_bf16x2(bf2f_lo((uint32_t)wv[c][j]) * rbf(bf2f_lo((uint32_t)hv[c][j]) * rs),
+                                      bf2f_hi((uint32_t)wv[c][j]) * rbf(bf2f_hi((uint32_t)hv[c][j]) * rs));
         }
     }
     if (xo) store_row<CH>(xo + (size_t)row * H, xv, C, lane);
@@ -199,7 +212,9 @@ __global__ __launch_bounds__(256) void add_layernorm_q_kernel(uint16_t *__restri
     const int row = row_of_wave();
     if (row >= rows) return;
     const int C = D / 8;
-    v4i hv[CH];
+    v4i wv[CH], bv[CH], hv[CH];
+    load_params<CH>(w, C, lane, wv);  // in flight with the row, used after the reductions
+    load_params<CH>(b, C, lane, bv);
     load_row_add<CH>(h + (size_t)row * D, y ? y + (size_t)row * D : nullptr, C, lane, hv);
     float sum = 0.f;
 #pragma unroll
@@ -226,12 +241,11 @@ __global__ __launch_bounds__(256) void add_layernorm_q_kernel(uint16_t *__restri
         const int i = c * 64 + lane;
         xv[c] = v4i{0, 0, 0, 0};
         if (i < C) {
-            const v4i wv = ld16(w + (size_t)i * 8), bv = ld16(b + (size_t)i * 8);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float lo = ((bf2f_lo((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_lo((uint32_t)wv[j]);
-                const float hi = ((bf2f_hi((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_hi((uint32_t)wv[j]);
-                xv[c][j] = (int)pack_bf16x2(lo + bf2f_lo((uint32_t)bv[j]), hi + bf2f_hi((uint32_t)bv[j]));
+                const float lo = ((bf2f_lo((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_lo((uint32_t)wv[c][j]);
+                const float hi = ((bf2f_hi((uint32_t)hv[c][j]) - mean) * rstd) * bf2f_hi((uint32_t)wv[c][j]);
+                xv[c][j] = (int)pack_bf16x2(lo + bf2f_lo((uint32_t)bv[c][j]), hi + bf2f_hi((uint32_t)bv[c][j]));
             }
         }
     }
