@@ -99,3 +99,44 @@ def test_decode_weight_file_round_trip(tmp_path):
     torch.save([torch.zeros(1)], tmp_path / "list.pt")
     with pytest.raises(ValueError, match="expected a dict"):
         load_decode_weights(tmp_path / "list.pt", device="cpu")
+
+
+def expected_new_tokens(new, eos, n_new, check_every=4):
+    """How many new tokens generate(stop_at_eos=True) returns for one row whose EOS-free greedy tokens are `new`:
+    the prefill's token, then replays in chunks of 1, 2, 4, ... (at most check_every), stopping after the first
+    chunk that leaves EOS among the tokens so far (runtime.py:473-492)."""
+    if new[0] == eos:
+        return 1
+    n, done, chunk = n_new - 1, 0, 1
+    while done < n:
+        k = min(chunk, n - done)
+        chunk = min(2 * chunk, check_every)
+        done += k
+        if done < n and eos in new[1:1 + done]:
+            break
+    return 1 + done
+
+
+def test_generate_stop_at_eos():
+    """stop_at_eos=True: EOS is not masked, and the replay loop stops at the first check (after 1, 2, 4, ... steps)
+    where every row has produced it; the tokens are the EOS-free greedy run's (runtime.py:461-494). The linears are
+    scaled up so that greedy decoding of the random model does not repeat one token, and EOS is the sixth new token:
+    the checks after 1 and 3 replays miss it, the one after 7 sees it."""
+    net = tiny_lfm2(seed=13, layer_types=("conv", "full_attention"))
+    with torch.no_grad():
+        for name, p in net.named_parameters():
+            if name.endswith("proj.weight") or ".feed_forward.w" in name:
+                p.mul_(4.0)
+    dec = StaticDecoder(net, bucket=16, linears=TorchLinears(decode_weights(net)))
+    dec.eos, dec.eos_bias = dec.eos[:0], dec.eos_bias[:, :0]
+    ids = torch.randint(3, net.config.vocab_size, (1, 5), generator=torch.Generator().manual_seed(3))
+    free = dec.generate(ids, 12, graph=False)[0, 5:].tolist()  # no EOS token at all: plain greedy decoding
+    assert free[5] not in free[:5], free
+    dec.eos, dec.eos_bias = torch.tensor([free[5]]), torch.zeros(1, 1)
+    out = dec.generate(ids, 12, stop_at_eos=True, graph=False)
+    m = expected_new_tokens(free, free[5], 12)
+    assert m == 8
+    assert out.shape == (1, 5 + m) and out[0, 5:].tolist() == free[:m]
+    # EOS as the very first token: no replay at all
+    dec.eos = torch.tensor([free[0]])
+    assert dec.generate(ids, 12, stop_at_eos=True, graph=False).shape == (1, 6)

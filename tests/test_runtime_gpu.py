@@ -38,6 +38,10 @@ def path_weight(lin, key, B):
         return lin._bf16_weight(key).float().cpu()
     if lin.fmt(key) == "int8":
         return (w.float() * lin.lin_scale[key].float()[:, None]).cpu()
+    if w.dtype == torch.int32:  # GPTQ-style entries (qweight, fp16 scales, qzeros)
+        from lfm2opt.quant import dequantize_int4_zp
+
+        return dequantize_int4_zp(w, lin.lin_scale[key], lin.lin_zeros[key]).float().cpu()
     return dequantize_int4(w, lin.lin_scale[key]).float().cpu()
 
 
@@ -179,3 +183,50 @@ def test_batched_prefill(nets, mode, flags, group, monkeypatch):
     assert int(s["pos"]) == T and int(s["step"]) == 1 and torch.equal(s["tok"].view(-1), first)
     out = dec.generate(ids, 6)
     assert out.shape == (B, T + 6) and torch.equal(out[:, T], first.cpu())
+
+
+def test_gptq_weights_from_disk(nets, tmp_path):
+    """Pre-quantized GPTQ-style INT4 decode weights (w4_pre) written with save_decode_weights and read back with
+    load_decode_weights onto the GPU, decoded through the runtime's graph: against transformers on the dequantized
+    weights, TOL."""
+    from lfm2opt.quant import quantize_int4_zp
+    from lfm2opt.runtime import StaticDecoder, decode_weights, load_decode_weights, save_decode_weights
+
+    _, gnet = nets
+    pre = {key: tuple(t.cpu() for t in quantize_int4_zp(w)) for key, w in decode_weights(gnet).items()}
+    save_decode_weights(tmp_path / "gptq.pt", pre)
+    dec = StaticDecoder(gnet, bucket=32, keep_logits=True, gemv="int4", w4_pre=load_decode_weights(tmp_path / "gptq.pt"))
+    assert all(dec.lin.lin[key].dtype == torch.int32 for key in pre)
+    ids = torch.randint(0, gnet.config.vocab_size, (2, 13), generator=torch.Generator().manual_seed(17))
+    got = step_logits(dec, ids, graph=True)
+    err = rel_err(got, reference_logits(oracle(gnet, dec, 2), ids))
+    print(f"runtime GPTQ-style int4: max |err| / max |ref| = {err:.2e}")
+    assert err <= TOL
+
+
+def test_int8_prefill_without_bf16_copies(cuda):
+    """prefill_int8 with drop_bf16: the prompt on W8A8, decoding on the INT8 weights alone; the prefill's last logits
+    against transformers on the dequantized weights (PREFILL_TOL), and generation continues from its state."""
+    from lfm2opt.runtime import StaticDecoder
+
+    gnet = copy.deepcopy(tiny_lfm2(seed=29)).to(cuda, torch.bfloat16)
+    dec = StaticDecoder(gnet, bucket=32, keep_logits=True, gemv="int8", drop_bf16=True, prefill_int8=True)
+    assert not dec.lin.lin_bf16
+    ids = torch.randint(3, gnet.config.vocab_size, (3, 17), generator=torch.Generator().manual_seed(19))
+    first, _ = dec.prefill(ids, 5)
+    ref = copy.deepcopy(tiny_lfm2(seed=29)).to(torch.bfloat16).to(torch.float32)
+    mods = dict(ref.named_modules())
+    from lfm2opt.runtime import decode_weight_modules
+
+    for key, names in decode_weight_modules(ref).items():
+        W = (dec.lin.lin[key].float() * dec.lin.lin_scale[key].float()[:, None]).cpu()
+        r0 = 0
+        for n in names:
+            rows = mods[n].weight.shape[0]
+            mods[n].weight = torch.nn.Parameter(W[r0:r0 + rows].clone(), requires_grad=False)
+            r0 += rows
+    err = rel_err(dec.last_prefill_logits.cpu(), reference_logits(ref, ids)[:, -1])
+    print(f"int8 prefill without bf16 copies: {err:.2e}")
+    assert err <= PREFILL_TOL
+    out = dec.generate(ids, 5)
+    assert out.shape == (3, 22) and torch.equal(out[:, 17], first.cpu())
