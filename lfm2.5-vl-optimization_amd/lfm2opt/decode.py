@@ -22,7 +22,10 @@ w1|w3 16384 x 2048, w2 2048 x 8192, lm_head 65536 x 2048):
                rows (13.9 us against 15.0); and with a kept BF16 copy F.linear takes over above 256 rows (128 for the
                lm_head, 32768+ rows: 77 us against 88 at 192 rows), where W8A16's per-tile weight conversion costs
                more than hipBLASLt's BF16 GEMM;
-  INT4, batch > 16: the kept BF16 copy through F.linear, or without one the GEMV in 16-row chunks (no INT4 GEMM);
+  INT4, batch > 16: the GEMV in 16-row chunks (no INT4 GEMM) while it beats F.linear on the kept BF16 copy -- up to
+               32 rows for narrow weights with K = 2048 (qkv 10.0 us against 11.5 at 32 rows), 24 for w1|w3-sized
+               ones (16.9 against 17.4), 48 for the lm_head (67 against 71) and never for w2 (15.9 against 13.8 at
+               17 rows) -- then F.linear; without a BF16 copy always the GEMV;
   BF16 weights: the GEMV up to batch 8, and up to 16 for K < 8192 (qkv 6.6 us against 11.3 us for F.linear at
                batch 16; w2 18.5 against 13.1), F.linear beyond.
 The reference's thresholds were measured on other GPUs (BF16 GEMV up to batch 4, INT8 up to 8, INT4 at batch 1).
@@ -70,7 +73,12 @@ def linear_path(mode, fmt, B, N, K, has_bf16):
         if has_bf16 and B > (W8A16_MAX_BATCH // 2 if N >= HEAD_ROWS else W8A16_MAX_BATCH):
             return "linear"
         return "w8a16"
-    return "linear" if has_bf16 else "gemv"
+    # INT4: the GEMV (16-row chunks, a quarter of the BF16 bytes) while it beats F.linear on the kept copy
+    if not has_bf16:
+        return "gemv"
+    if K >= 8192:
+        return "linear"
+    return "gemv" if B <= (48 if N >= HEAD_ROWS else 24 if N >= W8A16_MIN_ROWS else GEMV_MAX_BATCH_NARROW) else "linear"
 
 
 class DecodeLinears:

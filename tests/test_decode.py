@@ -46,9 +46,16 @@ def test_int8_above_16():
 
 
 def test_int4_above_16():
+    # with a kept BF16 copy: the GEMV (16-row chunks) up to 32 rows for narrow weights, 24 for w1|w3-sized ones, 48
+    # for the lm_head, never for w2; F.linear beyond
+    for shape in (QKV, IN, OUT):
+        assert [linear_path("int4", "int4", B, *shape, True) for B in (17, 32, 33, 1000)] == \
+            ["gemv", "gemv", "linear", "linear"]
+    assert [linear_path("int4", "int4", B, *W13, True) for B in (17, 24, 25)] == ["gemv", "gemv", "linear"]
+    assert [linear_path("int4", "int4", B, *HEAD, True) for B in (17, 48, 49)] == ["gemv", "gemv", "linear"]
+    assert [linear_path("int4", "int4", B, *W2, True) for B in (17, 64)] == ["linear", "linear"]
     for shape in (QKV, W13, W2, HEAD):
         for B in (17, 64, 1000):
-            assert linear_path("int4", "int4", B, *shape, True) == "linear"
             assert linear_path("int4", "int4", B, *shape, False) == "gemv"  # no INT4 GEMM: the GEMV in 16-row chunks
 
 

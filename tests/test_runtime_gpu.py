@@ -70,7 +70,7 @@ def rel_err(a, b):
 
 @pytest.mark.parametrize("mode,B,paths", [("int8", 2, {"gemv"}), ("int4", 2, {"gemv"}), ("bf16", 2, {"gemv"}),
                                           ("cublas", 2, {"linear"}), ("int8", 40, {"w8a16"}),
-                                          ("int4", 20, {"linear"})])
+                                          ("int4", 20, {"gemv"}), ("int4", 40, {"linear"})])
 def test_decode_step_against_transformers(nets, mode, B, paths):
     from lfm2opt.runtime import StaticDecoder
 
