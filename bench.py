@@ -180,16 +180,24 @@ class DecodeStep:
                 fn()
 
 
+_capture_stream = None
+
+
 def capture(fn):
-    """Capture fn's launches (all on torch's current stream) into a HIP graph."""
-    s = torch.cuda.Stream()
+    """Capture fn's launches (all on torch's current stream) into a HIP graph. Warm-up and capture run on one stream
+    kept for the process, so a library call that needs the stream's GEMM workspace creates it (and its zero fill)
+    in the eager warm-up, never inside a graph."""
+    global _capture_stream
+    if _capture_stream is None:
+        _capture_stream = torch.cuda.Stream()
+    s = _capture_stream
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         fn()  # eager warm-up outside the capture
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=s):
         fn()
     torch.cuda.synchronize()
     return graph
