@@ -111,7 +111,9 @@ def workspace(t):
     """The GEMM workspace of torch's current stream on t's device: lfm2q_gemm_workspace_bytes() of device memory,
     zero-filled (by a fill kernel on that stream) when first used and kept for the process. Calls on one stream are
     ordered, so they share it; another stream gets its own. A graph captured on a stream uses that stream's
-    workspace, so graphs captured on one stream must not be replayed concurrently with each other."""
+    workspace, so graphs captured on one stream must not be replayed concurrently with each other. Make the first
+    use on a capture stream an eager call before capturing: a first use inside a capture would record the 64 MiB
+    fill into that graph (correct, but replayed every time)."""
     s = torch.cuda.current_stream(t.device)
     key = (t.device.index, s.cuda_stream)
     w = _workspaces.get(key)
