@@ -601,13 +601,13 @@ def decode_e2e_results(steps, prompt=128, only=None):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(steps):
-                s["graph"].replay()
+                s.graph.replay()
             e1.record()
             torch.cuda.synchronize()
             ms = e0.elapsed_time(e1) / steps
             out[f"{mode}.{B}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(B * 1e3 / ms, 1)}
             log(f"decode e2e {mode} batch {B}: {ms:.4f} ms per step")
-        dec.graphs.clear()
+        dec.clear_states()
         del dec, s
         torch.cuda.empty_cache()
     del net
@@ -646,7 +646,7 @@ def prefill_e2e_results(reps=5):
             s = dec.state(1, T + 1, 1, graph=False)
             times = []
             for r in range(reps + 1):
-                dec._reset(s)
+                s.clear()
                 torch.cuda.synchronize()
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()

@@ -61,13 +61,12 @@ def step_logits(dec, ids, graph=False):
     """The runtime's logits at every position of ids [B, T]: the prompt fed one token per decode step (teacher
     forcing), each step's logits read from the state's logits buffer. [B, T, V] fp32 on the CPU."""
     B, T = ids.shape
-    s = dec.state(B, T + 1, 1, graph)
-    dec._reset(s)
+    st = dec.state(B, T + 1, 1, graph)
     out = []
     dev_ids = ids.to(dec.device)
     for t in range(T):
-        s["tok"].copy_(dev_ids[:, t:t + 1])
-        s["step"].zero_()
-        s["graph"].replay() if graph else dec._step(s)
-        out.append(s["logits"].float().cpu().clone())
+        st.tok.copy_(dev_ids[:, t])
+        st.row.zero_()
+        st.graph.replay() if graph else dec._step(st)
+        out.append(st.logits.cpu().clone())
     return torch.stack(out, dim=1)

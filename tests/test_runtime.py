@@ -128,11 +128,11 @@ def test_generate_stop_at_eos():
             if name.endswith("proj.weight") or ".feed_forward.w" in name:
                 p.mul_(4.0)
     dec = StaticDecoder(net, bucket=16, linears=TorchLinears(decode_weights(net)))
-    dec.eos, dec.eos_bias = dec.eos[:0], dec.eos_bias[:, :0]
+    dec.eos = dec.eos[:0]
     ids = torch.randint(3, net.config.vocab_size, (1, 5), generator=torch.Generator().manual_seed(3))
     free = dec.generate(ids, 12, graph=False)[0, 5:].tolist()  # no EOS token at all: plain greedy decoding
     assert free[5] not in free[:5], free
-    dec.eos, dec.eos_bias = torch.tensor([free[5]]), torch.zeros(1, 1)
+    dec.eos = torch.tensor([free[5]])
     out = dec.generate(ids, 12, stop_at_eos=True, graph=False)
     m = expected_new_tokens(free, free[5], 12)
     assert m == 8

@@ -174,14 +174,12 @@ def test_batched_prefill(nets, mode, flags, group, monkeypatch):
     err = rel_err(dec.last_prefill_logits.cpu(), want)
     step = StaticDecoder(gnet, bucket=32, gemv=mode)
     _, s2 = step.prefill(ids, 6, graph=False)
-    errs = {f"k{i}": rel_err(s["k"][i][:, :, :T].float().cpu(), s2["k"][i][:, :, :T].float().cpu()) for i in s["k"]}
-    errs.update({f"v{i}": rel_err(s["v"][i][:, :, :T].float().cpu(), s2["v"][i][:, :, :T].float().cpu())
-                 for i in s["v"]})
-    errs.update({f"conv{i}": rel_err(s["conv"][i].float().cpu(), s2["conv"][i].float().cpu()) for i in s["conv"]})
+    errs = {f"kv{i}": rel_err(s.kv[i][:, :, :, :T].float().cpu(), s2.kv[i][:, :, :, :T].float().cpu()) for i in s.kv}
+    errs.update({f"conv{i}": rel_err(s.conv[i].float().cpu(), s2.conv[i].float().cpu()) for i in s.conv})
     print(f"batched prefill {mode} {flags} group {group}: logits {err:.2e}, state {max(errs.values()):.2e}")
     assert err <= PREFILL_TOL
     assert max(errs.values()) <= PREFILL_TOL, errs
-    assert int(s["pos"]) == T and int(s["step"]) == 1 and torch.equal(s["tok"].view(-1), first)
+    assert s.ctr.tolist() == [T, 1] and torch.equal(s.tok, first)
     out = dec.generate(ids, 6)
     assert out.shape == (B, T + 6) and torch.equal(out[:, T], first.cpu())
 
@@ -264,4 +262,4 @@ def test_full_size_decode_against_transformers(full_size, mode, B, paths):
     err = rel_err(got, reference_logits(oracle(full_size, dec, B), ids))
     print(f"full-size {mode} B={B}: max |err| / max |ref| = {err:.2e}")
     assert err <= FULL_TOL
-    dec.graphs.clear()
+    dec.clear_states()
