@@ -59,6 +59,7 @@ def test_generate_requests():
     dec = StaticDecoder(net, bucket=8, linears=TorchLinears(decode_weights(net)))
     ids = torch.randint(3, net.config.vocab_size, (1, 4), generator=torch.Generator().manual_seed(1))
     assert dec.generate(ids, 1, graph=False).shape == (1, 5)
+    assert torch.equal(dec.generate(ids, 0, graph=False), dec.generate(ids, 1, graph=False))  # at least one token
     a = dec.generate(ids, 6, graph=False)
     assert torch.equal(dec.generate(ids, 6, graph=False), a)  # state reset between requests
     with pytest.raises(ValueError, match="padded"):
