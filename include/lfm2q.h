@@ -190,9 +190,9 @@ int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, const float
                   lfm2q_bf16 *Y, int M, int N, int K, int gelu, lfm2q_stream_t stream);
 
 /* lfm2q_gemm_i8 with a workspace: where the output tiles are fewer than the CUs (few tokens, narrow N) the
- * persistent 256 x 128 / 128 x 128 kernels may also cut K into 2..8 slices over workgroups; each slice's int32
- * accumulators go to the workspace and the last workgroup of a tile adds them (exact) before the epilogue, so Y is
- * bit-identical to lfm2q_gemm_i8's. ws: lfm2q_gemm_workspace_bytes() of device memory (or at least 64 KiB: a
+ * persistent 256 x 128 / 128 x 128 / 128 x 64 kernels may also cut K into 2..8 slices over workgroups; each slice's
+ * int32 accumulators go to the workspace and the last workgroup of a tile adds them (exact) before the epilogue, so
+ * Y is bit-identical to lfm2q_gemm_i8's. ws: lfm2q_gemm_workspace_bytes() of device memory (or at least 64 KiB: a
  * smaller one only limits the slices), 256-byte aligned, zero-filled before its first use; every call that returns
  * 0 leaves its counters zero again. Calls sharing a workspace must not overlap (one stream, or ordered); ws NULL is
  * lfm2q_gemm_i8. No counterpart in the reference (added for the K split). */
