@@ -298,4 +298,3 @@ def test_full_size_prefill_against_transformers(full_size, flags, bar):
     assert err <= bar
     assert torch.equal(got.argmax(-1), want.argmax(-1))
     dec.clear_states()
-
