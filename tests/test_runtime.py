@@ -68,6 +68,27 @@ def test_generate_requests():
         dec.prefill(ids[:, :0], 2, graph=False)
 
 
+def test_batched_prefill_leaves_the_state_of_the_step():
+    """fused_prefill on the CPU model: the last position's logits equal transformers' forward, and the key / value
+    caches and conv rings it leaves equal those of the prompt run through the step one position per step, at prompt
+    lengths covering every ring offset (T mod L) and a prompt shorter than L; generation then continues the same."""
+    net = tiny_lfm2(seed=4, conv_bias=True)
+    lin = TorchLinears(decode_weights(net))
+    assert net.config.conv_L_cache == 3
+    for T in (1, 2, 5, 7):
+        ids = torch.randint(3, net.config.vocab_size, (2, T), generator=torch.Generator().manual_seed(T))
+        fused = StaticDecoder(net, bucket=16, keep_logits=True, fused_prefill=True, linears=lin)
+        first, s = fused.prefill(ids, 4, graph=False)
+        assert rel_err(fused.last_prefill_logits, reference_logits(net, ids)[:, -1]) < 1e-5
+        step = StaticDecoder(net, bucket=16, linears=lin)
+        first2, s2 = step.prefill(ids, 4, graph=False)
+        assert torch.equal(first, first2) and s.ctr.tolist() == s2.ctr.tolist() == [T, 1]
+        for name in ("k", "v", "conv"):
+            for i, buf in getattr(s, name).items():
+                assert rel_err(buf, getattr(s2, name)[i]) < 1e-5, (T, name, i)
+        assert torch.equal(fused.generate(ids, 4, graph=False), step.generate(ids, 4, graph=False))
+
+
 def test_weight_keys_match_the_reference():
     """Keys and stacking order of the reference's StaticDecoder.lin (runtime.py:159-171, gptq.py:239-256)."""
     net = tiny_lfm2(seed=1, layer_types=("conv", "full_attention"))

@@ -174,7 +174,8 @@ def test_batched_prefill(nets, mode, flags, group, monkeypatch):
     err = rel_err(dec.last_prefill_logits.cpu(), want)
     step = StaticDecoder(gnet, bucket=32, gemv=mode)
     _, s2 = step.prefill(ids, 6, graph=False)
-    errs = {f"kv{i}": rel_err(s.kv[i][:, :, :, :T].float().cpu(), s2.kv[i][:, :, :, :T].float().cpu()) for i in s.kv}
+    errs = {f"k{i}": rel_err(s.k[i][..., :T].float().cpu(), s2.k[i][..., :T].float().cpu()) for i in s.k}
+    errs.update({f"v{i}": rel_err(s.v[i][:, :, :T].float().cpu(), s2.v[i][:, :, :T].float().cpu()) for i in s.v})
     errs.update({f"conv{i}": rel_err(s.conv[i].float().cpu(), s2.conv[i].float().cpu()) for i in s.conv})
     print(f"batched prefill {mode} {flags} group {group}: logits {err:.2e}, state {max(errs.values()):.2e}")
     assert err <= PREFILL_TOL
@@ -269,9 +270,12 @@ def test_full_size_decode_against_transformers(full_size, mode, B, paths):
 def test_full_size_prefill_against_transformers(full_size, flags, bar):
     """A 64-token prompt through the one-pass prefill at the LFM2-1.2B shapes: the last position's logits against
     transformers' fp32 forward on the CPU on the weights the GEMMs read (the dequantized INT8 weights for W8A8 and
-    the head, the BF16 ones for the BF16 GEMMs), and the same top token. The W8A8 bar (2e-1) covers quantizing every
-    GEMM input to int8 with grouped-64 scales: measured 10.9 % at this depth, against 3.4 % for the same pass on BF16
-    GEMMs and 4.2 % for the prompt through the decode step; a row at the wrong position or group is off by ~100 %."""
+    the head, the BF16 ones for the BF16 GEMMs): the largest error against the largest logit, and the correlation of
+    the two logit vectors (>= 0.98), which a row at the wrong position or group drives toward 0. The W8A8 bar (2e-1)
+    covers quantizing every GEMM input to int8 with grouped-64 scales: measured 9.3-10.9 % at this depth, against
+    3.4 % for the same pass on BF16 GEMMs and 4.2 % for the prompt through the decode step; a row at the wrong
+    position or group is off by ~100 %. The top token is not compared: a random model's 65536 logits are too close
+    for it to be fixed by errors of this size (a W8A8 run at 9.3 % picked another token than the fp32 forward)."""
     from lfm2opt.runtime import StaticDecoder, decode_weight_modules
 
     dec = StaticDecoder(full_size, bucket=16, keep_logits=True, gemv="int8", **flags)
@@ -294,7 +298,8 @@ def test_full_size_prefill_against_transformers(full_size, flags, bar):
     want = reference_logits(ref, ids)[:, -1]
     got = dec.last_prefill_logits.cpu()
     err = rel_err(got, want)
-    print(f"full-size prefill {flags}: max |err| / max |ref| = {err:.2e}")
+    corr = float(torch.corrcoef(torch.cat((got, want)))[0, 1])
+    print(f"full-size prefill {flags}: max |err| / max |ref| = {err:.2e}, correlation {corr:.5f}")
     assert err <= bar
-    assert torch.equal(got.argmax(-1), want.argmax(-1))
+    assert corr >= 0.98
     dec.clear_states()
