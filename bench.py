@@ -617,19 +617,24 @@ def decode_e2e_results(steps, prompt=128, only=None):
             "results": out}
 
 
-def prefill_e2e_results(reps=5):
+def prefill_e2e_results(reps=5, only=None):
     """Whole-prompt prefill of LFM2-1.2B through lfm2opt.runtime (random weights, batch 1): "int8" = every GEMM but the
     head on W8A8 with the fused quantizing producers (prefill_int8; activation scales per 64-channel group, the
     default), "int8_per_token" = the same with one scale per token (LFM2_INT8_GROUP=0), "bf16" = the same pass on
-    hipBLASLt BF16 GEMMs (fused_prefill in "cublas" mode); attention over the prompt in fp32 in all. Median of `reps`
-    eager passes."""
+    hipBLASLt BF16 GEMMs (fused_prefill in "cublas" mode); in all, the prompt's attention as bf16 batched products
+    with an fp32 softmax. Median of `reps` eager passes. only: one configuration 'mode.tokens' (e.g. int8.2048)."""
     from lfm2opt.runtime import StaticDecoder
 
+    tokens = (512, 2048)
+    if only is not None and only not in {f"{n}.{T}" for n in ("int8", "int8_per_token", "bf16") for T in tokens}:
+        raise ValueError(f"unknown prefill configuration {only!r}")
     net = lfm2_1p2b()
     out = {}
     for name, kw, group in (("int8", dict(gemv="int8", prefill_int8=True), None),
                             ("int8_per_token", dict(gemv="int8", prefill_int8=True), "0"),
                             ("bf16", dict(gemv="cublas", fused_prefill=True), None)):
+        if only is not None and not only.startswith(name + "."):
+            continue
         saved = os.environ.get("LFM2_INT8_GROUP")
         if group is not None:
             os.environ["LFM2_INT8_GROUP"] = group  # read when the W8A8 layers are built
@@ -641,7 +646,9 @@ def prefill_e2e_results(reps=5):
                     os.environ.pop("LFM2_INT8_GROUP")
                 else:
                     os.environ["LFM2_INT8_GROUP"] = saved
-        for T in (512, 2048):
+        for T in tokens:
+            if only is not None and only != f"{name}.{T}":
+                continue
             ids = torch.randint(3, VOCAB, (1, T), generator=torch.Generator().manual_seed(T)).cuda()
             s = dec.state(1, T + 1, 1, graph=False)
             times = []
@@ -879,6 +886,8 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the whole-decode-step runtime leg")
     ap.add_argument("--e2e-mode", default=None,
                     help="with --only-e2e: one decode configuration 'mode.batch' (e.g. int8.1) and no prefill leg")
+    ap.add_argument("--prefill-mode", default=None,
+                    help="with --only-e2e: one prefill configuration 'mode.tokens' (e.g. int8.2048) and no decode leg")
     ap.add_argument("--only-w8a8-grouped", action="store_true",
                     help="grouped-64 W8A8 shapes only (no decode step, no CPU baseline)")
     ap.add_argument("--eager-kind", default=None,
@@ -912,6 +921,8 @@ def main():
     if args.only_e2e:
         if args.e2e_mode:
             print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4), only=args.e2e_mode)}))
+        elif args.prefill_mode:
+            print(json.dumps({"prefill_e2e": prefill_e2e_results(only=args.prefill_mode)}))
         else:
             print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4)),
                               "prefill_e2e": prefill_e2e_results()}))
