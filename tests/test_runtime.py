@@ -71,13 +71,15 @@ def test_generate_requests():
 def test_batched_prefill_leaves_the_state_of_the_step():
     """fused_prefill on the CPU model: the last position's logits equal transformers' forward, and the key / value
     caches and conv rings it leaves equal those of the prompt run through the step one position per step, at prompt
-    lengths covering every ring offset (T mod L) and a prompt shorter than L; generation then continues the same."""
+    lengths covering every ring offset (T mod L) and a prompt shorter than L; generation then continues the same.
+    The prompt attention is taken in one block and (blocks_from = 4) in four blocks of uneven sizes."""
     net = tiny_lfm2(seed=4, conv_bias=True)
     lin = TorchLinears(decode_weights(net))
     assert net.config.conv_L_cache == 3
-    for T in (1, 2, 5, 7):
+    for T, blocks_from in ((1, 1024), (2, 1024), (5, 1024), (7, 1024), (5, 4), (7, 4), (11, 4)):
         ids = torch.randint(3, net.config.vocab_size, (2, T), generator=torch.Generator().manual_seed(T))
         fused = StaticDecoder(net, bucket=16, keep_logits=True, fused_prefill=True, linears=lin)
+        fused.prompt_blocks_from = blocks_from
         first, s = fused.prefill(ids, 4, graph=False)
         assert rel_err(fused.last_prefill_logits, reference_logits(net, ids)[:, -1]) < 1e-5
         step = StaticDecoder(net, bucket=16, linears=lin)
