@@ -60,3 +60,8 @@ def test_workloads():
     vision = {(10240, 1152, 3456, True, False), (10240, 1152, 1152, True, False), (10240, 1152, 4304, True, True),
               (10240, 4304, 1152, True, False)}
     assert len(bench.W8A8_SHAPES) == 13 and shapes == lm | vision
+
+
+def test_unknown_prefill_configuration_is_refused_before_building_the_model():
+    with pytest.raises(ValueError, match="unknown prefill configuration"):
+        bench.prefill_e2e_results(only="int8.1000")
