@@ -151,16 +151,19 @@ def prefill_oracle(gpu_net, dec, B, w8a8):
     return ref
 
 
-@pytest.mark.parametrize("mode,flags,group", [("int8", {"prefill_int8": True}, "64"),
-                                              ("int8", {"prefill_int8": True}, "0"),
-                                              ("int8", {"fused_prefill": True}, "64"),
-                                              ("cublas", {"fused_prefill": True}, "64")])
-def test_batched_prefill(nets, mode, flags, group, monkeypatch):
+@pytest.mark.parametrize("mode,flags,group,blocks_from", [("int8", {"prefill_int8": True}, "64", 1024),
+                                                          ("int8", {"prefill_int8": True}, "0", 1024),
+                                                          ("int8", {"fused_prefill": True}, "64", 1024),
+                                                          ("cublas", {"fused_prefill": True}, "64", 1024),
+                                                          ("int8", {"prefill_int8": True}, "64", 8),
+                                                          ("cublas", {"fused_prefill": True}, "64", 8)])
+def test_batched_prefill(nets, mode, flags, group, blocks_from, monkeypatch):
     """The whole prompt in one pass (W8A8 with the fused quantizing producers, or BF16 GEMMs): the last position's
     logits against transformers' forward on the weights the GEMMs read (bar PREFILL_TOL: the W8A8 form also
     quantizes every GEMM input to int8), and the k / v rows and conv states it leaves in the static buffers against
     the ones the per-token prefill leaves (same bar: a row at the wrong position or head is off by ~100 %); then
-    decoding continues from that state."""
+    decoding continues from that state. blocks_from 8 takes the prompt attention in four blocks of positions (the
+    form prompts of 1024 positions and more take)."""
     from lfm2opt.runtime import StaticDecoder
 
     _, gnet = nets
@@ -168,7 +171,8 @@ def test_batched_prefill(nets, mode, flags, group, monkeypatch):
     ids = torch.randint(3, gnet.config.vocab_size, (B, T), generator=torch.Generator().manual_seed(11))
     monkeypatch.setenv("LFM2_INT8_GROUP", group)  # W8A8 activation scales per 64-channel group, or per token
     dec = StaticDecoder(gnet, bucket=32, keep_logits=True, gemv=mode, **flags)
-    print(f"batched prefill {mode} {flags} group {group}", flush=True)
+    dec.prompt_blocks_from = blocks_from
+    print(f"batched prefill {mode} {flags} group {group} blocks_from {blocks_from}", flush=True)
     first, s = dec.prefill(ids, 6)
     want = reference_logits(prefill_oracle(gnet, dec, B, "prefill_int8" in flags), ids)[:, -1]
     err = rel_err(dec.last_prefill_logits.cpu(), want)
@@ -177,7 +181,8 @@ def test_batched_prefill(nets, mode, flags, group, monkeypatch):
     errs = {f"k{i}": rel_err(s.k[i][..., :T].float().cpu(), s2.k[i][..., :T].float().cpu()) for i in s.k}
     errs.update({f"v{i}": rel_err(s.v[i][:, :, :T].float().cpu(), s2.v[i][:, :, :T].float().cpu()) for i in s.v})
     errs.update({f"conv{i}": rel_err(s.conv[i].float().cpu(), s2.conv[i].float().cpu()) for i in s.conv})
-    print(f"batched prefill {mode} {flags} group {group}: logits {err:.2e}, state {max(errs.values()):.2e}")
+    print(f"batched prefill {mode} {flags} group {group} blocks_from {blocks_from}: logits {err:.2e}, "
+          f"state {max(errs.values()):.2e}")
     assert err <= PREFILL_TOL
     assert max(errs.values()) <= PREFILL_TOL, errs
     assert s.ctr.tolist() == [T, 1] and torch.equal(s.tok, first)
