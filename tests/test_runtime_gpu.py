@@ -200,7 +200,8 @@ def test_gptq_weights_from_disk(nets, tmp_path):
     _, gnet = nets
     pre = {key: tuple(t.cpu() for t in quantize_int4_zp(w)) for key, w in decode_weights(gnet).items()}
     save_decode_weights(tmp_path / "gptq.pt", pre)
-    dec = StaticDecoder(gnet, bucket=32, keep_logits=True, gemv="int4", w4_pre=load_decode_weights(tmp_path / "gptq.pt"))
+    dec = StaticDecoder(gnet, bucket=32, keep_logits=True, gemv="int4",
+                        w4_pre=load_decode_weights(tmp_path / "gptq.pt"))
     assert all(dec.lin.lin[key].dtype == torch.int32 for key in pre)
     ids = torch.randint(0, gnet.config.vocab_size, (2, 13), generator=torch.Generator().manual_seed(17))
     got = step_logits(dec, ids, graph=True)
