@@ -886,6 +886,8 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the whole-decode-step runtime leg")
     ap.add_argument("--e2e-mode", default=None,
                     help="with --only-e2e: one decode configuration 'mode.batch' (e.g. int8.1) and no prefill leg")
+    ap.add_argument("--e2e-prompt", type=int, default=128,
+                    help="with --only-e2e: prompt tokens before the timed decode steps (the cache grows with it)")
     ap.add_argument("--prefill-mode", default=None,
                     help="with --only-e2e: one prefill configuration 'mode.tokens' (e.g. int8.2048) and no decode leg")
     ap.add_argument("--only-w8a8-grouped", action="store_true",
@@ -920,11 +922,12 @@ def main():
         return
     if args.only_e2e:
         if args.e2e_mode:
-            print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4), only=args.e2e_mode)}))
+            print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4), prompt=args.e2e_prompt,
+                                                               only=args.e2e_mode)}))
         elif args.prefill_mode:
             print(json.dumps({"prefill_e2e": prefill_e2e_results(only=args.prefill_mode)}))
         else:
-            print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4)),
+            print(json.dumps({"decode_e2e": decode_e2e_results(max(16, args.steps // 4), prompt=args.e2e_prompt),
                               "prefill_e2e": prefill_e2e_results()}))
         return
     if args.only_w8a8_grouped:
