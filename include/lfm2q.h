@@ -124,8 +124,10 @@ size_t lfm2q_gemv_chain_workspace_bytes(void);
  * reads these; 16-byte aligned). K in {1024, 2048, 4096, 8192}, N <= 512 x the CU count, n_ops <= 128.
  * workspace: lfm2q_gemv_chain_workspace_bytes() of device memory, 256-byte aligned, zero-filled before its first
  * use and then left alone (it carries a launch counter between calls); calls sharing a workspace must be ordered
- * (one stream). Word 1 of the workspace (uint32) becomes nonzero if a dependency wait ran out (20 ms, e.g. because
- * not every workgroup of the launch could be resident); the outputs of that launch are then undefined.
+ * (one stream). Word 0 of the workspace (uint32) counts the completed launches; word 1 is set to that count (the
+ * launch's own number + 1) when a dependency wait of a launch runs out (20 ms, e.g. because not every workgroup of
+ * the launch could be resident; the bound is the knob LFM2Q_CHAIN_WAIT_MS): after a launch, word 1 == word 0 means
+ * that launch's outputs are undefined. An expired launch does not affect the launches after it.
  * No counterpart entry point in the reference, which chains separate launches with programmatic dependent launch
  * (kernels/lfm2_decode.cu:24-62, the weight prefetch before the dependency wait at :500-512, :600-609). */
 int lfm2q_gemv_chain(const lfm2q_gemv_op *ops, const lfm2q_gemv_op *ops_dev, int n_ops, void *workspace,

@@ -27,8 +27,10 @@
 //     read-modify-write atomics.
 //   * epoch(j) = gen * 1024 + j + 1 for the gen-th launch on a workspace (gen is read at the start, incremented
 //     once all workgroups have read it), compared as a wrapping difference, so the flags never need resetting.
-//     Every wait is bounded (20 ms of the real-time counter): a wait that runs out sets the workspace's error word,
-//     and from then on every wait of every workgroup returns at once, so the kernel always finishes.
+//     Every wait is bounded (20 ms of the real-time counter by default, knob LFM2Q_CHAIN_WAIT_MS): a wait that runs
+//     out writes the launch's tag gen + 1 into the workspace's error word, and from then on every wait of every
+//     workgroup of that launch returns at once, so the kernel always finishes. The next launch has another tag, so
+//     its waits are not cut short by an earlier launch's error.
 //
 // Per row the arithmetic is exactly the batch-1 GEMV kernels' (gemv_math.hpp: lane l owns 16-byte chunk l + 64 u of
 // the row, chunk products on v_dot2_f32_bf16 in order of u, fold_sum over the lanes, the same epilogue), so each
@@ -61,7 +63,7 @@ constexpr int WS_GEN = 0, WS_ERR = 1; // workspace words; the flags start 128 by
 constexpr int WS_FLAGS = 32;
 constexpr int FLAG_COPIES = 8;        // every flag is written to 8 copies of the flag array; workgroup g polls copy g % 8
 constexpr int FLAG_STRIDE = 1088;     // words between copies (4352 bytes: the copies sit in different memory channels)
-constexpr uint64_t WAIT_TICKS = 2000000;  // 20 ms at the 100 MHz s_memrealtime clock
+constexpr uint64_t TICKS_PER_MS = 100000;  // the s_memrealtime clock runs at 100 MHz
 constexpr int AUX_SC1 = 16;           // device-scope coherent access (sc1)
 
 struct ChainOp {
@@ -168,8 +170,8 @@ struct Loader {
         const v4i d = {__builtin_amdgcn_readfirstlane(desc[0]), __builtin_amdgcn_readfirstlane(desc[1]),
                        __builtin_amdgcn_readfirstlane(desc[2]), __builtin_amdgcn_readfirstlane(desc[3])};
         // non-temporal: each weight byte is read once (measured: 6.2 -> 7.0 TB/s for a streaming ring like this one)
-        asm volatile("buffer_load_dwordx4 %0, %1, 0 offen nt lds" ::"v"((uint32_t)lane * 16u + offset()), "s"(d),
-                     "{m0}"(lds_addr(slot))
+        asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dwordx4 %0, %1, 0 offen nt lds"
+                     ::"v"((uint32_t)lane * 16u + offset()), "s"(d), "{m0}"(lds_addr(slot))
                      : "memory");
     }
     // the next n units of the stream into the ring slots from position p on (a loop, not unrolled: one copy of
@@ -267,7 +269,10 @@ __device__ __forceinline__ bool all_reached(const uint32_t (&f)[4], int lane, in
     for (int e = 0; e < 4; ++e) ok = ok && (lane + 64 * e >= G || (int)(f[e] - target) >= 0);
     return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
-__device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target, int lane) {
+// The error word holds the tag (gen + 1) of the last launch whose wait ran out: a later launch on the workspace
+// compares it with its own tag, so one expired launch does not cut short the waits of the next.
+__device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target, int lane, uint32_t tag,
+                                           uint64_t wait_ticks) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     const uint32_t *flags = ws + WS_FLAGS + (blockIdx.x % FLAG_COPIES) * FLAG_STRIDE;
     if (G <= 256) {
@@ -284,9 +289,9 @@ __device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target,
             if (all_reached(b, lane, G, target)) break;
             poll(b);
             if ((it & 7) == 7) {
-                if (ld_word(ws + WS_ERR)) break;
-                if (__builtin_amdgcn_s_memrealtime() - t0 > WAIT_TICKS) {
-                    if (lane == 0) st_word(ws + WS_ERR, 1u);
+                if (ld_word(ws + WS_ERR) == tag) break;
+                if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) {
+                    if (lane == 0) st_word(ws + WS_ERR, tag);
                     break;
                 }
             }
@@ -295,9 +300,9 @@ __device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target,
         for (;;) {
             bool ok = true;
             for (int i = lane; i < G; i += 64) ok = ok && (int)(ld_word(flags + i) - target) >= 0;
-            if (__builtin_amdgcn_ballot_w64(!ok) == 0 || ld_word(ws + WS_ERR)) break;
-            if (__builtin_amdgcn_s_memrealtime() - t0 > WAIT_TICKS) {
-                if (lane == 0) st_word(ws + WS_ERR, 1u);
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0 || ld_word(ws + WS_ERR) == tag) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) {
+                if (lane == 0) st_word(ws + WS_ERR, tag);
                 break;
             }
         }
@@ -307,7 +312,8 @@ __device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target,
 
 __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp *__restrict__ ops, int n_ops,
                                                                    uint32_t *__restrict__ ws, int G,
-                                                                   uint32_t *__restrict__ status) {
+                                                                   uint32_t *__restrict__ status,
+                                                                   uint64_t wait_ticks) {
     __shared__ __attribute__((aligned(1024))) Lds L;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -320,7 +326,7 @@ __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp
     if (w == CW) {  // ------------------------------------------------------------------ the sync wavefront
         const uint32_t gen = __builtin_amdgcn_readfirstlane(ld_word(ws + WS_GEN));
         for (int j = 0; j < n_ops; ++j) {
-            if (j) wait_flags(ws, G, gen * EPOCHS + (uint32_t)j, lane);  // op j - 1 complete everywhere
+            if (j) wait_flags(ws, G, gen * EPOCHS + (uint32_t)j, lane, gen + 1u, wait_ticks);  // op j - 1 done
             const int N = __builtin_amdgcn_readfirstlane(L.ops[j].N), K = __builtin_amdgcn_readfirstlane(L.ops[j].K);
             const int epi = __builtin_amdgcn_readfirstlane(L.ops[j].epi);
             const float *scale = uniform_ptr(L.ops[j].scale);
@@ -337,12 +343,12 @@ __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp
                 if (1024 * q < K * 2) xv[q] = ld_dev16(xr, (uint32_t)(1024 * q + 16 * lane));
             const v4i sd = make_desc(scale, (uint32_t)(epi == EPI_SWIGLU ? 2 * N : N) * 4u);
             for (int i = 0; i < nr; i += 64) {
-                asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"((uint32_t)(r0 + i + lane) * 4u), "s"(sd),
-                             "{m0}"(lds_addr(&L.sc[0][i]))
+                asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dword %0, %1, 0 offen lds"
+                             ::"v"((uint32_t)(r0 + i + lane) * 4u), "s"(sd), "{m0}"(lds_addr(&L.sc[0][i]))
                              : "memory");
                 if (epi == EPI_SWIGLU)
-                    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"((uint32_t)(N + r0 + i + lane) * 4u),
-                                 "s"(sd), "{m0}"(lds_addr(&L.sc[1][i]))
+                    asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dword %0, %1, 0 offen lds"
+                                 ::"v"((uint32_t)(N + r0 + i + lane) * 4u), "s"(sd), "{m0}"(lds_addr(&L.sc[1][i]))
                                  : "memory");
             }
             const rsrc_t yr = make_rsrc(uniform_ptr(L.ops[j].y), (uint32_t)N * 2u);
@@ -367,10 +373,10 @@ __global__ __launch_bounds__(64 * (CW + 1)) void gemv_chain_kernel(const ChainOp
             if (lane < FLAG_COPIES) st_word(ws + WS_FLAGS + lane * FLAG_STRIDE + g, gen * EPOCHS + (uint32_t)j + 1u);
         }
         if (g == 0) {  // once every workgroup is past the last op (so has read gen), advance gen for the next launch
-            wait_flags(ws, G, gen * EPOCHS + (uint32_t)n_ops, lane);
+            wait_flags(ws, G, gen * EPOCHS + (uint32_t)n_ops, lane, gen + 1u, wait_ticks);
             if (lane == 0) st_word(ws + WS_GEN, gen + 1u);
             // every workgroup has stored its last flag, so any expired wait has set the error word by now
-            if (lane == 0 && status) st_word(status, ld_word(ws + WS_ERR));
+            if (lane == 0 && status) st_word(status, ld_word(ws + WS_ERR) == gen + 1u ? 1u : 0u);
         }
         return;
     }
@@ -433,8 +439,9 @@ int check_chain(const char *who, const lfm2q_gemv_op *ops, int n_ops, int &G) {
 
 int launch_chain(const char *who, const lfm2q_gemv_op *ops_dev, int n_ops, int G, uint32_t *ws, uint32_t *status,
                  hipStream_t stream) {
+    const uint64_t ticks = (uint64_t)std::max(0, knob_int(KNOB_CHAIN_WAIT_MS, 20)) * TICKS_PER_MS;
     gemv_chain_kernel<<<G, 64 * (CW + 1), 0, stream>>>(reinterpret_cast<const ChainOp *>(ops_dev), n_ops, ws, G,
-                                                       status);
+                                                       status, ticks);
     return launch_status(who);
 }
 

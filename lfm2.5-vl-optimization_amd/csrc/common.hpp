@@ -130,12 +130,22 @@ __device__ __forceinline__ v4i make_desc(const void *base, uint32_t bytes) {
 // which the compiler loads for the asm). Written as inline asm so the compiler, which cannot see which LDS bytes
 // the load writes, does not drain every outstanding load before each LDS read or barrier; the kernel orders it with
 // explicit s_waitcnt + barrier.
+// The compiler does not insert wait states in front of an inline-asm statement, and two gfx9 hazards apply to this
+// load's scalar operands: a VALU write of an SGPR (v_readlane_b32 restoring a spilled resource, v_readfirstlane_b32)
+// needs 5 wait states before a vector memory instruction reads it, and an SALU write of M0 needs 1 before a
+// direct-to-LDS load reads it. Without them the load can take the register's old value: a stale resource base
+// faulted the GPU in a persistent GEMM whose spilled resource was reloaded just before its load. Hence the
+// `s_nop 4` (5 wait states) inside the statement; hazard_lint.py checks the built library for both hazards.
+#define LFM2Q_LDS_DMA_WAIT "s_nop 4\n\t"
 __device__ __forceinline__ void lds_dma16(v4i desc, uint32_t voff, uint32_t lds_base) {
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base) : "memory");
+    asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(desc),
+                 "{m0}"(lds_base)
+                 : "memory");
 }
 // 4 bytes per lane from buffer offset `voff` into LDS at lds_base + 4 * lane
 __device__ __forceinline__ void lds_dma4(v4i desc, uint32_t voff, uint32_t lds_base) {
-    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base) : "memory");
+    asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base)
+                 : "memory");
 }
 // LDS address of p as a wavefront-uniform (SGPR) value for M0
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {

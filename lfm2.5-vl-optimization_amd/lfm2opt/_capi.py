@@ -107,17 +107,47 @@ def ptr(t):
 _workspaces = {}
 
 
-def workspace(t):
-    """The GEMM workspace of torch's current stream on t's device: lfm2q_gemm_workspace_bytes() of device memory,
-    zero-filled (by a fill kernel on that stream) when first used and kept for the process. Calls on one stream are
-    ordered, so they share it; another stream gets its own. A graph captured on a stream uses that stream's
-    workspace, so graphs captured on one stream must not be replayed concurrently with each other. Make the first
-    use on a capture stream an eager call before capturing: a first use inside a capture would record the 64 MiB
-    fill into that graph (correct, but replayed every time)."""
-    s = torch.cuda.current_stream(t.device)
-    key = (t.device.index, s.cuda_stream)
+def _ws_key(device, stream):
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    s = torch.cuda.current_stream(device) if stream is None else stream
+    return device, (device.index, s.cuda_stream)
+
+
+def prepare_workspace(device=None, stream=None):
+    """Create (and zero-fill, by a fill kernel on that stream) the GEMM workspace of `stream` (default: torch's
+    current stream) on `device`, if it does not exist yet, and return it. Call it on a capture stream before
+    capturing: the fill must not be recorded into a graph."""
+    device, key = _ws_key(device, stream)
     w = _workspaces.get(key)
     if w is None:
-        w = torch.zeros(lib().lfm2q_gemm_workspace_bytes(), dtype=torch.uint8, device=t.device)
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("lfm2q: the GEMM workspace of this stream does not exist yet and the stream is being "
+                               "captured; call lfm2opt.kernels.prepare_workspace() on the capture stream before the "
+                               "capture (its zero fill must stay out of the graph)")
+        s = torch.cuda.current_stream(device) if stream is None else stream
+        with torch.cuda.stream(s):
+            w = torch.zeros(lib().lfm2q_gemm_workspace_bytes(), dtype=torch.uint8, device=device)
         _workspaces[key] = w
     return w
+
+
+def release_workspace(device=None, stream=None):
+    """Drop the GEMM workspace of `stream` on `device` (its memory returns to torch's allocator once no other
+    reference remains). Only when no call on that stream is in flight and no captured graph that used it will be
+    replayed again: such a graph keeps the workspace's address. Returns whether there was one."""
+    _, key = _ws_key(device, stream)
+    return _workspaces.pop(key, None) is not None
+
+
+def workspace(t):
+    """The GEMM workspace of torch's current stream on t's device: lfm2q_gemm_workspace_bytes() of device memory
+    (arrival counters for the K split across workgroups, then the partial tiles), zero-filled when first used and
+    kept until release_workspace(). Calls on one stream are ordered, so they share it; another stream gets its own
+    (so a caller that makes a stream per request should release it afterwards). A graph captured on a stream uses
+    that stream's workspace, so graphs captured on one stream must not be replayed concurrently with each other.
+    Inside a capture the stream's workspace must already exist (an eager call on that stream, or
+    prepare_workspace()): otherwise this raises, since a zero fill recorded into one graph would leave the counters
+    undefined for every later graph and eager call that shares the buffer."""
+    return prepare_workspace(t.device)

@@ -14,6 +14,11 @@ import torch
 
 from . import _capi
 
+# The per-stream GEMM workspace (the K split across workgroups): create it on a capture stream before capturing,
+# release it when a stream is retired.
+prepare_workspace = _capi.prepare_workspace
+release_workspace = _capi.release_workspace
+
 _EXT = None
 
 
@@ -243,9 +248,11 @@ class GemvChain:
                        self.ws.data_ptr(), self.ws_bytes, torch.cuda.current_stream(self.device).cuda_stream)
 
     def wait_expired(self):
-        """True if a dependency wait of a launch on this chain ran out (its outputs are then undefined). Reads the
-        workspace's error word on the host (synchronizes)."""
-        return int(self.ws[1].item()) != 0
+        """True if a dependency wait of the last launch on this chain ran out (its outputs are then undefined; the
+        launches after it are not affected). Reads the workspace's launch count and error tag on the host
+        (synchronizes)."""
+        gen, tag = (int(v) for v in self.ws[:2].tolist())
+        return gen != 0 and tag == gen
 
 
 class Int8Ops:

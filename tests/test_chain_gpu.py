@@ -191,6 +191,40 @@ def test_chain_graph_replays(E):
     assert not chain.wait_expired()
 
 
+def test_chain_expired_wait_is_not_sticky(E, tune):
+    """A launch whose dependency waits run out (forced from the host: a wait bound of 0 ms) reports it, and the next
+    launch on the same workspace, with the normal bound, is not cut short by that error: its outputs equal the
+    separate calls bit for bit and it reports no expired wait."""
+    from lfm2opt import _capi
+
+    g = torch.Generator(device="cuda").manual_seed(9)
+    types = "AC"
+    weights = make_weights(g, types, vocab=8192)
+    a = Step(g, 2, vocab=8192)
+    b = Step(torch.Generator(device="cuda").manual_seed(10), 2, vocab=8192)
+    h0 = a.h.clone()
+    b.h.copy_(h0)
+    ops_a, ops_b = step_ops(weights, a, types), step_ops(weights, b, types)
+    chain = E.gemv_chain(ops_b)
+    tune("LFM2Q_CHAIN_WAIT_MS", 0)
+    expired = False
+    for _ in range(5):
+        chain()
+        torch.cuda.synchronize()
+        if chain.wait_expired():
+            expired = True
+            break
+    assert expired, "no wait ran out with a 0 ms bound"
+    _capi.set_tuning("LFM2Q_CHAIN_WAIT_MS", None)
+    b.h.copy_(h0)
+    run_separately(E, ops_a)
+    chain()
+    torch.cuda.synchronize()
+    assert not chain.wait_expired()
+    for u, v in zip(a.bufs(), b.bufs()):
+        assert same_bits(u, v), "the launch after an expired one differs from the separate calls"
+
+
 def test_chain_argument_errors(E):
     W = torch.zeros(64, 1024, device="cuda", dtype=torch.int8)
     s = torch.ones(64, device="cuda")

@@ -83,12 +83,16 @@ def _snapshot(out):
 
 
 def test_graph_replays_match_eager(cuda):
+    from lfm2opt.kernels import prepare_workspace
+
     run, out, inp = _ops(1)
     h0 = inp["h"].clone()
     run()  # warm-up outside the capture (library load, first-call setup)
+    cap = torch.cuda.Stream()
+    prepare_workspace(stream=cap)  # the capture stream's GEMM workspace, zero-filled outside the graph
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=cap):
         run()
     g = torch.Generator(device="cuda").manual_seed(7)
     for rep in range(3):
@@ -131,3 +135,71 @@ def test_two_streams_match_serial(cuda):
     for i, (_, out, _) in enumerate(runs):
         for k, v in out.items():
             assert torch.equal(v, serial[i][k]), f"stream {i}: {k} differs from the serial run"
+
+
+def test_capture_without_workspace_raises(cuda):
+    """A GEMM that needs its stream's workspace inside a capture, before the workspace exists, raises: the zero fill
+    would otherwise exist only in that graph and leave the K-split counters undefined for the next user."""
+    from lfm2opt.kernels import int8_ext, release_workspace
+
+    E8 = int8_ext()
+    xq = torch.ones(64, 2048, device="cuda", dtype=torch.int8)
+    sx = torch.ones(64, device="cuda")
+    wq = torch.ones(3072, 2048, device="cuda", dtype=torch.int8)
+    sw = torch.ones(3072, device="cuda")
+    y = torch.empty(64, 3072, device="cuda", dtype=torch.bfloat16)
+    cap = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="prepare_workspace"):
+        with torch.cuda.graph(graph, stream=cap):
+            E8.gemm_i8(xq, sx, wq, sw, None, y, False)
+    torch.cuda.synchronize()
+    assert not release_workspace(stream=cap)  # nothing was created for it
+
+
+def test_two_graphs_on_one_capture_stream(cuda):
+    """Two graphs captured on one stream share its workspace: replaying the second one first, then the first, then
+    eager calls on that stream all reproduce the eager results, K split included (64 tokens: 24 tiles)."""
+    from lfm2opt.kernels import int8_ext, prepare_workspace, release_workspace
+
+    E8 = int8_ext()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    wq = torch.randint(-127, 128, (3072, 2048), device="cuda", dtype=torch.int8, generator=g)
+    sw = torch.rand(3072, device="cuda", generator=g) * 0.01
+    xs = [torch.randn(64, 2048, device="cuda", generator=g).to(torch.bfloat16) for _ in range(2)]
+    qs = [(torch.empty(64, 2048, device="cuda", dtype=torch.int8), torch.empty(64, device="cuda")) for _ in xs]
+    ys = [torch.empty(64, 3072, device="cuda", dtype=torch.bfloat16) for _ in xs]
+
+    def call(i):
+        E8.quant_rows(xs[i], *qs[i])
+        E8.gemm_i8(qs[i][0], qs[i][1], wq, sw, None, ys[i], False)
+
+    for i in range(2):
+        call(i)
+    torch.cuda.synchronize()
+    eager = [y.clone() for y in ys]
+    cap = torch.cuda.Stream()
+    prepare_workspace(stream=cap)
+    torch.cuda.synchronize()
+    graphs = [torch.cuda.CUDAGraph() for _ in range(2)]
+    for i in range(2):
+        with torch.cuda.graph(graphs[i], stream=cap):
+            call(i)
+    for rep in range(3):
+        for y in ys:
+            y.fill_(0)
+        torch.cuda.synchronize()
+        graphs[1].replay()
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(ys[i], eager[i]), f"rep {rep}: graph {i} differs from the eager call"
+        with torch.cuda.stream(cap):
+            for i in range(2):
+                call(i)
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(ys[i], eager[i]), f"rep {rep}: eager call {i} on the capture stream differs"
+    del graphs
+    torch.cuda.synchronize()
+    assert release_workspace(stream=cap)
