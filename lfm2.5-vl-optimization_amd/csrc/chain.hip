@@ -285,6 +285,10 @@ __device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target,
         poll(b);
         for (int it = 0;; ++it) {
             if (all_reached(a, lane, G, target)) break;
+            if (wait_ticks == 0) {  // a zero bound: a dependency not met at the first poll has run out
+                if (lane == 0) st_word(ws + WS_ERR, tag);
+                break;
+            }
             poll(a);
             if (all_reached(b, lane, G, target)) break;
             poll(b);
@@ -301,7 +305,7 @@ __device__ __forceinline__ void wait_flags(uint32_t *ws, int G, uint32_t target,
             bool ok = true;
             for (int i = lane; i < G; i += 64) ok = ok && (int)(ld_word(flags + i) - target) >= 0;
             if (__builtin_amdgcn_ballot_w64(!ok) == 0 || ld_word(ws + WS_ERR) == tag) break;
-            if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) {
+            if (wait_ticks == 0 || __builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) {
                 if (lane == 0) st_word(ws + WS_ERR, tag);
                 break;
             }

@@ -41,7 +41,7 @@ enum Knob {
     KNOB_GEMM_RING,     // 256 x 256 one-workgroup-per-tile ring shape (1282, 644, 645)
     KNOB_GEMM_STAGES,   // LDS ring depth (3, 6; 2 for the persistent kernels)
     KNOB_GEMM_SPLITK,   // per-token W8A8 with a workspace: K slices over workgroups (1 = none, 2..8)
-    KNOB_CHAIN_WAIT_MS, // GEMV chain: bound of each dependency wait in milliseconds (default 20; 0 = at once)
+    KNOB_CHAIN_WAIT_MS, // GEMV chain: bound of each dependency wait in milliseconds (default 20; 0: at once)
     KNOB_COUNT
 };
 struct KnobVal {
