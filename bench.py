@@ -341,6 +341,7 @@ def decode_results(B, steps, warmup, wfmt="int8"):
     log(f"decode step ({wfmt}), batch {B}: {ms * 1e3:.1f} us/step, {res['gbs']:.0f} GB/s")
     if wfmt == "int8" and B == 1:
         res["chain"] = chain_results(step, steps, warmup)
+        res["bandwidth_roof"] = bandwidth_roof(step)
     del graph, step
     torch.cuda.empty_cache()
     return res
@@ -729,7 +730,8 @@ def producer_results(reps):
         s = torch.empty((L // 64, rows) if grouped else (rows,), device=dev)
         return lambda: E.quant_rows(x, q, s)
 
-    for rows, L, grouped in ((4096, 2048, False), (4096, 2048, True), (10240, 1152, False), (4096, 8192, True)):
+    for rows, L, grouped in ((512, 8192, False), (4096, 2048, False), (4096, 2048, True), (10240, 1152, False),
+                             (4096, 8192, True)):
         ns = (L // 64) * rows if grouped else rows
         run("quant_groups" if grouped else "quant_rows", rows, L, lambda: quant(rows, L, grouped),
             3 * rows * L + 4 * ns)
@@ -765,6 +767,43 @@ def producer_results(reps):
         return lambda: E.silu_mul_q(gg, q, s)
 
     run("silu_mul_q", 4096, 8192, lambda: silu_q(4096, 8192), 5 * 4096 * 8192 + 4 * 4096)
+    return res
+
+
+def quant_sweep(reps):
+    """quant_rows / grouped quant_rows on the W8A8 workload's activation shapes under both launch forms (a wavefront
+    per row, LFM2Q_QUANT_WG=0; a workgroup per row, =1) and the automatic choice, timed as producer_results times
+    them (rotating copies, one graph): which form each shape should take."""
+    from lfm2opt import _capi
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    dev, bf = "cuda", torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(3)
+    res = []
+    shapes = sorted({(M, K) for M, K, _, _, _, _ in W8A8_SHAPES})
+    for M, K in shapes:
+        for grouped in ((False, True) if K % 64 == 0 else (False,)):
+            nbytes = 3 * M * K + 4 * ((K // 64) * M if grouped else M)
+            ncopy = max(4, -(-512 * 2 ** 20 // nbytes))
+            xs = [torch.randn(M, K, device=dev, generator=g).to(bf) for _ in range(ncopy)]
+            qs = [torch.empty(M, K, device=dev, dtype=torch.int8) for _ in range(ncopy)]
+            ss = [torch.empty((K // 64, M) if grouped else (M,), device=dev) for _ in range(ncopy)]
+            row = {"rows": M, "len": K, "grouped": grouped}
+            for name, val in (("wave", 0), ("wg", 1), ("auto", None)):
+                _capi.set_tuning("LFM2Q_QUANT_WG", val)
+                gr = capture(lambda: [E.quant_rows(x, q, sc) for x, q, sc in zip(xs, qs, ss)])
+                t, _ = time_graph(gr, reps, 2)
+                us = t * 1e3 / ncopy
+                row[f"us_{name}"] = round(us, 2)
+                row[f"gbs_{name}"] = round(nbytes / us / 1e3, 1)
+                del gr
+            _capi.set_tuning("LFM2Q_QUANT_WG", None)
+            res.append(row)
+            log(f"quant {M}x{K}{' grouped' if grouped else ''}: wave {row['us_wave']} us, wg {row['us_wg']} us, "
+                f"auto {row['us_auto']} us")
+            del xs, qs, ss
+            torch.cuda.empty_cache()
     return res
 
 
@@ -829,13 +868,137 @@ def gemm_sweep(reps):
             "us_best_total": round(sum(r["us_best"] for r in out), 1)}
 
 
+_calib = None
+
+
+def calib_lib():
+    """lib/liblfm2q_calib.so: the calibration kernels (measurement equipment, not the product)."""
+    global _calib
+    if _calib is None:
+        L = ctypes.CDLL(str(ROOT / "lfm2.5-vl-optimization_amd" / "lib" / "liblfm2q_calib.so"))
+        L.lfm2q_calib_mfma_i8.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
+                                          ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        L.lfm2q_calib_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_void_p]
+        _calib = L
+    return _calib
+
+
+def stream_read(buf, nbytes, out, per_lane, aux=2):
+    """One bare read of buf's first nbytes (calib stream_read_kernel) on torch's current stream."""
+    st = calib_lib().lfm2q_calib_stream_read(buf.data_ptr(), nbytes, out.data_ptr(), per_lane, aux,
+                                             torch.cuda.current_stream().cuda_stream)
+    assert st == 0, st
+
+
+def bandwidth_roof(step, reps=10):
+    """The measured bandwidth roof of the decode GEMVs (the reference measured its practical DRAM roof with a 2 GB
+    sum, docs/experiment_log.md:949). Kernels that only read (calib stream_read_kernel, 16-byte loads, 1-16 in
+    flight per lane), replayed from HIP graphs:
+      * `sizes`: one buffer of 4 MiB .. 1 GiB per launch, launches cycling over distinct buffers of at least 1 GiB in
+        all (so no read comes from the 256 MB memory-side cache), best of the loads-per-lane settings, non-temporal
+        loads (how the GEMVs read) and, at 1 GiB, cached loads too;
+      * `step_graph`: one bare read per weight matrix of the INT8 decode step (the same 65 buffers, in step order,
+        one launch each): what a graph of 65 kernels can reach with no arithmetic at all;
+      * `node_floor_us`: a graph of 65 launches of one 16-byte read each: the per-node cost of a graph kernel.
+    `measured_roof_gbs` is the best 1 GiB figure."""
+    dev = "cuda"
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    MiB = 1 << 20
+    pool = torch.empty(2048 * MiB, dtype=torch.uint8, device=dev)
+    res = {"sizes": {}}
+    for size_mib in (4, 16, 32, 128, 1024):
+        nb = max(2, 1024 // size_mib)
+        nbytes = size_mib * MiB
+        bufs = [pool[i * nbytes:(i + 1) * nbytes] for i in range(nb)]
+        row = {}
+        for aux in ((2, 0) if size_mib == 1024 else (2,)):
+            for per_lane in (1, 4, 8, 16):
+                g = capture(lambda: [stream_read(b, nbytes, out, per_lane, aux) for b in bufs])
+                ms, _ = time_graph(g, reps, 2)
+                row[f"{'nt' if aux == 2 else 'cached'}_u{per_lane}"] = round(nbytes * nb / ms / 1e6, 1)
+                del g
+        best = max(row.values())
+        res["sizes"][f"{size_mib}MiB"] = {"best_gbs": best, "us_per_launch": round(nbytes / best / 1e3, 2),
+                                          "launches_per_graph": nb, **row}
+        log(f"bare reads {size_mib} MiB: {best:.0f} GB/s")
+    del pool
+    torch.cuda.empty_cache()
+    wts = [w for w in step.weights if w.dtype == torch.int8]
+    wbytes = sum(w.numel() for w in wts)
+    sg = {}
+    for per_lane in (1, 8):
+        g = capture(lambda: [stream_read(w, w.numel(), out, per_lane) for w in wts])
+        ms, _ = time_graph(g, reps * 2, 3)
+        sg[f"nt_u{per_lane}"] = {"us_per_step": round(ms * 1e3, 1), "gbs": round(wbytes / ms / 1e6, 1)}
+        del g
+    best = min(sg.values(), key=lambda r: r["us_per_step"])
+    res["step_graph"] = {"launches": len(wts), "weight_bytes": wbytes, "best_us_per_step": best["us_per_step"],
+                         "best_gbs": best["gbs"], **sg}
+    log(f"bare reads of the decode step's 65 weight matrices: {best['us_per_step']} us, {best['gbs']:.0f} GB/s")
+    g = capture(lambda: [stream_read(wts[0], 16, out, 1) for _ in wts])
+    ms, _ = time_graph(g, reps * 4, 3)
+    res["node_floor_us"] = round(ms * 1e3 / len(wts), 2)
+    del g
+    res["measured_roof_gbs"] = res["sizes"]["1024MiB"]["best_gbs"]
+    return res
+
+
+def read_branch_experiment(step, reps=40):
+    """Staging the next weights through the memory-side cache on a concurrent branch, measured (the reference's
+    programmatic dependent launch prefetches the next GEMV's weights before its dependency wait,
+    kernels/lfm2_decode.cu:24-62): the INT8 batch-1 step's graph against the same graph with a second captured
+    stream that reads weight matrix k (bare read kernel) once GEMV k - d has finished -- one cross-stream edge per
+    GEMV, at most d matrices ahead -- and against a cached read of matrix i + 1 before each GEMV i on one stream."""
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    wts = [w for w in step.weights if w.dtype == torch.int8]
+    fns = [fn for _, fn, _ in step.ops]
+    res = {}
+
+    def t(fn):
+        g = capture(fn)
+        ms, _ = time_graph(g, reps, 5)
+        del g
+        return round(ms * 1e3, 1)
+
+    def branched(d, u, aux):
+        main, side = torch.cuda.current_stream(), torch.cuda.Stream()
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for k in range(min(d, len(wts))):
+                stream_read(wts[k], wts[k].numel(), out, u, aux)
+        for i, fn in enumerate(fns):
+            fn()
+            if i + d < len(wts):
+                ev = torch.cuda.Event()
+                ev.record(main)
+                side.wait_event(ev)
+                with torch.cuda.stream(side):
+                    stream_read(wts[i + d], wts[i + d].numel(), out, u, aux)
+        main.wait_stream(side)
+
+    def serial_next(u, aux):
+        for i, fn in enumerate(fns):
+            if i + 1 < len(wts):
+                stream_read(wts[i + 1], wts[i + 1].numel(), out, u, aux)
+            fn()
+
+    res["step_us"] = t(step.run)
+    for d in (1, 2, 3, 5):
+        for u, aux in ((1, 0), (8, 0), (1, 2)):
+            res[f"branch_d{d}_u{u}_{'cached' if aux == 0 else 'nt'}_us"] = t(lambda: branched(d, u, aux))
+    res["serial_next_cached_us"] = t(lambda: serial_next(1, 0))
+    res["reads_only_cached_us"] = t(lambda: [stream_read(w, w.numel(), out, 1, 0) for w in wts])
+    log(f"read branch: step {res['step_us']} us, branched {min(v for k, v in res.items() if k.startswith('branch'))}"
+        f" us at best, serial next-read {res['serial_next_cached_us']} us")
+    return res
+
+
 def mfma_rate(iters=20000):
     """The int8 matrix-core rate the chip sustains (lib/liblfm2q_calib.so: every SIMD issuing nothing but
     independent v_mfma_i32_32x32x32_i8, two wavefronts per SIMD) on random and on all-zero operand bytes, with the
     shader clock measured during the run (s_memtime against the 100 MHz s_memrealtime)."""
-    L = ctypes.CDLL(str(ROOT / "lfm2.5-vl-optimization_amd" / "lib" / "liblfm2q_calib.so"))
-    L.lfm2q_calib_mfma_i8.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
-                                      ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    L = calib_lib()
     blocks = 2 * torch.cuda.get_device_properties(0).multi_processor_count
     waves = 4 * blocks
     g = torch.Generator(device="cuda").manual_seed(7)
@@ -897,6 +1060,11 @@ def main():
                          "eagerly, for counter collection")
     ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
     ap.add_argument("--mfma-rate", action="store_true", help="only the sustained int8 matrix-core rate calibration")
+    ap.add_argument("--bw-roof", action="store_true", help="only the bare-read bandwidth roof")
+    ap.add_argument("--quant-sweep", action="store_true",
+                    help="only the activation quantizers under both launch forms on the W8A8 shapes")
+    ap.add_argument("--read-branch", action="store_true",
+                    help="only the decode step with a concurrent weight-read branch (memory-side-cache staging)")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the per-token W8A8 GEMM under every forced (tile, K split) on the 13 shapes")
     args = ap.parse_args()
@@ -913,6 +1081,16 @@ def main():
         return
     if args.mfma_rate:
         print(json.dumps({"mfma_sustained": mfma_rate()}))
+        return
+    if args.quant_sweep:
+        print(json.dumps({"quant_sweep": quant_sweep(max(5, args.steps // 10))}))
+        return
+    if args.read_branch:
+        print(json.dumps({"read_branch": read_branch_experiment(DecodeStep(1, "cuda"))}))
+        return
+    if args.bw_roof:
+        step = DecodeStep(1, "cuda")
+        print(json.dumps({"bandwidth_roof": bandwidth_roof(step, max(5, args.steps // 20))}))
         return
     if args.only_w8a8:
         print(json.dumps({"w8a8_shapes": w8a8_results(max(5, args.steps // 10))}))
@@ -962,6 +1140,15 @@ def main():
                      "us_per_launch": dom["us_per_launch"], "bytes_per_launch": dom["bytes_per_launch"]},
         "decode": {str(B): r for B, r in [(batches[0], res1)] + list(extra.items())},
     }
+    roof = res1.get("bandwidth_roof")
+    if roof:
+        # the chip's measured streaming roof (bare 1 GiB reads) beside the 8 TB/s datasheet peak, and the step against
+        # a graph of bare reads over its own 65 weight matrices
+        out["roofline"]["measured_roof"] = roof["measured_roof_gbs"]
+        out["roofline"]["frac_of_measured_roof"] = round(dom["gbs"] / roof["measured_roof_gbs"], 4)
+        out["measured_roof_gbs"] = roof["measured_roof_gbs"]
+        out["step_vs_bare_read_graph"] = round(roof["step_graph"]["best_us_per_step"] / (res1["ms_per_step"] * 1e3),
+                                               4)
     log("single GEMV 8192 x 2048")
     out["single_gemv"] = single_gemv_results(max(20, args.steps // 2), cpu=not args.no_cpu)
     w4b = [int(b) for b in args.w4_batches.split(",") if b]

@@ -100,6 +100,60 @@ __global__ __launch_bounds__(256) void quant_kernel(const uint16_t *__restrict__
     }
 }
 
+// One row per workgroup of 4 wavefronts, for the shapes where one wavefront per row leaves the CUs short of
+// wavefronts (few rows) or makes each one long (K up to 8192: 16 vectors per lane, ~1300 VALU instructions of
+// quantization per wavefront): thread t (0 .. 255) holds the vectors c 256 + t (c < CH) of the row. Per-row scales
+// take the wavefronts' maxima through LDS (a maximum does not depend on the order it is taken in); a grouped scale
+// covers 8 consecutive vectors, i.e. 8 consecutive lanes of one wavefront, as in quant_kernel. Each value is quantized
+// by the same quant8 with the same scale and reciprocal, so the bytes and scales equal quant_kernel's.
+template <int CH, bool GROUPED>
+__global__ __launch_bounds__(256) void quant_row_wg_kernel(const uint16_t *__restrict__ x, int8_t *__restrict__ q,
+                                                           float *__restrict__ s, int rows, int K) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int row = blockIdx.x;
+    const uint16_t *xr = x + (size_t)row * K;
+    int8_t *qr = q + (size_t)row * K;
+    const int C = K / 8;
+    v4i v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 256 + t;
+        v[c] = i < C ? ld_nt16(xr + (size_t)i * 8) : v4i{0, 0, 0, 0};
+    }
+    float sc_row = 0.f, rc_row = 0.f;
+    if (!GROUPED) {
+        __shared__ float wmax[4];
+        float m = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) m = absmax8(v[c], m);
+        m = wave_max(m);
+        if (lane == 0) wmax[wave] = m;
+        __syncthreads();
+        sc_row = scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+        rc_row = 1.f / sc_row;
+        if (t == 0) s[row] = sc_row;
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 256 + t;
+        float sc = sc_row, rc = rc_row;
+        if (GROUPED) {
+            float m = absmax8(v[c], 0.f);
+            m = fmaxf(m, __shfl_xor(m, 1));
+            m = fmaxf(m, __shfl_xor(m, 2));
+            m = fmaxf(m, __shfl_xor(m, 4));
+            sc = scale_of(m);
+            rc = 1.f / sc;
+            if (i < C && (t & 7) == 0) s[(size_t)(i >> 3) * rows + row] = sc;
+        }
+        if (i < C) {
+            int lo, hi;
+            quant8(v[c], sc, rc, lo, hi);
+            *reinterpret_cast<int2 *>(qr + (size_t)i * 8) = make_int2(lo, hi);
+        }
+    }
+}
+
 // Per-row scales only, s = max(amax, 1e-8) / 127 -- the s of quant_rows (a maximum does not depend on the order it
 // is taken in): the first pass of the bf16-activation GEMM, which quantizes the rows itself with these scales.
 __global__ __launch_bounds__(256) void row_scale_kernel(const uint16_t *__restrict__ x, float *__restrict__ s, int rows,
@@ -301,6 +355,40 @@ __global__ __launch_bounds__(256) void silu_mul_q_kernel(const uint16_t *__restr
         default: CALL(16); break;                                                                                    \
     }
 
+// quant_rows / quant_groups launch: a workgroup per row (quant_row_wg_kernel) or a wavefront per row (quant_kernel).
+// Knob LFM2Q_QUANT_WG: 1 / 0 forces one or the other. Default, from MI355X timings of both forms on the W8A8
+// workload's activations (bench.py --quant-sweep): a workgroup per row from K = 4096 (512 x 8192 12.6 -> 6.4 us,
+// 4096 x 8192 31.7 -> 20.6 us, 10240 x 4304 31.2 -> 27.9 us), and from K = 2048 with grouped scales or at most
+// 8 rows per CU (512 x 2048 4.6 -> 3.3 us); a wavefront per row for the short vision rows (10240 x 1152: 10.9 against
+// 14.3 us, half of a workgroup's threads would hold no vector) and for many per-token rows of 2048.
+inline bool wg_rows(int rows, int K, bool grouped) {
+    const int f = knob_int(KNOB_QUANT_WG, -1);
+    if (K > 8192) return false;
+    if (f >= 0) return f != 0;
+    return K >= 4096 || (K >= 2048 && (grouped || rows <= 8 * device_cus()));
+}
+
+template <bool GROUPED>
+void launch_quant(const uint16_t *x, int8_t *q, float *s, int rows, int K, hipStream_t st) {
+    if (wg_rows(rows, K, GROUPED)) {
+        const int C = K / 8;
+        switch ((C + 255) / 256) {
+            case 1: quant_row_wg_kernel<1, GROUPED><<<rows, 256, 0, st>>>(x, q, s, rows, K); break;
+            case 2: quant_row_wg_kernel<2, GROUPED><<<rows, 256, 0, st>>>(x, q, s, rows, K); break;
+            case 3: quant_row_wg_kernel<3, GROUPED><<<rows, 256, 0, st>>>(x, q, s, rows, K); break;
+            default: quant_row_wg_kernel<4, GROUPED><<<rows, 256, 0, st>>>(x, q, s, rows, K); break;
+        }
+        return;
+    }
+    const dim3 grid((rows + 3) / 4);
+#define LFM2Q_Q(CH_) quant_kernel<CH_, GROUPED><<<grid, 256, 0, st>>>(x, q, s, rows, K)
+    if (K > 8192)
+        LFM2Q_Q(0);
+    else
+        LFM2Q_CH_SWITCH(K, LFM2Q_Q)
+#undef LFM2Q_Q
+}
+
 int check_rows(const char *name, int rows, int len, int grouped, int maxlen) {
     LFM2Q_REQUIRE(rows >= 1 && len >= 8, LFM2Q_ERR_SHAPE, "%s: need rows >= 1 and a row length >= 8 (rows=%d, %d)",
                   name, rows, len);
@@ -327,14 +415,7 @@ extern "C" int lfm2q_quant_rows(const lfm2q_bf16 *x, int8_t *q, float *s, int ro
                   "quant_rows: K must be a multiple of 8 (rows=%d K=%d)", rows, K);
     LFM2Q_REQUIRE(aligned16(x) && ((uintptr_t)q & 7) == 0, LFM2Q_ERR_ALIGN,
                   "quant_rows: x must be 16-byte and q 8-byte aligned");
-    const dim3 grid((rows + 3) / 4);
-    const hipStream_t st = (hipStream_t)stream;
-#define LFM2Q_Q(CH_) quant_kernel<CH_, false><<<grid, 256, 0, st>>>(x, q, s, rows, K)
-    if (K > 8192)
-        LFM2Q_Q(0);
-    else
-        LFM2Q_CH_SWITCH(K, LFM2Q_Q)
-#undef LFM2Q_Q
+    launch_quant<false>(x, q, s, rows, K, (hipStream_t)stream);
     return launch_status("quant_rows");
 }
 
@@ -344,14 +425,7 @@ extern "C" int lfm2q_quant_groups(const lfm2q_bf16 *x, int8_t *q, float *sT, int
                   "quant_groups: K must be a multiple of 64 (rows=%d K=%d)", rows, K);
     LFM2Q_REQUIRE(aligned16(x) && ((uintptr_t)q & 7) == 0, LFM2Q_ERR_ALIGN,
                   "quant_groups: x must be 16-byte and q 8-byte aligned");
-    const dim3 grid((rows + 3) / 4);
-    const hipStream_t st = (hipStream_t)stream;
-#define LFM2Q_Q(CH_) quant_kernel<CH_, true><<<grid, 256, 0, st>>>(x, q, sT, rows, K)
-    if (K > 8192)
-        LFM2Q_Q(0);
-    else
-        LFM2Q_CH_SWITCH(K, LFM2Q_Q)
-#undef LFM2Q_Q
+    launch_quant<true>(x, q, sT, rows, K, (hipStream_t)stream);
     return launch_status("quant_groups");
 }
 

@@ -42,6 +42,7 @@ enum Knob {
     KNOB_GEMM_STAGES,   // LDS ring depth (3, 6; 2 for the persistent kernels)
     KNOB_GEMM_SPLITK,   // per-token W8A8 with a workspace: K slices over workgroups (1 = none, 2..8)
     KNOB_CHAIN_WAIT_MS, // GEMV chain: bound of each dependency wait in milliseconds (default 20; 0: at once)
+    KNOB_QUANT_WG,      // quant_rows / quant_groups: 1 a workgroup per row, 0 a wavefront per row
     KNOB_COUNT
 };
 struct KnobVal {

@@ -60,6 +60,36 @@ def test_quant_rows_vs_oracle(E, M, K):
     assert np.array_equal(q.cpu().numpy(), rq)
 
 
+@pytest.mark.parametrize("wg", [0, 1])
+@pytest.mark.parametrize("M,K", [(512, 8192), (512, 2048), (777, 4304), (3, 1024), (2048, 6144), (10240, 1152)])
+def test_quant_both_kernels_vs_oracle(E, tune, wg, M, K):
+    """quant_rows and grouped quant_rows on each of the two launch forms (a wavefront per row, LFM2Q_QUANT_WG=0, and
+    a workgroup per row, =1): q and s bit-exact against the oracle, 0.1% outliers at 20 sigma, K with a partial last
+    vector round (4304 = 538 vectors over 256 threads), the golden division traps in row 0."""
+    tune("LFM2Q_QUANT_WG", wg)
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g)
+    out = torch.rand(M, K, generator=g) < 1e-3
+    x[out] = 20.0 * torch.sign(torch.randn(int(out.sum()), generator=g))
+    xb = x.to(torch.bfloat16)
+    bits = xb.view(torch.int16).numpy().view(np.uint16).copy()
+    traps = load("quant_rows_traps_k64")["x"][0]
+    bits[0, :traps.size] = traps
+    xd = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda()
+    q = torch.empty(M, K, device="cuda", dtype=torch.int8)
+    s = torch.empty(M, device="cuda", dtype=torch.float32)
+    E.quant_rows(xd, q, s)
+    rq, rs = oracle.quant_rows(bits)
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(q.cpu().numpy(), rq)
+    if K % 64 == 0:
+        sT = torch.empty(K // 64, M, device="cuda", dtype=torch.float32)
+        E.quant_rows(xd, q, sT)
+        gq, gs = oracle.quant_groups(bits)
+        assert np.array_equal(sT.cpu().numpy(), gs)
+        assert np.array_equal(q.cpu().numpy(), gq)
+
+
 # ------------------------------------------------------------------------------------------------ fixtures
 @pytest.mark.parametrize("name", ["gemm_i8_m37_k320_n24_bias", "gemm_i8_m70_k1152_n100",
                                   "gemm_i8_m33_k576_n40_bias_gelu", "gemm_i8_m129_k4304_n72_bias"])
