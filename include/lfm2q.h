@@ -85,6 +85,17 @@ int lfm2q_gemv_swiglu(int wtype, const void *W, const float *scale, const lfm2q_
 int lfm2q_gemv_residual(int wtype, const void *W, const float *scale, const lfm2q_bf16 *x, lfm2q_bf16 *h, int B,
                         int N, int K, lfm2q_stream_t stream);
 
+/* Batch-1 GEMV of an RMS-normalized row: x = bf16(norm_w * bf16(h * rs)), rs = 1 / sqrt(mean(h^2) + eps), computed
+ * inside the GEMV, then y = x W^T s (epi 0, y bf16 [1, N]) or the SwiGLU of x over W = w1|w3 [2N, K] (epi 1,
+ * y [1, N]). h and norm_w bf16 [K]; h is read, not written. Bit-identical to lfm2q_add_rmsnorm_q with no residual
+ * input (its bf16 x) followed by lfm2q_gemv_w8 / lfm2q_gemv_swiglu (wtype 0: int8 W with fp32 scale, K in {1024,
+ * 2048, 4096, 8192}; wtype 1: bf16 W, scale optional, K in {512, 1024, 2048, 4096}). Replaces the pair the
+ * reference's decode step runs before every qkv / in_proj / w1|w3 / lm_head linear: add_rmsnorm
+ * (kernels/lfm2_decode.cpp:33-38, kernel kernels/lfm2_decode.cu:96-121) then gemv / gemv_epi(0)
+ * (kernels/lfm2_decode.cpp:74-85, :130-150), at the call sites src/lfm2opt/runtime.py:251-255, :276-281, :284-285. */
+int lfm2q_gemv_rmsnorm(int wtype, int epi, const void *W, const float *scale, const lfm2q_bf16 *h,
+                       const lfm2q_bf16 *norm_w, float eps, lfm2q_bf16 *y, int N, int K, lfm2q_stream_t stream);
+
 /* Weight-only INT4 GEMV with group-wise scales and zero points: acc[b, n] = sum_k s[n, k/group] (q[n, k] - z[n,
  * k/group]) x[b, k] in fp32, y[b, n] = bf16(acc[b, n]) (epi 0), the SwiGLU pair of W = w1|w3 [2N, K] (epi 1, same
  * roundings as lfm2q_gemv_swiglu with the scales folded into acc) or h[b, n] = bf16(h[b, n] + bf16(acc[b, n]))

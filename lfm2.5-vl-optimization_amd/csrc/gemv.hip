@@ -24,6 +24,7 @@
 // gemv_dispatch :667-706), kernels/lfm2_decode.cu:954-963 (silu_mul), :108-113 (residual rounding).
 #include "common.hpp"
 #include "gemv_math.hpp"
+#include "rmsnorm.hpp"
 #include "status.hpp"
 
 #include <algorithm>
@@ -35,15 +36,74 @@ namespace lfm2q {
 namespace {
 
 // ------------------------------------------------------------------------------------------------ batch 1
+// A batch-1 kernel's activations: lane l holds the XL vectors of 8 bf16 that chunk l + 64 u (u < CPL) multiplies,
+// i.e. vectors XL (l + 64 u) + q. NORM: x is the RMSNorm of the row h with weight nw, computed here exactly as
+// add_rmsnorm_q computes it (rmsnorm.hpp), so the GEMV of the normalized row equals add_rmsnorm_q followed by the
+// GEMV bit for bit: the sum of squares is taken in add_rmsnorm_q's order -- lane l sums vectors c 64 + l, c < CH =
+// CPL XL -- by fetching those vectors from the lanes that hold them (for XL = 2 vector c 64 + l is register
+// [c / 2][l % 2] of lane 32 (c % 2) + l / 2; for XL = 1 the two layouts coincide), then x = bf16(w bf16(h rs))
+// elementwise in the kernel's own layout. Needs K = 64 PER CPL exactly (every vector in range).
+template <int PER, int XL, int CPL, bool NORM>
+struct XLoadB1 {
+    v4i hv[CPL][XL], wv[CPL][XL];
+    // NORM: the row and the norm weight, in flight before the caller issues its weight loads
+    __device__ __forceinline__ void issue(const uint16_t *__restrict__ x, const uint16_t *__restrict__ nw, int lane) {
+        if constexpr (NORM) {
+#pragma unroll
+            for (int u = 0; u < CPL; ++u)
+#pragma unroll
+                for (int q = 0; q < XL; ++q) {
+                    hv[u][q] = ld16(x + (size_t)(lane + 64 * u) * PER + 8 * q);
+                    wv[u][q] = ld16(nw + (size_t)(lane + 64 * u) * PER + 8 * q);
+                }
+        }
+    }
+    __device__ __forceinline__ void finish(const uint16_t *__restrict__ x, float eps, int K, int lane,
+                                           v4i (&xr)[CPL][XL]) {
+        if constexpr (!NORM) {
+#pragma unroll
+            for (int u = 0; u < CPL; ++u)
+#pragma unroll
+                for (int q = 0; q < XL; ++q) xr[u][q] = ld16(x + (size_t)(lane + 64 * u) * PER + 8 * q);
+        } else {
+            float ss = 0.f;
+#pragma unroll
+            for (int c = 0; c < CPL * XL; ++c) {
+                if constexpr (XL == 1) {
+                    ss = sumsq8(hv[c][0], ss);
+                } else {
+                    const int src = 32 * (c & 1) + (lane >> 1);
+                    v4i g;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int a = __shfl(hv[c >> 1][0][j], src), b = __shfl(hv[c >> 1][1][j], src);
+                        g[j] = (lane & 1) ? b : a;
+                    }
+                    ss = sumsq8(g, ss);
+                }
+            }
+            const float rs = rms_scale(wave_sum(ss), K, eps);
+#pragma unroll
+            for (int u = 0; u < CPL; ++u)
+#pragma unroll
+                for (int q = 0; q < XL; ++q)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        xr[u][q][j] = (int)rms_apply2((uint32_t)wv[u][q][j], (uint32_t)hv[u][q][j], rs);
+        }
+    }
+};
+
 // Persistent batch-1 GEMV: about WPC wavefronts per CU, wavefront g handles output rows g, g + nw, g + 2 nw, ...
 // (nw = wavefronts in the grid). K = 64 PER CPL: lane l owns the 16-byte chunks l, l + 64, ..., of every row, and
 // its activations for those chunks stay in registers (packed bf16) for the whole kernel. The next row's weights are
 // in flight while the current row is reduced (two register buffers used in turn), so every wavefront keeps its
 // loads streaming instead of paying one memory latency per row. EPI_SWIGLU: a work item is the row pair (n, S + n).
-template <typename WT, int CPL, int EPI>
+template <typename WT, int CPL, int EPI, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_b1p_kernel(const WT *__restrict__ W, const float *__restrict__ scale,
                                                        const uint16_t *__restrict__ x, uint16_t *__restrict__ y, int N,
-                                                       int K, int S) {
+                                                       int K, int S, const uint16_t *__restrict__ normw = nullptr,
+                                                       float eps = 0.f) {
     using D = PairDot<WT>;
     constexpr int PER = D::PER, XL = D::XL;
     constexpr int NROW = EPI == EPI_SWIGLU ? 2 : 1;
@@ -55,10 +115,11 @@ __global__ __launch_bounds__(256) void gemv_b1p_kernel(const WT *__restrict__ W,
     int n = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (n >= N) return;  // no block-level synchronization in this kernel
     v4i xr[CPL][XL];
-#pragma unroll
-    for (int u = 0; u < CPL; ++u)
-#pragma unroll
-        for (int q = 0; q < XL; ++q) xr[u][q] = ld16(x + (size_t)(lane + 64 * u) * PER + 8 * q);
+    {
+        XLoadB1<PER, XL, CPL, NORM> xl;
+        xl.issue(x, normw, lane);
+        xl.finish(x, eps, K, lane, xr);
+    }
     // one buffer resource per row (scalar base = the row, range = its K weights); each lane adds its fixed byte
     // offset, so no vector address arithmetic sits between a row's loads and the next row's
     const char *wbase = reinterpret_cast<const char *>(W);
@@ -153,13 +214,15 @@ __global__ __launch_bounds__(256) void gemv_b1p_kernel(const WT *__restrict__ W,
 // dot. CPL == 0: any K % PER == 0, chunks streamed 8 per lane at a time. Per row, the arithmetic is that of the
 // persistent kernel (same chunk order, same PairDot, same fold_sum lane pairing), so either kernel gives the same
 // bits.
-template <typename WT, int R, int CPL, int EPI>
+template <typename WT, int R, int CPL, int EPI, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, const float *__restrict__ scale,
                                                       const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
-                                                      int N, int K, int S) {
+                                                      int N, int K, int S,
+                                                      const uint16_t *__restrict__ normw = nullptr, float eps = 0.f) {
     using D = PairDot<WT>;
     constexpr int PER = D::PER, XL = D::XL;
     constexpr int NROW = EPI == EPI_SWIGLU ? 2 * R : R;
+    static_assert(!NORM || CPL > 0, "the normalizing form needs K = 64 PER CPL");
     const int lane = threadIdx.x & 63;
     const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * R);
     if (n0 >= N) return;  // no block-level synchronization in this kernel
@@ -181,14 +244,13 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, 
 
     if constexpr (CPL > 0) {
         v4i w[CPL][NROW], xr[CPL][XL];
+        XLoadB1<PER, XL, CPL, NORM> xl;
+        xl.issue(x, normw, lane);
 #pragma unroll
         for (int u = 0; u < CPL; ++u)
 #pragma unroll
             for (int i = 0; i < NROW; ++i) w[u][i] = ld_nt16(rp[i] + (size_t)(lane + 64 * u) * 16);
-#pragma unroll
-        for (int u = 0; u < CPL; ++u)
-#pragma unroll
-            for (int q = 0; q < XL; ++q) xr[u][q] = ld16(x + (size_t)(lane + 64 * u) * PER + 8 * q);
+        xl.finish(x, eps, K, lane, xr);
 #pragma unroll
         for (int u = 0; u < CPL; ++u)
 #pragma unroll
@@ -566,9 +628,9 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 // rows), else 1; the LFM2Q_GEMV_R knob (1, 2 or 4) overrides it where the registers allow. Both need
 // K = 64 PER CPL with CPL in {1, 2, 4, 8}; other K take the one-shot kernel's generic loop, where `rows` (1, 2, 4)
 // sets the output rows per wavefront. Per-row arithmetic is the same in all of them.
-template <typename WT, int EPI>
+template <typename WT, int EPI, bool NORM = false>
 void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, int N, int K, int S, int rows,
-               hipStream_t st) {
+               hipStream_t st, const uint16_t *nw = nullptr, float eps = 0.f) {
     constexpr int PER = PairDot<WT>::PER;
     const int wpc = knob_int(KNOB_GEMV_WPC, 8);
     const int C = K / PER;
@@ -583,13 +645,15 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
 #define LFM2Q_B1(C_)                                                                                        \
     do {                                                                                                    \
         if (persistent)                                                                                     \
-            gemv_b1p_kernel<WT, C_, EPI><<<gridp, 256, 0, st>>>(W, scale, x, y, N, K, S);                   \
+            gemv_b1p_kernel<WT, C_, EPI, NORM><<<gridp, 256, 0, st>>>(W, scale, x, y, N, K, S, nw, eps);    \
         else if (r1 == 4 && C_ <= 2)                                                                        \
-            gemv_b1_kernel<WT, C_ <= 2 ? 4 : 1, C_, EPI><<<grid(4), 256, 0, st>>>(W, scale, x, y, N, K, S); \
+            gemv_b1_kernel<WT, C_ <= 2 ? 4 : 1, C_, EPI, NORM><<<grid(4), 256, 0, st>>>(W, scale, x, y, N, K, \
+                                                                                       S, nw, eps);         \
         else if (r1 == 2 && C_ <= 4)                                                                        \
-            gemv_b1_kernel<WT, C_ <= 4 ? 2 : 1, C_, EPI><<<grid(2), 256, 0, st>>>(W, scale, x, y, N, K, S); \
+            gemv_b1_kernel<WT, C_ <= 4 ? 2 : 1, C_, EPI, NORM><<<grid(2), 256, 0, st>>>(W, scale, x, y, N, K, \
+                                                                                       S, nw, eps);         \
         else                                                                                                \
-            gemv_b1_kernel<WT, 1, C_, EPI><<<grid(1), 256, 0, st>>>(W, scale, x, y, N, K, S);               \
+            gemv_b1_kernel<WT, 1, C_, EPI, NORM><<<grid(1), 256, 0, st>>>(W, scale, x, y, N, K, S, nw, eps); \
     } while (0)
     switch (cpl) {
         case 1: LFM2Q_B1(1); break;
@@ -597,12 +661,14 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
         case 4: LFM2Q_B1(4); break;
         case 8: LFM2Q_B1(8); break;
         default: {
-            if (EPI == EPI_SWIGLU || rows <= 1)
-                gemv_b1_kernel<WT, 1, 0, EPI><<<grid(1), 256, 0, st>>>(W, scale, x, y, N, K, S);
-            else if (rows == 2)
-                gemv_b1_kernel<WT, 2, 0, EPI><<<grid(2), 256, 0, st>>>(W, scale, x, y, N, K, S);
-            else
-                gemv_b1_kernel<WT, 4, 0, EPI><<<grid(4), 256, 0, st>>>(W, scale, x, y, N, K, S);
+            if constexpr (!NORM) {  // the normalizing form's entry point admits only the four K above
+                if (EPI == EPI_SWIGLU || rows <= 1)
+                    gemv_b1_kernel<WT, 1, 0, EPI><<<grid(1), 256, 0, st>>>(W, scale, x, y, N, K, S);
+                else if (rows == 2)
+                    gemv_b1_kernel<WT, 2, 0, EPI><<<grid(2), 256, 0, st>>>(W, scale, x, y, N, K, S);
+                else
+                    gemv_b1_kernel<WT, 4, 0, EPI><<<grid(4), 256, 0, st>>>(W, scale, x, y, N, K, S);
+            }
         }
     }
 #undef LFM2Q_B1
@@ -793,6 +859,37 @@ extern "C" int lfm2q_gemv_residual(int wtype, const void *W, const float *scale,
         return gemv_run<uint16_t, EPI_RESIDUAL>("gemv_residual", (const uint16_t *)W, scale, x, h, B, N, K, 0,
                                                 (hipStream_t)stream);
     return set_error(LFM2Q_ERR_ARG, "gemv_residual: wtype must be 0 (int8) or 1 (bf16), got %d", wtype);
+}
+
+extern "C" int lfm2q_gemv_rmsnorm(int wtype, int epi, const void *W, const float *scale, const lfm2q_bf16 *h,
+                                  const lfm2q_bf16 *norm_w, float eps, lfm2q_bf16 *y, int N, int K,
+                                  lfm2q_stream_t stream) {
+    const char *name = "gemv_rmsnorm";
+    LFM2Q_REQUIRE(W && h && norm_w && y, LFM2Q_ERR_ARG, "%s: null pointer", name);
+    LFM2Q_REQUIRE(wtype == 0 || wtype == 1, LFM2Q_ERR_ARG, "%s: wtype must be 0 (int8) or 1 (bf16), got %d", name,
+                  wtype);
+    LFM2Q_REQUIRE(epi == EPI_NONE || epi == EPI_SWIGLU, LFM2Q_ERR_ARG, "%s: epi must be 0 (none) or 1 (swiglu), got %d",
+                  name, epi);
+    LFM2Q_REQUIRE(wtype == 1 || scale, LFM2Q_ERR_ARG, "%s: int8 W needs fp32 scale", name);
+    const int per_chunk = wtype == 0 ? 1024 : 512;  // K of one 16-byte weight chunk per lane
+    LFM2Q_REQUIRE(N >= 1 && (K == per_chunk || K == 2 * per_chunk || K == 4 * per_chunk || K == 8 * per_chunk),
+                  LFM2Q_ERR_SHAPE, "%s: N >= 1 and K in {%d, %d, %d, %d} (N=%d K=%d)", name, per_chunk, 2 * per_chunk,
+                  4 * per_chunk, 8 * per_chunk, N, K);
+    LFM2Q_REQUIRE(aligned16(W) && aligned16(h) && aligned16(norm_w), LFM2Q_ERR_ALIGN,
+                  "%s: W, h and norm_w must be 16-byte aligned", name);
+    const hipStream_t st = (hipStream_t)stream;
+    if (wtype == 0) {
+        if (epi == EPI_SWIGLU)
+            launch_b1<int8_t, EPI_SWIGLU, true>((const int8_t *)W, scale, h, y, N, K, N, 0, st, norm_w, eps);
+        else
+            launch_b1<int8_t, EPI_NONE, true>((const int8_t *)W, scale, h, y, N, K, N, 0, st, norm_w, eps);
+    } else {
+        if (epi == EPI_SWIGLU)
+            launch_b1<uint16_t, EPI_SWIGLU, true>((const uint16_t *)W, scale, h, y, N, K, N, 0, st, norm_w, eps);
+        else
+            launch_b1<uint16_t, EPI_NONE, true>((const uint16_t *)W, scale, h, y, N, K, N, 0, st, norm_w, eps);
+    }
+    return launch_status(name);
 }
 
 extern "C" int lfm2q_silu_mul(const lfm2q_bf16 *g, lfm2q_bf16 *y, int B, int I, lfm2q_stream_t stream) {

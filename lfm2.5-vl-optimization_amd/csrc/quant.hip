@@ -14,6 +14,7 @@
 // (add_rmsnorm), kernels/vision_ops.cu:29-80 (add_layernorm); bound in kernels/int8_gemm.cpp:83-141.
 #include "common.hpp"
 #include "quantize.hpp"
+#include "rmsnorm.hpp"
 #include "status.hpp"
 
 #include <algorithm>
@@ -229,15 +230,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_q_kernel(uint16_t *__restrict
     load_row_add<CH>(h + (size_t)row * H, y ? y + (size_t)row * H : nullptr, C, lane, hv);
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float a = bf2f_lo((uint32_t)hv[c][j]), b = bf2f_hi((uint32_t)hv[c][j]);
-            ss += a * a;
-            ss += b * b;
-        }
-    ss = wave_sum(ss);
-    const float rs = 1.f / sqrtf(ss / (float)H + eps);
+    for (int c = 0; c < CH; ++c) ss = sumsq8(hv[c], ss);
+    const float rs = rms_scale(wave_sum(ss), H, eps);
     v4i xv[CH];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -245,9 +239,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_q_kernel(uint16_t *__restrict
         xv[c] = v4i{0, 0, 0, 0};
         if (i < C) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                xv[c][j] = (int)pack_bf16x2(bf2f_lo((uint32_t)wv[c][j]) * rbf(bf2f_lo((uint32_t)hv[c][j]) * rs),
-                                      bf2f_hi((uint32_t)wv[c][j]) * rbf(bf2f_hi((uint32_t)hv[c][j]) * rs));
+            for (int j = 0; j < 4; ++j) xv[c][j] = (int)rms_apply2((uint32_t)wv[c][j], (uint32_t)hv[c][j], rs);
         }
     }
     if (xo) store_row<CH>(xo + (size_t)row * H, xv, C, lane);

@@ -32,6 +32,7 @@ SIGNATURES = {
     "lfm2q_gemv_bf16": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemv_swiglu": [_I, _P, _P, _P, _P, _I, _I, _I, _P],
     "lfm2q_gemv_residual": [_I, _P, _P, _P, _P, _I, _I, _I, _P],
+    "lfm2q_gemv_rmsnorm": [_I, _I, _P, _P, _P, _P, _F, _P, _I, _I, _P],
     "lfm2q_gemv_w4": [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "lfm2q_silu_mul": [_P, _P, _I, _I, _P],
     "lfm2q_quant_rows": [_P, _P, _P, _I, _I, _P],

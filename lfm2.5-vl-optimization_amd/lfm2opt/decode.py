@@ -100,6 +100,8 @@ class DecodeLinears:
         self.mode, self.drop_bf16 = gemv, drop_bf16
         self.K = ext()
         self.epilogue_fusion = os.environ.get("LFM2_EPI", "1") != "0"  # runtime.py:35; 0 = separate ops
+        # the batch-1 GEMVs that normalize their input row themselves (gemv_rmsnorm); 0 = add_rmsnorm_q, then the GEMV
+        self.norm_fusion = os.environ.get("LFM2_NORM_GEMV", "1") != "0"
         self.last_path = None
         self.lin, self.lin_scale, self.lin_zeros, self.lin_inv_s, self.lin_bf16, self.w8 = {}, {}, {}, {}, {}, {}
         w4_pre = w4_pre or {}
@@ -203,6 +205,27 @@ class DecodeLinears:
             g = self.linear(x, key)
             self.K.silu_mul(g, act)
         return act
+
+    def norm_fusable(self, B, key):
+        """Whether the linear for key at batch B runs as one GEMV that also computes its input's RMSNorm
+        (gemv_rmsnorm): batch 1 on the GEMV path, INT8 or BF16 weights, K a supported chunk multiple."""
+        if not (self.norm_fusion and B == 1 and self.path(B, key) == "gemv"):
+            return False
+        fmt = self.fmt(key)
+        K = self.shape(key)[1]
+        if fmt == "int8":
+            return K in (1024, 2048, 4096, 8192)
+        return fmt == "bf16" and K in (512, 1024, 2048, 4096)
+
+    def linear_normed(self, h, key, norm_w, eps, swiglu=False, out=None):
+        """linear(rms_norm(h) * norm_w, key), or swiglu(...) of it, as one GEMV (norm_fusable(1, key) must hold):
+        bit-identical to add_rmsnorm_q's x followed by the GEMV."""
+        w = self.lin[key]
+        N = w.shape[0] // 2 if swiglu else w.shape[0]
+        y = out if out is not None else torch.empty(1, N, device=h.device, dtype=h.dtype)
+        self.last_path = "gemv"
+        self.K.gemv_rmsnorm(w, self.lin_scale.get(key), h.contiguous(), norm_w, eps, y, 1 if swiglu else 0)
+        return y
 
     def residual(self, x, key, h):
         """h [B, N] = bf16(h + bf16(x @ W^T)) in place: the GEMV's fused residual epilogue on the GEMV path, else the

@@ -172,6 +172,35 @@ class DecodeOps:
         self.gemv_impl = int(impl)
 
     # ---- additions ----------------------------------------------------------------------------------------
+    def gemv_rmsnorm(self, W, scale, h, norm_w, eps, y, epi=0):
+        """The batch-1 GEMV of RMSNorm(h) (an addition): x = bf16(norm_w * bf16(h * rsqrt(mean(h^2) + eps))) is
+        formed inside the GEMV, then y [1, N] = x @ W^T * scale (epi 0) or the SwiGLU of x over W = w1|w3 (epi 1, y
+        [1, N] from W [2N, K]). Bit-identical to add_rmsnorm (no residual input) followed by gemv / gemv_epi(0), the
+        pair the reference's decode step runs before each of these linears (src/lfm2opt/runtime.py:251-255,
+        :276-285). h, norm_w bf16 [K]; W int8 (K in 1024 .. 8192, powers of two, fp32 scale) or bf16 (K in 512 ..
+        4096, scale optional)."""
+        _check_bf16(h, "h")
+        _check_bf16(norm_w, "norm_w")
+        _check_bf16(y, "y")
+        if epi not in (0, 1):
+            raise RuntimeError("gemv_rmsnorm: epi 0 (none) or 1 (swiglu)")
+        if not (W.is_cuda and W.is_contiguous() and W.dim() == 2 and W.dtype in (torch.int8, torch.bfloat16)):
+            raise RuntimeError("W must be a contiguous CUDA bf16 or int8 matrix")
+        int8 = W.dtype == torch.int8
+        R, K = W.shape
+        N = R // 2 if epi == 1 else R
+        if int8 and (scale is None or scale.dtype != torch.float32):
+            raise RuntimeError("int8 W needs fp32 scale")
+        if scale is not None:
+            _check_t(scale, torch.float32, "scale")
+            if scale.numel() != R:
+                raise RuntimeError("scale must have one value per weight row")
+        if (epi == 1 and R % 2) or h.numel() != K or norm_w.numel() != K or y.numel() != N:
+            raise RuntimeError("gemv_rmsnorm: h [1, K], norm_w [K], y [1, N] (batch 1)")
+        _same_device(W, h, norm_w, y, scale)
+        _capi.call("lfm2q_gemv_rmsnorm", 0 if int8 else 1, int(epi), W.data_ptr(), _capi.ptr(scale), h.data_ptr(),
+                   norm_w.data_ptr(), float(eps), y.data_ptr(), N, K, _capi.stream(h))
+
     def gemv_residual(self, W, scale, x, h):
         """h [B, N] += bf16(x @ W^T * scale) in place, rounded as the reference's residual add
         (kernels/lfm2_decode.cu:108-113): h = bf16(h + bf16(acc * s))."""
