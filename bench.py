@@ -807,6 +807,56 @@ def quant_sweep(reps):
     return res
 
 
+def dispatch_sweep(reps, batches=(1, 4, 8, 16, 17, 24, 32, 48, 64, 96, 128, 256)):
+    """The decode dispatch (lfm2opt/decode.py linear_path) against measurement: each decode weight shape at each batch
+    on every path it could take -- the INT8 GEMV, W8A16 (with the K split), F.linear on the BF16 copy (hipBLASLt) and
+    the GPTQ-style INT4 GEMV -- timed as one call per rotated weight copy in a graph (>= 512 MB of copies), with the
+    path linear_path picks for INT8 and for INT4 weights (a BF16 copy kept) and how far each pick is from the
+    fastest path available to that weight format."""
+    from lfm2opt.decode import linear_path
+    from lfm2opt.kernels import ext, int8_ext
+
+    E, E8 = ext(), int8_ext()
+    g = torch.Generator(device="cuda").manual_seed(4)
+    shapes = [("qkv", QKV, H), ("in", CONV_IN, H), ("o", H, H), ("w13", 2 * FFN, H), ("w2", H, FFN),
+              ("head", VOCAB, H)]
+    res = []
+    for name, N, K in shapes:
+        nc = max(2, -(-512 * 2 ** 20 // (N * K * 2)))
+        W8 = [torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g) for _ in range(nc)]
+        Wb = [(torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16) for _ in range(nc)]
+        W4 = [(torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 8), device="cuda", dtype=torch.int32, generator=g),
+               (torch.rand(N, K // W4_GROUP, device="cuda", generator=g) * 0.02 + 1e-3).half(),
+               torch.randint(-2 ** 31, 2 ** 31 - 1, (N, (K // W4_GROUP + 7) // 8), device="cuda", dtype=torch.int32,
+                             generator=g)) for _ in range(nc)]
+        s = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+        for B in batches:
+            x = torch.randn(B, K, device="cuda", generator=g).to(torch.bfloat16)
+            y = torch.empty(B, N, device="cuda", dtype=torch.bfloat16)
+            t = {}
+            for path, fn in (("gemv", lambda: [E.gemv(W, s, x, y) for W in W8]),
+                             ("w8a16", lambda: [E8.gemm_w8(x, W, s, None, y, False) for W in W8]),
+                             ("linear", lambda: [torch.mm(x, W.t(), out=y) for W in Wb]),
+                             ("gemv_int4", lambda: [E.gemv_w4z(*W, x, y) for W in W4])):
+                gr = capture(fn)
+                t[path] = round(time_graph(gr, reps, 2)[0] * 1e3 / nc, 2)
+                del gr
+            p8 = linear_path("int8", "int8", B, N, K, True)
+            p4 = linear_path("int4", "int4", B, N, K, True)
+            best8 = min(("gemv", "w8a16", "linear"), key=t.get)
+            best4 = min(("gemv_int4", "linear"), key=t.get)
+            row = {"shape": name, "N": N, "K": K, "B": B, **{f"us_{k}": v for k, v in t.items()},
+                   "pick_int8": p8, "best_int8": best8, "pick_int8_vs_best": round(t[p8] / t[best8], 3),
+                   "pick_int4": p4, "best_int4": best4,
+                   "pick_int4_vs_best": round(t["gemv_int4" if p4 == "gemv" else p4] / t[best4], 3)}
+            res.append(row)
+            log(f"dispatch {name} B={B}: " + ", ".join(f"{k} {v}" for k, v in t.items()) + f"; int8 pick {p8} "
+                f"({row['pick_int8_vs_best']} x best), int4 pick {p4} ({row['pick_int4_vs_best']} x best)")
+        del W8, Wb, W4
+        torch.cuda.empty_cache()
+    return res
+
+
 # every (tile, K split) configuration of the per-token W8A8 kernels (the cost model's candidates); 256 x 256 and
 # the first 256 x 128, 128 x 128 and 128 x 64 are the persistent kernels, "…/1g" the one-tile-per-workgroup kernels, "…sN"
 # the persistent kernels with K cut into N slices over workgroups
@@ -1061,6 +1111,8 @@ def main():
     ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
     ap.add_argument("--mfma-rate", action="store_true", help="only the sustained int8 matrix-core rate calibration")
     ap.add_argument("--bw-roof", action="store_true", help="only the bare-read bandwidth roof")
+    ap.add_argument("--dispatch-sweep", action="store_true",
+                    help="only the decode linears on every path at batches 1-256 against the dispatch's pick")
     ap.add_argument("--quant-sweep", action="store_true",
                     help="only the activation quantizers under both launch forms on the W8A8 shapes")
     ap.add_argument("--read-branch", action="store_true",
@@ -1081,6 +1133,9 @@ def main():
         return
     if args.mfma_rate:
         print(json.dumps({"mfma_sustained": mfma_rate()}))
+        return
+    if args.dispatch_sweep:
+        print(json.dumps({"dispatch_sweep": dispatch_sweep(max(5, args.steps // 20))}))
         return
     if args.quant_sweep:
         print(json.dumps({"quant_sweep": quant_sweep(max(5, args.steps // 10))}))
