@@ -67,8 +67,11 @@ def test_gemm_grouped_every_tile(E, tile, tune):
 
 @pytest.mark.skip(reason="a persistent grouped-64 kernel (two groups per 128-byte stage, scale ring in LDS) faulted "
                          "the GPU on this case, its first run with more tiles than workgroups (128 x 64 tiles, "
-                         "1100 x 320 x 2056); the cause was not found and the kernel was taken out, so the grouped "
-                         "path runs the one-tile-per-workgroup kernels and this case stays off the GPU")
+                         "1100 x 320 x 2056). Cause since found on the CPU: an inline-asm direct-to-LDS load read a "
+                         "buffer resource that v_readlane_b32 had restored with no wait states (a stale base); "
+                         "every such load now has the wait states and the build checks for the hazard, but the "
+                         "kernel stays out of the library, so the grouped path runs the one-tile-per-workgroup "
+                         "kernels and this case stays off the GPU")
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64"])
 @pytest.mark.parametrize("gelu", [False, True])
 def test_gemm_grouped_persistent_many_tiles(E, tile, gelu, tune):
