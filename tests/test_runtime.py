@@ -91,6 +91,45 @@ def test_batched_prefill_leaves_the_state_of_the_step():
         assert torch.equal(fused.generate(ids, 4, graph=False), step.generate(ids, 4, graph=False))
 
 
+@pytest.mark.parametrize("fused", [False, True])
+def test_prefill_from_input_embeddings(fused):
+    """prefill / generate with inputs_embeds (the VL case: image features in place of some token embeddings): with
+    random vectors at some positions the last position's logits equal transformers' forward over the same embeddings,
+    and the continuation equals transformers' greedy decoding of it; with the token embeddings themselves the result
+    equals the ids-only request. Step-by-step prompt (eager steps) and the one-pass prefill."""
+    net = tiny_lfm2(seed=12, conv_bias=True)
+    lin = TorchLinears(decode_weights(net))
+    B, T, H = 2, 7, net.config.hidden_size
+    ids = torch.randint(3, net.config.vocab_size, (B, T), generator=torch.Generator().manual_seed(13))
+    emb = net.model.embed_tokens(ids).detach().clone()
+    emb[:, 2:5] = torch.randn(B, 3, H, generator=torch.Generator().manual_seed(14)) * 0.5  # "image" positions
+    dec = StaticDecoder(net, bucket=16, keep_logits=True, fused_prefill=fused, linears=lin)
+    first, st = dec.prefill(ids, 3, graph=False, inputs_embeds=emb)
+    with torch.no_grad():
+        want = net(inputs_embeds=emb, use_cache=False).logits.float()[:, -1]
+    if fused:
+        assert rel_err(dec.last_prefill_logits, want) < 1e-5
+    else:
+        assert rel_err(st.logits, want) < 1e-5
+    want[:, dec.eos] = float("-inf")
+    assert torch.equal(first, want.argmax(-1))
+    out = dec.generate(ids, 3, graph=False, inputs_embeds=emb)
+    with torch.no_grad():
+        seq = emb
+        for t in range(3):
+            logits = net(inputs_embeds=seq, use_cache=False).logits.float()[:, -1]
+            logits[:, dec.eos] = float("-inf")
+            tok = logits.argmax(-1)
+            assert torch.equal(out[:, T + t], tok), t
+            seq = torch.cat([seq, net.model.embed_tokens(tok)[:, None]], dim=1)
+    plain = net.model.embed_tokens(ids).detach()
+    assert torch.equal(dec.generate(ids, 3, graph=False, inputs_embeds=plain), dec.generate(ids, 3, graph=False))
+    with pytest.raises(ValueError, match="inputs_embeds must be"):
+        dec.prefill(ids, 3, graph=False, inputs_embeds=emb[:, :-1])
+    with pytest.raises(ValueError, match="LFM2-VL"):
+        dec.prefill(ids, 3, graph=False, pixel_values=torch.zeros(1, 3, 8, 8))
+
+
 def test_weight_keys_match_the_reference():
     """Keys and stacking order of the reference's StaticDecoder.lin (runtime.py:159-171, gptq.py:239-256)."""
     net = tiny_lfm2(seed=1, layer_types=("conv", "full_attention"))

@@ -102,6 +102,31 @@ def test_generate_graph_equals_eager(nets):
     assert torch.equal(dec.generate(ids, 12), a)  # a second request on the same captured graph
 
 
+@pytest.mark.parametrize("flags", [{}, {"prefill_int8": True}, {"fused_prefill": True}])
+def test_prefill_from_input_embeddings_on_the_gpu(nets, flags):
+    """prefill / generate with inputs_embeds on the library's kernels: the token embeddings themselves give the
+    ids-only request's tokens exactly, and embeddings with 'image' vectors at some positions give the logits of
+    transformers' fp32 forward over the same embeddings (the weights the GPU paths read) within the bar."""
+    from lfm2opt.runtime import StaticDecoder
+
+    _, gnet = nets
+    dec = StaticDecoder(gnet, bucket=32, keep_logits=True, gemv="int8", **flags)
+    ids = torch.randint(3, gnet.config.vocab_size, (2, 9), generator=torch.Generator().manual_seed(31))
+    emb = gnet.model.embed_tokens(ids.cuda()).detach()
+    assert torch.equal(dec.generate(ids, 6, inputs_embeds=emb), dec.generate(ids, 6))
+    img = emb.clone()
+    img[:, 3:6] = (torch.randn(2, 3, emb.shape[-1], generator=torch.Generator().manual_seed(32)) * 0.5).to(img)
+    first, st = dec.prefill(ids, 2, inputs_embeds=img)
+    got = dec.last_prefill_logits.cpu() if flags else st.logits.float().cpu()
+    ref = oracle(gnet, dec, 2)
+    with torch.no_grad():
+        want = ref(inputs_embeds=img.float().cpu(), use_cache=False).logits.float()[:, -1]
+    err = rel_err(got, want)
+    print(f"inputs_embeds prefill {flags}: max |err| / max |ref| = {err:.2e}")
+    assert err <= (PREFILL_TOL if flags else TOL)
+    dec.clear_states()
+
+
 def test_drop_bf16_frees_the_module_weights(cuda):
     """drop_bf16: the HF linears' own weights are freed, the tied head's table stays (the step's embedding), and
     decoding runs on the INT8 weights alone (W8A16 above the GEMV's batches)."""
@@ -309,3 +334,109 @@ def test_full_size_prefill_against_transformers(full_size, flags, bar):
     assert err <= bar
     assert corr >= 0.98
     dec.clear_states()
+
+
+def _fake_quant_grouped(x, group=64):
+    """Symmetric INT8 fake quantization per row and group of 64 columns (the runtime's default activation scales):
+    s = max(amax, 1e-8) / 127, x -> round(x / s) s, in fp32."""
+    xf = x.float()
+    xg = xf.reshape(*xf.shape[:-1], xf.shape[-1] // group, group)
+    sc = xg.abs().amax(-1, keepdim=True).clamp_min(1e-8) / 127.0
+    return (torch.round(xg / sc).clamp(-127, 127) * sc).reshape(xf.shape)
+
+
+def _frob(a, b):
+    """||a - b|| / ||b|| (Frobenius), the reference's own error measure for the W8A8 GEMMs
+    (tests/test_int8_gemm.py:81-104): one flipped quantization step moves a max-based error by up to 1/127 of the
+    tensor's largest value, but the norm by almost nothing."""
+    a, b = a.float(), b.float()
+    return float((a - b).norm() / b.norm())
+
+
+def test_full_size_prefill_w8a8_against_fake_quant_emulation(full_size, monkeypatch):
+    """The W8A8 one-pass prefill at the LFM2-1.2B shapes, checked GEMM call by GEMM call and against an emulation.
+
+    Per call (all 64 W8A8 GEMMs of the 64-token pass): the GEMM's bf16 output against fp32 arithmetic on the same
+    call's int8 input dequantized with its own grouped-64 scales, times the dequantized INT8 weight (+ bias): within
+    bf16 output rounding (relative Frobenius error <= 5e-3). A wrong group scale, a row read with another row's scale,
+    a scale buffer of the wrong layer or a wrong weight scale moves that far past the bar. Each producer's int8 input
+    is bit-identical to the grouped quantizer of the bf16 x it computes (tests/test_producers_gpu.py), so the two
+    checks cover every quantization point of the pass.
+
+    End to end: an emulation that keeps every op of the runtime's prompt pass (the same PyTorch attention, conv, norms
+    and bf16 rounding points, on the GPU) and replaces each W8A8 GEMM by the library's grouped quantizer of its bf16
+    input, dequantized, times the dequantized weight in fp32. The two take the same quantization decisions until fp32
+    rounding (the kernels sum exact int32 partials) flips one, after which a random-weight network of this depth
+    amplifies the difference; the same emulation with fp64 products shows how much that alone accounts for. Bar: on
+    the last position's logits and on the keys every attention layer leaves in the cache, the W8A8 pass is no farther
+    from the emulation (relative Frobenius error) than 1.5 x the fp32-vs-fp64 difference + 2e-3 (measured: equal to it
+    at every layer, 1.3e-2 at the first attention layer to 5.0e-2 at the last), and at most 1e-1; against transformers' fp32 forward the W8A8 prefill is ~10 % off (max-based), whether
+    or not that forward fake-quantizes its fp32 activations, because bf16 rounding alone moves enough quantization
+    decisions that the two quantization noises are independent."""
+    import torch.nn.functional as F
+
+    from lfm2opt import runtime
+    from lfm2opt.int8 import quantize_rows
+    from lfm2opt.runtime import StaticDecoder
+
+    T = 64
+    ids = torch.randint(3, full_size.config.vocab_size, (1, T), generator=torch.Generator().manual_seed(7))
+    dec = StaticDecoder(full_size, bucket=16, keep_logits=True, gemv="int8", prefill_int8=True)
+    deq = {key: dec.lin.lin[key].float() * dec.lin.lin_scale[key].float()[:, None] for key in dec.lin.lin}
+
+    def dequant_input(x):
+        q, sT = x  # the producers' (int8 [R, K], scales [K / 64, R])
+        R, K = q.shape
+        return (q.float().view(R, K // 64, 64) * sT.t().reshape(R, K // 64, 1)).view(R, K)
+
+    orig = runtime._PromptPass.gemm
+    calls = []
+
+    def gemm_checked(self, key, x, bias=None):
+        y = orig(self, key, x, bias)
+        if isinstance(x, tuple):
+            xi = dequant_input(x)
+        else:  # a bf16 input quantized inside its Int8Linear (attention / conv output)
+            xi = dequant_input(quantize_rows(x, 64))
+        ref = F.linear(xi, deq[key])
+        if bias is not None:
+            ref = ref + bias.float()
+        calls.append((key, _frob(y, ref)))
+        return y
+
+    monkeypatch.setattr(runtime._PromptPass, "gemm", gemm_checked)
+    print("full-size W8A8 prefill, GEMM by GEMM and against its fp32 fake-quant emulation", flush=True)
+    _, st = dec.prefill(ids, 2, graph=False)
+    got_logits = dec.last_prefill_logits.clone()
+    got_k = {i: st.k[i][..., :T].clone() for i in st.k}
+    dec.clear_states()
+    del dec
+    worst_call = max(calls, key=lambda c: c[1])
+    print(f"{len(calls)} W8A8 GEMM calls: worst output against fp32 on its own input {worst_call[1]:.2e} "
+          f"({worst_call[0]})")
+    assert len(calls) == 4 * 16  # qkv and o, or in_proj and out_proj; w1|w3 and w2: four per layer
+    assert worst_call[1] <= 5e-3
+
+    def emulation(dtype):
+        def gemm_fq(self, key, x, bias=None):
+            R, K = x.shape
+            xi = dequant_input(quantize_rows(x, 64))
+            y = F.linear(xi.to(dtype), deq[key].to(dtype)).to(x.dtype)
+            return y if bias is None else y + bias
+
+        monkeypatch.setattr(runtime._PromptPass, "gemm", gemm_fq)
+        emu = StaticDecoder(full_size, bucket=16, keep_logits=True, gemv="int8", fused_prefill=True)
+        _, st2 = emu.prefill(ids, 2, graph=False)
+        out = emu.last_prefill_logits.clone(), {i: st2.k[i][..., :T].clone() for i in st2.k}
+        emu.clear_states()
+        return out
+
+    e32, e64 = emulation(torch.float32), emulation(torch.float64)
+    pairs = [("logits", _frob(got_logits, e32[0]), _frob(e32[0], e64[0]))]
+    pairs += [(f"layer {i} keys", _frob(k, e32[1][i]), _frob(e32[1][i], e64[1][i])) for i, k in got_k.items()]
+    for what, e, base in pairs:
+        print(f"{what}: W8A8 vs emulation {e:.2e}; emulation fp32 vs fp64 products {base:.2e}")
+    # the W8A8 pass sits no farther from the emulation than an fp32-rounding perturbation of the emulation itself
+    for what, e, base in pairs:
+        assert e <= 1.5 * base + 2e-3, what
+        assert e <= 1e-1, what
