@@ -212,8 +212,24 @@ int lfm2q_gemm_i8(const int8_t *A, const float *sa, const int8_t *B, const float
 int lfm2q_gemm_i8_ex(const int8_t *A, const float *sa, const int8_t *B, const float *sb, const lfm2q_bf16 *bias,
                      lfm2q_bf16 *Y, int M, int N, int K, int gelu, void *ws, size_t ws_bytes, lfm2q_stream_t stream);
 
-/* Bytes of the lfm2q_gemm_i8_ex / lfm2q_gemm_w8_ex workspace (64 MiB + 64 KiB). */
+/* Bytes of the lfm2q_gemm_i8_ex / lfm2q_gemm_w8_ex / lfm2q_gemm_i8_fq workspace (64 MiB + 320 KiB). */
 size_t lfm2q_gemm_workspace_bytes(void);
+
+/* The per-token W8A8 layer on bf16 activations: q int8 [M, K] and sa fp32 [M] receive X's per-token quantization
+ * (the bytes lfm2q_quant_rows writes) and Y the GEMM on them; Y, q and sa equal lfm2q_quant_rows followed by
+ * lfm2q_gemm_i8_ex bit for bit. By default the call runs exactly that pair (the faster form on MI355X). With the
+ * tuning knob LFM2Q_GEMM_FQ = 1 it runs them as one launch where the shape fits the persistent GEMM (K <= 16384,
+ * N % 8 == 0, Y 16-byte aligned, M K and M N below 2^30): the workgroups first quantize X together, in chunks of
+ * rows, each waiting until every chunk is written (a workgroup that waits longer than LFM2Q_GEMM_FQ_WAIT_US, 20 us
+ * by default, quantizes the open chunks itself), then run the GEMM's tiles. ws: the lfm2q_gemm_i8_ex workspace at
+ * its full size (lfm2q_gemm_workspace_bytes()), 256-byte aligned, zero-filled before its first use; its last
+ * 256 KiB hold the one-launch form's control block, which every call leaves valid. Calls sharing a workspace must
+ * not overlap. Shapes, alignment, B, sb, bias, gelu as in lfm2q_gemm_i8; X and q 16-byte aligned.
+ * The reference runs the pair as two kernels (quantize_rows then gemm_i8: src/lfm2opt/int8.py:45-51,
+ * kernels/int8_gemm.cu:391-432 then :125-297); this entry point is the pair behind one call. */
+int lfm2q_gemm_i8_fq(const lfm2q_bf16 *X, int8_t *q, float *sa, const int8_t *B, const float *sb,
+                     const lfm2q_bf16 *bias, lfm2q_bf16 *Y, int M, int N, int K, int gelu, void *ws, size_t ws_bytes,
+                     lfm2q_stream_t stream);
 
 /* W8A8 GEMM on bf16 activations, quantized per token inside the GEMM: a first pass writes sa fp32 [M], the
  * scales lfm2q_quant_rows would write for X, and the GEMM quantizes each stage of X bf16 [M, K] on its way into

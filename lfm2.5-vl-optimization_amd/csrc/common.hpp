@@ -147,6 +147,18 @@ __device__ __forceinline__ void lds_dma4(v4i desc, uint32_t voff, uint32_t lds_b
     asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(desc), "{m0}"(lds_base)
                  : "memory");
 }
+// The same two loads at device scope (sc1): they do not take a line this XCD's L2 may hold from before, for data
+// another XCD's workgroup wrote with device-scope stores during the same launch.
+__device__ __forceinline__ void lds_dma16_dev(v4i desc, uint32_t voff, uint32_t lds_base) {
+    asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dwordx4 %0, %1, 0 offen sc1 lds" ::"v"(voff), "s"(desc),
+                 "{m0}"(lds_base)
+                 : "memory");
+}
+__device__ __forceinline__ void lds_dma4_dev(v4i desc, uint32_t voff, uint32_t lds_base) {
+    asm volatile(LFM2Q_LDS_DMA_WAIT "buffer_load_dword %0, %1, 0 offen sc1 lds" ::"v"(voff), "s"(desc),
+                 "{m0}"(lds_base)
+                 : "memory");
+}
 // LDS address of p as a wavefront-uniform (SGPR) value for M0
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(p));

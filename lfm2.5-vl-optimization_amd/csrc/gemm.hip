@@ -43,6 +43,7 @@ constexpr bool out_gelu(int o) { return o == OUT_BF16_GELU || o == OUT_Q8_GELU; 
 constexpr bool out_q8(int o) { return o == OUT_Q8 || o == OUT_Q8_GELU; }
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 // per-token: ((float)acc * sx) * sw + b, each op rounded separately (no FMA contraction)
 __device__ __forceinline__ float dequant(int acc, float sx, float sw, float b) {
@@ -76,10 +77,13 @@ __device__ __forceinline__ void tile_of(int w, int tm_n, int tn_n, int &tm, int 
 }
 
 constexpr int STAGES = 3;  // LDS ring depth: stage s computes while s + 1 and s + 2 are loading
-// The workspace of the K split across workgroups (lfm2q_gemm_i8_ex / lfm2q_gemm_w8_ex): one arrival counter per
-// output tile, then the partial accumulator tiles.
+// The GEMM workspace: for the K split across workgroups (lfm2q_gemm_i8_ex / lfm2q_gemm_w8_ex) one arrival counter
+// per output tile, then the partial accumulator tiles; after them the control block of the quantizing prologue
+// (lfm2q_gemm_i8_fq), which the split never touches.
 constexpr uint32_t SPLIT_CNT_WORDS = 16384;
-constexpr size_t GEMM_WS_BYTES = 4 * SPLIT_CNT_WORDS + (64u << 20);
+constexpr size_t GEMM_SPLIT_BYTES = 4 * SPLIT_CNT_WORDS + (64u << 20);
+constexpr size_t GEMM_CTL_BYTES = 65536 * 4;
+constexpr size_t GEMM_WS_BYTES = GEMM_SPLIT_BYTES + GEMM_CTL_BYTES;
 
 // s_waitcnt immediate for vmcnt(n) with the other counters at their maximum (gfx9: vmcnt bits 3:0 and 15:14)
 constexpr int vmcnt_imm(int n) { return 0x3f70 | (n & 15) | ((n >> 4) << 14); }
@@ -870,11 +874,170 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 // Nothing waits on another workgroup. The counters must be 0 when a call starts (a zero-filled workspace; every
 // completed call leaves them 0).
 
-template <int OUT, int BM, int BN, int NSLOT, bool SPL = false>
+// ------------------------------------------------------------------------------------------------ quantizing prologue
+// XQ (lfm2q_gemm_i8_fq): the persistent kernel takes bf16 activations and quantizes them itself, once, before its
+// tiles: per-token scales s = max(amax, 1e-8) / 127 and q = rint(x / s) by the quantizers' own code (quant8), so the
+// int8 rows, the scales and therefore every output equal quant_rows followed by the GEMM bit for bit.
+//   * The rows are cut into chunks of rpc rows (at most 16384 values: 4 vectors of 8 per thread of a 512-thread
+//     workgroup, and no more rows than spread the chunks over every workgroup) and chunk c belongs to workgroup
+//     c % G. Each workgroup quantizes its chunks (all 512 threads on one chunk, the row maxima meeting in LDS),
+//     writes the int8 rows and the scales to the caller's q and sx with device-scope stores, waits for them,
+//     publishes each chunk as done in a state word and adds their number to a done count.
+//   * Before its first tile a workgroup waits until the count reaches the number of chunks, then reads the int8
+//     rows and scales with device-scope loads (a line of q in this XCD's L2 may be from an earlier call; one
+//     agent-scope acquire fence per workgroup instead, an invalidation of the XCD's L2, measured 15 us on MI355X
+//     and the device-scope loads no slower than ordinary ones in the tiles). Nothing waits on a chunk's owner for long: after
+//     steal_ticks of waiting (20 us by default) the waiter quantizes, and publishes, every chunk whose state is
+//     still open itself (the bytes are a function of x alone, so a second writer stores what the first did; only
+//     owners add to the count), so the kernel finishes whatever runs beside it and however many of its workgroups
+//     are resident.
+//   * States hold epoch * 4 + 2 for done, epoch = control word 0, so they never need clearing: the last workgroup
+//     to leave (control word 1 counts them) zeroes the counts (words 1 and 2) and advances the epoch. A zero-filled
+//     control block is a valid start; two launches on one control block at the same time race.
+constexpr int XQ_CTL = 64;                                       // control words ahead of the chunk states
+constexpr int XQ_CHUNK_VALS = 16384;                             // values per chunk at most
+constexpr int XQ_MAX_CHUNKS = (int)(GEMM_CTL_BYTES / 4) - XQ_CTL;  // chunk states in the control block
+constexpr int XQ_WAIT_US = 20;                                   // default wait before stealing, in microseconds
+constexpr uint64_t XQ_TICKS_PER_US = 100;                        // s_memrealtime runs at 100 MHz
+constexpr int AUX_DEV = 16;                                      // device-scope (sc1) buffer access
+
+// Rows per chunk for K and a grid of G workgroups: as many as 16384 values hold, but no more than ceil(M / G), so
+// every workgroup gets a chunk where there are rows enough. The chunk count never exceeds that of the first bound
+// or G, whichever is larger.
+__host__ __device__ inline int xq_rows_per_chunk(int M, int K, int G) {
+    const int cap = K >= XQ_CHUNK_VALS ? 1 : XQ_CHUNK_VALS / K, spread = (M + G - 1) / G;
+    return spread < cap ? (spread > 0 ? spread : 1) : cap;
+}
+
+// Chunk c is rows r0 .. r0 + R - 1, V = R K / 8 vectors of 8 values; thread t holds vectors t + 512 j, j < 4.
+struct XqChunk {
+    int r0, R, V;
+    __device__ XqChunk(int c, int rpc, int M, int K) : r0(c * rpc), R(min(rpc, M - c * rpc)), V(R * (K >> 3)) {}
+};
+
+__device__ __forceinline__ void xq_load(const XqChunk &ch, int K, rsrc_t rxb, int tid, v4i (&v)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = tid + 512 * j;
+        v[j] = idx < ch.V ? buf_ld16_nt(rxb, (uint32_t)(((size_t)ch.r0 * K + (size_t)idx * 8) * 2)) : v4i{0, 0, 0, 0};
+    }
+}
+
+// Quantize a loaded chunk with all 512 threads; smem: R floats of scratch (the rows' maxima).
+__device__ __forceinline__ void xq_quant(const XqChunk &ch, int K, const v4i (&v)[4], rsrc_t rxq, rsrc_t rsx,
+                                         uint8_t *smem, int tid) {
+    const int C8 = K >> 3, V = ch.V;
+    unsigned *rmax = reinterpret_cast<unsigned *>(smem);
+    for (int i = tid; i < ch.R; i += 512) rmax[i] = 0u;
+    __syncthreads();
+    // the rows' maxima of |x| (non-negative fp32 values order as their bit patterns): a wavefront whose 64 vectors
+    // lie in one row reduces them first and sends one value, the others one per lane
+    const int wbase = tid & ~63;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = tid + 512 * j, first = wbase + 512 * j, last = first + 63;
+        const float m = absmax8(v[j], 0.f);
+        if (last < V && first / C8 == last / C8) {  // uniform over the wavefront
+            const float wm = wave_max(m);
+            if ((tid & 63) == 0) atomicMax(&rmax[first / C8], __float_as_uint(wm));
+        } else if (idx < V) {
+            atomicMax(&rmax[idx / C8], __float_as_uint(m));
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = tid + 512 * j;
+        if (idx < V) {
+            const int r = idx / C8, cv = idx - r * C8;
+            const float sc = scale_of(__uint_as_float(rmax[r])), rc = 1.f / sc;
+            int lo, hi;
+            quant8(v[j], sc, rc, lo, hi);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{(uint32_t)lo, (uint32_t)hi}, rxq,
+                                                  (int)(((size_t)(ch.r0 + r) * K + (size_t)cv * 8)), 0, AUX_DEV);
+            if (cv == 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sc), rsx, (ch.r0 + r) * 4, 0, AUX_DEV);
+        }
+    }
+    __syncthreads();  // the maxima are read before the next chunk clears them
+}
+
+// Phase 1 of an XQ launch (every thread of the workgroup); returns the epoch, for xq_leave.
+__device__ __forceinline__ uint32_t xq_prologue(const uint16_t *__restrict__ Xb, int8_t *__restrict__ Xq,
+                                                float *__restrict__ sx, uint32_t *__restrict__ ctl, int M, int K,
+                                                uint64_t steal_ticks, uint8_t *smem, int tid) {
+    __shared__ uint32_t bcast[2];
+    const int G = gridDim.x, rpc = xq_rows_per_chunk(M, K, G), nch = (M + rpc - 1) / rpc;
+    const rsrc_t rxb = make_rsrc(Xb, (uint32_t)((size_t)M * K * 2)), rxq = make_rsrc(Xq, (uint32_t)((size_t)M * K));
+    const rsrc_t rsx = make_rsrc(sx, (uint32_t)M * 4u);
+    if (tid == 0) bcast[0] = __hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const uint32_t epoch = bcast[0], done = epoch * 4u + 2u;
+    uint32_t *state = ctl + XQ_CTL;
+    int own = 0;
+    for (int c = blockIdx.x; c < nch; c += G, ++own) {
+        v4i v[4];
+        const XqChunk ch(c, rpc, M, K);
+        xq_load(ch, K, rxb, tid, v);
+        xq_quant(ch, K, v, rxq, rsx, smem, tid);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores have completed
+    __syncthreads();
+    if (tid == 0 && own) {
+        for (int c = blockIdx.x; c < nch; c += G)
+            __hip_atomic_store(&state[c], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(ctl + 2, (uint32_t)own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // every chunk done by its owner, or after steal_ticks the ones still open quantized (and published) here
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        if (tid == 0)
+            bcast[1] = __hip_atomic_load(ctl + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= (uint32_t)nch;
+        __syncthreads();
+        if (bcast[1]) break;  // uniform
+        if (__syncthreads_or(tid == 0 && __builtin_amdgcn_s_memrealtime() - t0 >= steal_ticks)) {
+            for (int c = 0; c < nch; ++c) {  // in order; each chunk that is still open, by the whole workgroup
+                if (tid == 0)
+                    bcast[1] = __hip_atomic_load(&state[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != done;
+                __syncthreads();
+                if (bcast[1]) {
+                    v4i v[4];
+                    const XqChunk ch(c, rpc, M, K);
+                    xq_load(ch, K, rxb, tid, v);
+                    xq_quant(ch, K, v, rxq, rsx, smem, tid);
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    __syncthreads();
+                    if (tid == 0) __hip_atomic_store(&state[c], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __syncthreads();
+            }
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // nothing of the prologue outstanding when the ring starts
+    return epoch;
+}
+
+// The workgroup leaves: the last one zeroes the counts and advances the epoch (every workgroup has read them and is
+// past its last state access) for the next launch on this control block.
+__device__ __forceinline__ void xq_leave(uint32_t *__restrict__ ctl, uint32_t epoch, int tid) {
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t before = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (before == gridDim.x - 1) {
+            __hip_atomic_store(ctl + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ctl, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <int OUT, int BM, int BN, int NSLOT, bool SPL = false, bool XQ = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_bigp_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
-    uint32_t *__restrict__ ws = nullptr, int SK = 1) {
+    uint32_t *__restrict__ ws = nullptr, int SK = 1, const uint16_t *__restrict__ Xb = nullptr,
+    uint32_t *__restrict__ ctl = nullptr, uint64_t steal_ticks = 0) {
     static_assert(OUT == OUT_BF16 || OUT == OUT_BF16_GELU, "bf16 output only");
     static_assert((BM == 256 && (BN == 256 || BN == 128)) || (BM == 128 && (BN == 128 || BN == 64)), "tile shape");
     constexpr int BKT = 128, WMt = BM / 4, WNt = BN / 2, TM = WMt / 32, TN = WNt / 32;
@@ -896,7 +1059,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int KTT = (K + BKT - 1) / BKT;                  // stages of the whole K
     const int SPS = SPL ? (KTT + SK - 1) / SK : KTT;      // stages per slice
     int t = blockIdx.x;                                   // work unit
-    if (t >= T) return;  // the launch sizes the grid to at most T; uniform per workgroup
+    // XQ: X (the int8 rows) and sx are written here first, by every workgroup of the grid (which may hold more
+    // workgroups than units); otherwise the launch sizes the grid to at most T
+    uint32_t epoch = 0;
+    if constexpr (XQ)
+        epoch = xq_prologue(Xb, const_cast<int8_t *>(X), const_cast<float *>(sx), ctl, M, K, steal_ticks, smem, tid);
+    if (t >= T) {  // uniform per workgroup
+        if constexpr (XQ) xq_leave(ctl, epoch, tid);
+        return;
+    }
 
     uint32_t off[ILX];
     int cb[ILX];
@@ -928,7 +1099,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
         for (int j = 0; j < ILX; ++j) {
             const bool in = k0 + cb[j] < K;
-            lds_dma16(rx, in ? off[j] + k0 : 0xfffffff0u, sX + 1024 * (8 * j + wbase));
+            if constexpr (XQ)  // written by this launch's prologue: device-scope loads
+                lds_dma16_dev(rx, in ? off[j] + k0 : 0xfffffff0u, sX + 1024 * (8 * j + wbase));
+            else
+                lds_dma16(rx, in ? off[j] + k0 : 0xfffffff0u, sX + 1024 * (8 * j + wbase));
             if (j < ILW) lds_dma16(rw, in ? off[j] + k0 : 0xfffffff0u, sW + 1024 * (8 * j + wbase));
         }
     };
@@ -943,7 +1117,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         int l = lane;
         asm volatile("" : "+v"(l));
         if (wbase < 4) {
-            if (wbase < BM / 64) lds_dma4(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
+            if (wbase < BM / 64) {
+                if constexpr (XQ)
+                    lds_dma4_dev(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
+                else
+                    lds_dma4(rsx, (uint32_t)(m0 + 64 * wbase + l) * 4, eb + 256 * wbase);
+            }
             if (wbase < (BN >= 128 ? BN / 128 : 1) && bias)
                 lds_dma4(rb, (uint32_t)(n0 + 128 * wbase + 2 * l) * 2, eb + 4 * BM + 4 * BN + 256 * wbase);
         } else if (wbase < 4 + BN / 64) {
@@ -1114,6 +1293,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         if (tnext >= T) break;
         t = tnext;
     }
+    if constexpr (XQ) xq_leave(ctl, epoch, tid);
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
@@ -1180,10 +1360,10 @@ inline int split_fits(const TileCfg &o, long tiles, int sk, int K, size_t ws_byt
            tiles <= (long)SPLIT_CNT_WORDS && 4 * (size_t)SPLIT_CNT_WORDS + (size_t)tiles * sk * o.bm * o.bn * 4 <= ws_bytes;
 }
 
-inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0) {
+inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0, bool pers_only = false) {
     const int force_bm = knob_int(KNOB_GEMM_BM, 0), force_bn = knob_int(KNOB_GEMM_BN, 0);
-    const int force_ks = knob_int(KNOB_GEMM_KSPLIT, 0), force_sk = knob_int(KNOB_GEMM_SPLITK, 0);
-    const bool pers_ok = knob_int(KNOB_GEMM_BIGP, 1) != 0;
+    const int force_ks = pers_only ? 0 : knob_int(KNOB_GEMM_KSPLIT, 0), force_sk = knob_int(KNOB_GEMM_SPLITK, 0);
+    const bool pers_ok = pers_only || knob_int(KNOB_GEMM_BIGP, 1) != 0;
     static const TileCfg opts[] = {
         {256, 256, 1, 0.1582, 10.87, 1, 1}, {256, 128, 1, 0.2033, 5.808, 1, 1}, {128, 128, 1, 0.2894, 2.859, 1, 1},
         {128, 64, 1, 0.4104, 1.750, 1, 1},
@@ -1193,7 +1373,9 @@ inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0) {
         {128, 64, 1, 0.5114, 3.760, 4},  {64, 128, 4, 0.4555, 3.970, 1},  {64, 128, 2, 0.4864, 2.494, 2},
         {64, 128, 1, 0.5502, 3.505, 4},  {64, 64, 6, 0.5660, 3.086, 1},   {64, 64, 3, 0.6101, 0.836, 2},
         {64, 64, 1, 0.7027, 2.256, 4}};
-    const auto usable = [&](const TileCfg &o) { return pers_ok || !o.pers || (o.bm == 256 && o.bn == 256); };
+    const auto usable = [&](const TileCfg &o) {
+        return pers_only ? o.pers == 1 : pers_ok || !o.pers || (o.bm == 256 && o.bn == 256);
+    };
     if (force_bm && force_bn) {
         const int ks = force_ks == 4 ? 4 : force_ks == 2 ? 2 : 1;
         for (const TileCfg &o : opts)
@@ -1208,7 +1390,7 @@ inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0) {
     }
     const long cus = device_cus();
     double best = 1e300;
-    TileCfg bestc = opts[8];
+    TileCfg bestc = pers_only ? opts[2] : opts[8];
     for (const TileCfg &o : opts) {
         if ((force_ks && o.ksp != force_ks) || !usable(o)) continue;
         const long tiles = (long)((M + o.bm - 1) / o.bm) * ((N + o.bn - 1) / o.bn);
@@ -1237,7 +1419,7 @@ inline TileCfg pick_tile_pt(int M, int N, int K, size_t ws_bytes = 0) {
 template <int OUT>
 void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float *sw, const uint16_t *bias, void *Y,
                  int M, int N, int K, hipStream_t st, void *ws = nullptr, size_t ws_bytes = 0) {
-    const TileCfg t = pick_tile_pt(M, N, K, (OUT == OUT_BF16 || OUT == OUT_BF16_GELU) && ws ? ws_bytes : 0);
+    const TileCfg t = pick_tile_pt(M, N, K, (OUT == OUT_BF16 || OUT == OUT_BF16_GELU) && ws ? std::min(ws_bytes, GEMM_SPLIT_BYTES) : 0);
     const int sh = knob_int(KNOB_GEMM_SWZ, 2);
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
     if (t.pers) {
@@ -1323,6 +1505,49 @@ void launch_gemm(const int8_t *A, const int8_t *B, const float *sx, const float 
 #undef LFM2Q_GEMM
 }
 
+// bf16 activations quantized by the persistent kernel's own prologue (q, sx: quant_rows' bytes), the persistent
+// configurations only, every CU in the grid (a workgroup with no tile quantizes and leaves). True where the knob
+// LFM2Q_GEMM_FQ = 1 asks for it and the shape and pointers fit the persistent kernel; otherwise the caller runs the
+// pair (quant_rows, then the GEMM), which is the default because it is the faster form on MI355X: the prologue's
+// wait for every chunk (device-scope counts seen across the XCDs) and its leaving count cost 5-10 us more than the
+// kernel boundary they replace, and its chunks stream no faster than quant_rows' grid.
+inline bool fq_applies(int M, int N, int K, const void *Y, const void *bias) {
+    const int rpc = xq_rows_per_chunk(M, K, 1);
+    return knob_int(KNOB_GEMM_FQ, 0) == 1 && K <= XQ_CHUNK_VALS && (M + rpc - 1) / rpc <= XQ_MAX_CHUNKS &&
+           (N & 7) == 0 && ((uintptr_t)Y & 15) == 0 && ((uintptr_t)bias & 3) == 0 &&
+           (size_t)M * N * 2 < 0x80000000ull && (size_t)M * K * 2 < 0x80000000ull;
+}
+
+template <int OUT>
+void launch_gemm_fq(const uint16_t *X, int8_t *q, float *sx, const int8_t *B, const float *sw, const uint16_t *bias,
+                    void *Y, int M, int N, int K, hipStream_t st, void *ws) {
+    const TileCfg t = pick_tile_pt(M, N, K, GEMM_SPLIT_BYTES, true);
+    const int grid = (int)device_cus();
+    uint32_t *const w = static_cast<uint32_t *>(ws);
+    uint32_t *const ctl = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(ws) + GEMM_SPLIT_BYTES);
+    const uint64_t ticks = (uint64_t)knob_int(KNOB_GEMM_FQ_WAIT_US, XQ_WAIT_US) * XQ_TICKS_PER_US;
+#define LFM2Q_FQ(BM_, BN_, NS_, SPL_)                                                                               \
+    gemm_i8_bigp_kernel<OUT, BM_, BN_, NS_, SPL_, true><<<grid, 512, 0, st>>>(q, B, sx, sw, bias, Y, M, N, K, w, t.sk,\
+                                                                            X, ctl, ticks)
+    if (t.sk > 1) {
+        if (t.bm == 256)
+            LFM2Q_FQ(256, 128, 3, true);
+        else if (t.bn == 64)
+            LFM2Q_FQ(128, 64, 6, true);
+        else
+            LFM2Q_FQ(128, 128, 4, true);
+    } else if (t.bm == 256 && t.bn == 256) {
+        LFM2Q_FQ(256, 256, 2, false);
+    } else if (t.bm == 256) {
+        LFM2Q_FQ(256, 128, 3, false);
+    } else if (t.bn == 64) {
+        LFM2Q_FQ(128, 64, 6, false);
+    } else {
+        LFM2Q_FQ(128, 128, 4, false);
+    }
+#undef LFM2Q_FQ
+}
+
 // grouped-64 activation scales (sxT [K/64, M]); OUT_Q8*: Y = Yq int8 [M, N], YsT [N/64, M]
 template <int OUT>
 void launch_gemm_grouped(const int8_t *A, const int8_t *B, const float *sxT, const float *sw, const uint16_t *bias,
@@ -1379,7 +1604,7 @@ void launch_gemm_w8(const uint16_t *X, const int8_t *W, const float *sw, const u
         const long cus = device_cus();
         sk = (int)std::min<long>(8, std::min<long>(cus / tiles, K / 2048));
         if (const int f = knob_int(KNOB_GEMM_SPLITK, 0)) sk = std::min(f, std::max(1, KT));
-        while (sk > 1 && 4 * (size_t)SPLIT_CNT_WORDS + (size_t)tiles * sk * t.bm * t.bn * 4 > ws_bytes) --sk;
+        while (sk > 1 && 4 * (size_t)SPLIT_CNT_WORDS + (size_t)tiles * sk * t.bm * t.bn * 4 > std::min(ws_bytes, GEMM_SPLIT_BYTES)) --sk;
         if (tiles > (long)SPLIT_CNT_WORDS || sk < 2) sk = 1;
     }
     const dim3 grid(tiles * sk);
@@ -1487,6 +1712,28 @@ extern "C" int lfm2q_gemm_i8_bf16a(const lfm2q_bf16 *X, float *sa, const int8_t 
     else
         launch_gemm_bf16a<OUT_BF16>(X, B, sa, sb, bias, Y, M, N, K, st);
     return launch_status("gemm_i8_bf16a");
+}
+
+extern "C" int lfm2q_gemm_i8_fq(const lfm2q_bf16 *X, int8_t *q, float *sa, const int8_t *B, const float *sb,
+                                const lfm2q_bf16 *bias, lfm2q_bf16 *Y, int M, int N, int K, int gelu, void *ws,
+                                size_t ws_bytes, lfm2q_stream_t stream) {
+    LFM2Q_REQUIRE(X && q && sa && B && sb && Y && ws, LFM2Q_ERR_ARG, "gemm_i8_fq: null pointer");
+    if (int st = check_gemm("gemm_i8_fq", q, B, Y, M, N, K)) return st;
+    LFM2Q_REQUIRE((long)M * K * 2 < (1L << 31), LFM2Q_ERR_SHAPE, "gemm_i8_fq: x must be smaller than 2 GiB");
+    LFM2Q_REQUIRE(aligned16(X) && ((uintptr_t)sa & 3) == 0, LFM2Q_ERR_ALIGN,
+                  "gemm_i8_fq: x must be 16-byte and sa 4-byte aligned");
+    LFM2Q_REQUIRE(((uintptr_t)ws & 255) == 0 && ws_bytes >= GEMM_WS_BYTES, LFM2Q_ERR_ARG,
+                  "gemm_i8_fq: workspace must be 256-byte aligned and at least %zu bytes", GEMM_WS_BYTES);
+    const hipStream_t st = (hipStream_t)stream;
+    if (!fq_applies(M, N, K, Y, bias)) {  // the pair: quant_rows, then the GEMM
+        if (int e = lfm2q_quant_rows(X, q, sa, M, K, stream)) return e;
+        return lfm2q_gemm_i8_ex(q, sa, B, sb, bias, Y, M, N, K, gelu, ws, ws_bytes, stream);
+    }
+    if (gelu)
+        launch_gemm_fq<OUT_BF16_GELU>(X, q, sa, B, sb, bias, Y, M, N, K, st, ws);
+    else
+        launch_gemm_fq<OUT_BF16>(X, q, sa, B, sb, bias, Y, M, N, K, st, ws);
+    return launch_status("gemm_i8_fq");
 }
 
 extern "C" int lfm2q_gemm_i8_grouped(const int8_t *A, const float *saT, const int8_t *B, const float *sb,

@@ -43,6 +43,8 @@ enum Knob {
     KNOB_GEMM_SPLITK,   // per-token W8A8 with a workspace: K slices over workgroups (1 = none, 2..8)
     KNOB_CHAIN_WAIT_MS, // GEMV chain: bound of each dependency wait in milliseconds (default 20; 0: at once)
     KNOB_QUANT_WG,      // quant_rows / quant_groups: 1 a workgroup per row, 0 a wavefront per row
+    KNOB_GEMM_FQ,       // gemm_i8_fq: 1 = the one-launch kernel (quantizing prologue); default 0, quant_rows + GEMM
+    KNOB_GEMM_FQ_WAIT_US, // gemm_i8_fq prologue: microseconds before a waiting workgroup quantizes open chunks itself
     KNOB_COUNT
 };
 struct KnobVal {

@@ -45,6 +45,7 @@ SIGNATURES = {
     "lfm2q_gemm_workspace_bytes": [],
     "lfm2q_gemm_i8_grouped": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_i8_bf16a": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "lfm2q_gemm_i8_fq": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
     "lfm2q_gemm_i8_q": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_w8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "lfm2q_gemm_w8_ex": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],

@@ -328,6 +328,27 @@ class Int8Ops:
         _capi.call("lfm2q_gemm_i8_bf16a", x.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(), _capi.ptr(bias),
                    y.data_ptr(), M, N, K, int(bool(gelu)), _capi.stream(x))
 
+    def gemm_i8_fq(self, x, xq, sx, w, sw, bias, y, gelu):
+        """The per-token pair quant_rows(x) -> (xq, sx), then gemm_i8, behind one call with the stream's workspace;
+        xq, sx and y are bit-identical to the pair's. By default the library runs the pair; with the tuning knob
+        LFM2Q_GEMM_FQ = 1 the persistent GEMM's workgroups quantize x first and then run the tiles, in one launch.
+        Reference pair: src/lfm2opt/int8.py:45-51 (quantize_rows, then gemm_i8)."""
+        _check_bf16(x, "x")
+        _check_t(xq, torch.int8, "xq")
+        _check_t(sx, torch.float32, "sx")
+        K = x.size(-1)
+        M = x.numel() // K if K else 0
+        if xq.numel() != M * K or xq.size(-1) != K:
+            raise RuntimeError("xq shape")
+        if sx.numel() != M:
+            raise RuntimeError("sx shape")
+        N = self._check_common(w, sw, bias, y, M, K)
+        _same_device(x, xq, sx, w, sw, bias, y)
+        ws = _capi.workspace(x)
+        _capi.call("lfm2q_gemm_i8_fq", x.data_ptr(), xq.data_ptr(), sx.data_ptr(), w.data_ptr(), sw.data_ptr(),
+                   _capi.ptr(bias), y.data_ptr(), M, N, K, int(bool(gelu)), ws.data_ptr(), ws.numel(),
+                   _capi.stream(x))
+
     def gemm_i8_q(self, xq, sxT, w, sw, bias, yq, ysT, gelu):
         """Grouped W8A8 writing the next W8A8 GEMM's input: (yq [M, N], ysT [N/64, M]) = quant_groups(the bf16 output
         gemm_i8 would write), bit-identical to that pair of calls. Reference: gemm_i8_q(), kernels/int8_gemm.cpp:53-69

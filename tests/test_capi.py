@@ -84,7 +84,17 @@ def test_status_codes_without_launch(L):
     assert L.lfm2q_gemm_i8_ex(fake, fake, fake, fake, None, fake, 4, 8, 64, 0, fake, 4096, None) == 1
     assert L.lfm2q_gemm_w8_ex(fake, fake, fake, None, fake, 4, 8, 64, 0, ctypes.c_void_p(0x1108), 1 << 20, None) == 1
     assert L.lfm2q_gemm_w8_ex(None, fake, fake, None, fake, 4, 8, 64, 0, None, 0, None) == 1
-    assert L.lfm2q_gemm_workspace_bytes() == 4 * 16384 + (64 << 20)
+    assert L.lfm2q_gemm_workspace_bytes() == 4 * 16384 + (64 << 20) + (256 << 10)
+    ws = ctypes.c_void_p(0x100000)
+    full = L.lfm2q_gemm_workspace_bytes()
+    assert L.lfm2q_gemm_i8_fq(fake, fake, fake, fake, fake, None, fake, 4, 8, 64, 0, None, full, None) == 1
+    assert "null pointer" in L.lfm2q_last_error().decode()
+    assert L.lfm2q_gemm_i8_fq(fake, fake, fake, fake, fake, None, fake, 4, 8, 72, 0, ws, full, None) == 2
+    assert L.lfm2q_gemm_i8_fq(fake, fake, fake, fake, fake, None, fake, 4, 8, 64, 0, ws, 64 << 20, None) == 1
+    assert "at least" in L.lfm2q_last_error().decode()
+    assert L.lfm2q_gemm_i8_fq(fake, fake, fake, fake, fake, None, fake, 4, 8, 64, 0, ctypes.c_void_p(0x100010), full,
+                              None) == 1
+    assert "256-byte aligned" in L.lfm2q_last_error().decode()
 
 
 def test_python_checks_match_reference_wording():
