@@ -27,6 +27,7 @@
 #include "status.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace lfm2q {
 namespace {
@@ -379,8 +380,8 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
             *reinterpret_cast<int2 *>(x_s + dxb[j]) = make_int2(lo, hi);
         }
     };
-    auto issue = [&](int kt) {  // kt: this group's stage index
-        const int buf = kt % NSTG, k0 = (kt0 + kt) * BK;
+    auto issue_in = [&](int kt, int buf) {  // kt: this group's stage index, buf = kt % NSTG
+        const int k0 = (kt0 + kt) * BK;
         if constexpr (XBF)
 #pragma unroll
             for (int j = 0; j < IXB; ++j) {
@@ -402,6 +403,7 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
             lds_dma4(rs, (uint32_t)(((long)(kt0 + kt) * M + m0 + 64 * wave + lane) * 4),
                      lds_addr(reinterpret_cast<uint8_t *>(sS[buf]) + 256 * wave));
     };
+    auto issue = [&](int kt) { issue_in(kt, kt % NSTG); };
 
     v16f facc[GRP ? TN : 1][GRP ? TM : 1];
     if (GRP)
@@ -430,9 +432,10 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         for (int j = 0; j < TM; ++j) fx[kk][j] = swz(wm * WMt + 32 * j + lr, 2 * kk + lh, sh);
     }
 
-    // the MFMAs of stage kt (its operands are in LDS and visible)
-    auto compute = [&](int kt) {
-        const uint8_t *x_s = sX[kt % NSTG], *w_s = sW[kt % NSTG];
+    // the MFMAs of stage kt (its operands are in LDS and visible); slot = kt % NSTG, a compile-time constant where
+    // the caller knows it (the LDS addresses then fold into the reads' immediate offsets)
+    auto compute_in = [&](int slot) {
+        const uint8_t *x_s = sX[slot], *w_s = sW[slot];
         // both k steps' fragments are read up front, the second set while the first set's MFMAs run
         v4i wf[2][TN], xf[2][TM];
 #pragma unroll
@@ -453,7 +456,7 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk][i], xf[kk][j],
                                                                      (GRP && kk == 0) ? zero : acc[i][j], 0, 0, 0);
         if (GRP) {
-            const float *s_s = sS[kt % NSTG];
+            const float *s_s = sS[slot];
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const float sj = s_s[wm * WMt + 32 * j + lr];
@@ -466,6 +469,8 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
             }
         }
     };
+
+    auto compute = [&](int kt) { compute_in(kt % NSTG); };
 
     if constexpr (XBF) {
         // Stage kt + 2 is issued after stage kt's barrier; after stage kt's MFMAs each wavefront waits for its own
@@ -493,6 +498,26 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
 #pragma unroll
     for (int p = 0; p < NSTG - 1; ++p)
         if (p < KT) issue(p);
+    if constexpr (GRP && KSP == 1) {
+        // the grouped fold is VALU-bound: the stage loop is unrolled by the ring depth so that each copy's slot is a
+        // constant and no per-stage address arithmetic remains beside the fold (same loads, order and results)
+        auto step = [&](int kt, auto slot_c) {
+            constexpr int SLOT = decltype(slot_c)::value;
+            wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
+            asm volatile("s_barrier" ::: "memory");
+            if (kt + NSTG - 1 < KT) issue_in(kt + NSTG - 1, (SLOT + NSTG - 1) % NSTG);
+            compute_in(SLOT);
+        };
+        static_assert(NSTG == 3, "grouped ring depth");
+        int kt = 0;
+        for (; kt + 3 <= KT; kt += 3) {
+            step(kt, std::integral_constant<int, 0>{});
+            step(kt + 1, std::integral_constant<int, 1>{});
+            step(kt + 2, std::integral_constant<int, 2>{});
+        }
+        if (kt < KT) step(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < KT) step(kt + 1, std::integral_constant<int, 1>{});
+    } else
     for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
         // stage kt has landed once at most the loads of the (up to NSTG - 2) stages issued after it are outstanding
         wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
