@@ -65,16 +65,17 @@ __device__ __forceinline__ float dequant(float facc, float, float sw, float b) {
 // tile sequence is split into 8 contiguous bands and band x is given to the workgroups of XCD x; inside the band
 // tiles go in groups of 8 M-tiles that sweep N, so concurrently resident workgroups of one XCD share operand panels
 // in that XCD's L2.
-__device__ __forceinline__ void tile_of(int w, int tm_n, int tn_n, int &tm, int &tn) {
-    const int T = tm_n * tn_n;
-    int t = w;
-    if (T % 8 == 0) t = (w % 8) * (T / 8) + w / 8;
+__device__ __forceinline__ void group_of(int t, int tm_n, int tn_n, int &tm, int &tn) {
     constexpr int GM = 8;
     const int per_group = GM * tn_n;
     const int g = t / per_group, r = t % per_group;
     const int gm = min(GM, tm_n - g * GM);
     tm = g * GM + r % gm;
     tn = r / gm;
+}
+__device__ __forceinline__ void tile_of(int w, int tm_n, int tn_n, int &tm, int &tn) {
+    const int T = tm_n * tn_n;
+    group_of(T % 8 == 0 ? (w % 8) * (T / 8) + w / 8 : w, tm_n, tn_n, tm, tn);
 }
 
 constexpr int STAGES = 3;  // LDS ring depth: stage s computes while s + 1 and s + 2 are loading
@@ -1103,14 +1104,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         off[j] = (uint32_t)row * K + cb[j];
     }
     int m0 = 0, n0 = 0, kb = 0, KT = KTT;  // the unit's tile corner and its stages kb .. kb + KT - 1
+    int utile = 0, uslice = 0;              // K split: the unit's tile (its arrival counter) and K slice
     v4i rx, rw;
     auto at_tile = [&](int tt) {
         int tm, tn;
-        tile_of(SPL ? tt / SK : tt, tm_n, tn_n, tm, tn);
+        if (SPL && (tm_n * tn_n) % 8 == 0 && gridDim.x % 8 == 0) {
+            // unit tt runs on XCD tt % 8: that XCD's band of tiles (tile_of's band), each tile's SK slices in a row,
+            // so the slices of a tile and the tiles sharing operand panels meet in one L2
+            const int x = tt % 8, r = tt / 8;
+            utile = x * (tm_n * tn_n / 8) + r / SK;
+            uslice = r % SK;
+            group_of(utile, tm_n, tn_n, tm, tn);
+        } else {
+            utile = SPL ? tt / SK : tt;
+            uslice = SPL ? tt % SK : 0;
+            tile_of(utile, tm_n, tn_n, tm, tn);
+        }
         m0 = tm * BM;
         n0 = tn * BN;
         if (SPL) {
-            kb = (tt % SK) * SPS;
+            kb = uslice * SPS;
             KT = max(0, min(KTT - kb, SPS));
         }
         rx = make_desc(X + (size_t)m0 * K, (uint32_t)std::min<long>((long)(M - m0) * K, 0x7fffffffL));
@@ -1224,7 +1237,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         // the next tile's first NSLOT - 1 stages (slots g .. g + NSLOT - 2, every slot but the last stage's: free
         // since the barrier of this tile's last stage) and epilogue operands go out before this tile's epilogue
         const int tnext = t + (int)gridDim.x;
-        const int pm0 = m0, pn0 = n0, pt = t;
+        const int pm0 = m0, pn0 = n0, ptile = utile, pslice = uslice;
         if (tnext < T) {
             at_tile(tnext);
 #pragma unroll
@@ -1238,7 +1251,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         if constexpr (SPL) {
             constexpr int NREG = TN * TM * 16;
             constexpr int SC1 = 16;  // buffer cache policy: device-scope coherent
-            const int ptile = pt / SK, pslice = pt % SK;
             const rsrc_t pr = make_rsrc(ws + SPLIT_CNT_WORDS, 0x7ffffff0u);
             auto word = [&](int unit, int r) { return (uint32_t)(((unit * NREG + r) * 512 + tid) * 4); };
 #pragma unroll
@@ -1247,7 +1259,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                 for (int j = 0; j < TM; ++j)
 #pragma unroll
                     for (int e = 0; e < 16; ++e)
-                        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)acc[i][j][e], pr, (int)word(pt, (i * TM + j) * 16 + e), 0, SC1);
+                        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)acc[i][j][e], pr, (int)word(ptile * SK + pslice, (i * TM + j) * 16 + e), 0, SC1);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
             __shared__ uint32_t arrived;
             __syncthreads();
