@@ -203,8 +203,15 @@ def capture(fn):
     return graph
 
 
-def time_graph(graph, reps, warmup):
-    """ms per replay over `reps` back-to-back replays, bracketed by synchronizations (HIP events on the stream)."""
+def time_graph(graph, reps, warmup, warm_ms=0.0):
+    """ms per replay over `reps` back-to-back replays, bracketed by synchronizations (HIP events on the stream),
+    after `warmup` untimed replays and, with warm_ms, untimed replays for at least that long first (the matrix-core
+    legs: clocks that dropped while the host prepared the next shape take ~0.1 s of load to come back)."""
+    if warm_ms > 0:
+        t_end = time.perf_counter() + warm_ms * 1e-3
+        while time.perf_counter() < t_end:
+            graph.replay()
+            torch.cuda.synchronize()
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -419,6 +426,15 @@ def chain_results(step, steps, warmup):
     return res
 
 
+# Before each W8A8 timing: 150 ms of untimed replays, then W8A8_WARMUP more. After the host has spent a moment
+# preparing a shape (or after 2 s idle) the first replays of a matrix-core-bound graph ran up to 18 % slower on
+# MI355X (512 x 2048 x 16384: 26.3 -> 22.3 us over ~0.1 s of load, the same memory and graph), which left the
+# first configuration timed per shape at a disadvantage. The HBM-bound decode step showed no such ramp (333.5 us
+# cold and warm).
+W8A8_WARMUP = 4
+W8A8_WARM_MS = 150.0
+
+
 def w8a8_results(reps):
     """Per shape: per-token quantization of the bf16 activations + W8A8 GEMM (bf16 out, bias / GELU where the
     layer has them), each call on its own weights (>= 512 MB of distinct weights rotated). Activations ~N(0,1)
@@ -472,10 +488,10 @@ def w8a8_results(reps):
         _capi.set_tuning("LFM2Q_GEMM_FQ", 1)  # the one-launch kernel (the entry point's default is the pair)
         g_fq = capture(one_launch)
         _capi.set_tuning("LFM2Q_GEMM_FQ", None)
-        t_full, _ = time_graph(g_full, reps, 2)
-        t_gemm, _ = time_graph(g_gemm, reps, 2)
-        t_lib, _ = time_graph(g_lib, reps, 2)
-        t_fq, _ = time_graph(g_fq, reps, 2)
+        t_full, _ = time_graph(g_full, reps, W8A8_WARMUP, W8A8_WARM_MS)
+        t_gemm, _ = time_graph(g_gemm, reps, W8A8_WARMUP, W8A8_WARM_MS)
+        t_lib, _ = time_graph(g_lib, reps, W8A8_WARMUP, W8A8_WARM_MS)
+        t_fq, _ = time_graph(g_fq, reps, W8A8_WARMUP, W8A8_WARM_MS)
         t_fused, _ = time_graph(g_fused, max(3, reps // 4), 1)  # 3-6x slower than the pair: fewer replays
         us_full, us_gemm, us_lib = t_full * 1e3 / ncopy, t_gemm * 1e3 / ncopy, t_lib * 1e3 / ncopy
         us_fused, us_fq = t_fused * 1e3 / ncopy, t_fq * 1e3 / ncopy
@@ -560,13 +576,13 @@ def grouped_results(reps):
         ysT = torch.empty(N // 64, M, device="cuda") if N % 64 == 0 else None
         E.quant_rows(x, xq, sxT)
         g_gemm = capture(lambda: [E.gemm_i8(xq, sxT, W, sw, b, y, gelu) for W in Ws])
-        t_gemm, _ = time_graph(g_gemm, reps, 2)
+        t_gemm, _ = time_graph(g_gemm, reps, W8A8_WARMUP, W8A8_WARM_MS)
         ops = 2.0 * M * N * K
         r = {"name": name, "M": M, "K": K, "N": N, "us_gemm": round(t_gemm * 1e3 / ncopy, 2),
              "tops_gemm": round(ops / (t_gemm * 1e3 / ncopy) / 1e6, 1)}
         if ysT is not None:
             g_q = capture(lambda: [E.gemm_i8_q(xq, sxT, W, sw, b, yq, ysT, gelu) for W in Ws])
-            t_q, _ = time_graph(g_q, reps, 2)
+            t_q, _ = time_graph(g_q, reps, W8A8_WARMUP, W8A8_WARM_MS)
             r["us_gemm_i8_q"] = round(t_q * 1e3 / ncopy, 2)
             r["tops_gemm_i8_q"] = round(ops / (t_q * 1e3 / ncopy) / 1e6, 1)
             del g_q
@@ -706,7 +722,7 @@ def w8a16_results(reps):
         x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
         y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
         gr = capture(lambda: [E.gemm_w8(x, W, sw, b, y, gelu) for W in Ws])
-        t, _ = time_graph(gr, reps, 2)
+        t, _ = time_graph(gr, reps, W8A8_WARMUP, W8A8_WARM_MS)
         us = t * 1e3 / ncopy
         nbytes = N * K + 2 * M * K + 2 * M * N + 4 * N
         out.append({"name": name, "M": M, "K": K, "N": N, "us": round(us, 2),
@@ -878,10 +894,10 @@ GEMM_CONFIGS = [(256, 256, 1), (128, 256, 1), (128, 256, 2), (256, 128, 1), (256
                 (128, 128, 1), (128, 128, 1, 0), (128, 128, 2), (128, 64, 1), (128, 64, 2), (128, 64, 4), (64, 128, 1),
                 (64, 128, 2), (64, 128, 4), (64, 64, 1), (64, 64, 2), (64, 64, 4), (256, 128, 1, 1, 2),
                 (256, 128, 1, 1, 4), (128, 128, 1, 1, 2), (128, 128, 1, 1, 4), (128, 128, 1, 1, 8), (128, 64, 1, 0),
-                (128, 64, 1, 1, 2)]
+                (128, 64, 1, 1, 2), (128, 64, 1, 1, 4), (128, 64, 1, 1, 8), (256, 128, 1, 1, 8)]
 
 
-def gemm_sweep(reps):
+def gemm_sweep(reps, only=None):
     """The per-token W8A8 GEMM on the 13 shapes under every forced (tile, K split) and under the automatic choice,
     timed as in w8a8_results (one call per rotated weight copy in a graph): how far the cost model's pick is from
     the best configuration of each shape."""
@@ -892,6 +908,8 @@ def gemm_sweep(reps):
     knobs = ("LFM2Q_GEMM_BM", "LFM2Q_GEMM_BN", "LFM2Q_GEMM_KSPLIT", "LFM2Q_GEMM_BIGP", "LFM2Q_GEMM_SPLITK")
     out = []
     for M, K, N, bias, gelu, name in W8A8_SHAPES:
+        if only and only not in name:
+            continue
         log(f"sweep {name} {M}x{K}x{N}")
         g = torch.Generator(device="cuda").manual_seed(M + K + N)
         ncopy = max(2, -(-512 * 2 ** 20 // (N * K)))
@@ -915,7 +933,7 @@ def gemm_sweep(reps):
                     for k, v in zip(knobs, cfg):
                         _capi.set_tuning(k, v)
                 graph = capture(fn)
-                t = min(time_graph(graph, reps, 2)[0] for _ in range(2))
+                t = min(time_graph(graph, reps, W8A8_WARMUP, W8A8_WARM_MS)[0] for _ in range(2))
                 label = "auto" if cfg is None else "%dx%d/%d" % cfg[:3] + (
                     "g" if len(cfg) == 4 else "s%d" % cfg[4] if len(cfg) > 4 else "")
                 us[label] = round(t * 1e3 / ncopy, 2)
@@ -944,6 +962,8 @@ def calib_lib():
                                           ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
         L.lfm2q_calib_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
                                               ctypes.c_int, ctypes.c_void_p]
+        L.lfm2q_calib_fold_overlap.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                               ctypes.c_int, ctypes.c_void_p]
         _calib = L
     return _calib
 
@@ -1097,6 +1117,42 @@ def mfma_rate(iters=20000):
     return res
 
 
+def fold_ceiling(iters=2000):
+    """The grouped-64 fold's cost against the matrix work it folds (lib/liblfm2q_calib.so fold_overlap): per round of
+    a 64 x 64 wavefront block, 8 v_mfma_i32_32x32x32_i8 alone, the fold's 64 conversions + 64 FMAs (+ 64 integer
+    adds) alone, and both interleaved, at 1, 2 and 4 wavefronts per SIMD. Both ~= the vector work alone means the SIMD
+    overlaps them and the fold's vector instructions, not the matrix core, bound the grouped GEMM."""
+    L = calib_lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    inp = torch.randint(-100, 100, (512,), dtype=torch.int32, device="cuda")
+    res = {}
+    for per_simd in (1, 2, 4):
+        blocks = cus * per_simd
+        out = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
+        row = {}
+        for mode, name in ((0, "mfma_only"), (1, "fold_only"), (2, "both")):
+            st = torch.cuda.current_stream().cuda_stream
+            assert L.lfm2q_calib_fold_overlap(mode, inp.data_ptr(), out.data_ptr(), blocks, 20, st) == 0
+            torch.cuda.synchronize()
+            best = 1e30
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                assert L.lfm2q_calib_fold_overlap(mode, inp.data_ptr(), out.data_ptr(), blocks, iters, st) == 0
+                e1.record()
+                e1.synchronize()
+                best = min(best, e0.elapsed_time(e1))
+            row[name + "_ns_per_round"] = round(best * 1e6 / iters / per_simd, 1)
+        row["both_over_fold_only"] = round(row["both_ns_per_round"] / row["fold_only_ns_per_round"], 3)
+        row["both_over_sum"] = round(row["both_ns_per_round"] /
+                                     (row["mfma_only_ns_per_round"] + row["fold_only_ns_per_round"]), 3)
+        res[f"{per_simd}_waves_per_simd"] = row
+        log(f"fold overlap, {per_simd} wave(s)/SIMD: {row}")
+    res["workload"] = (f"{cus} x (1, 2, 4) workgroups of 4 wavefronts, {iters} rounds; ns per round per wavefront "
+                       "(divided by the wavefronts sharing a SIMD)")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1125,12 +1181,15 @@ def main():
     ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
     ap.add_argument("--mfma-rate", action="store_true", help="only the sustained int8 matrix-core rate calibration")
     ap.add_argument("--bw-roof", action="store_true", help="only the bare-read bandwidth roof")
+    ap.add_argument("--fold-ceiling", action="store_true",
+                    help="only the grouped fold's MFMA / vector-work overlap calibration")
     ap.add_argument("--dispatch-sweep", action="store_true",
                     help="only the decode linears on every path at batches 1-256 against the dispatch's pick")
     ap.add_argument("--quant-sweep", action="store_true",
                     help="only the activation quantizers under both launch forms on the W8A8 shapes")
     ap.add_argument("--read-branch", action="store_true",
                     help="only the decode step with a concurrent weight-read branch (memory-side-cache staging)")
+    ap.add_argument("--sweep-only", default=None, help="--gemm-sweep: only the shapes whose name contains this")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the per-token W8A8 GEMM under every forced (tile, K split) on the 13 shapes")
     args = ap.parse_args()
@@ -1143,10 +1202,13 @@ def main():
         eager_kind(args.eager_kind, int(args.batches.split(",")[0]), args.steps, args.wfmt)
         return
     if args.gemm_sweep:
-        print(json.dumps({"gemm_sweep": gemm_sweep(max(5, args.steps // 20))}))
+        print(json.dumps({"gemm_sweep": gemm_sweep(max(5, args.steps // 20), args.sweep_only)}))
         return
     if args.mfma_rate:
         print(json.dumps({"mfma_sustained": mfma_rate()}))
+        return
+    if args.fold_ceiling:
+        print(json.dumps({"fold_ceiling": fold_ceiling()}))
         return
     if args.dispatch_sweep:
         print(json.dumps({"dispatch_sweep": dispatch_sweep(max(5, args.steps // 20))}))
