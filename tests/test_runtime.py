@@ -62,8 +62,9 @@ def test_generate_requests():
     assert torch.equal(dec.generate(ids, 0, graph=False), dec.generate(ids, 1, graph=False))  # at least one token
     a = dec.generate(ids, 6, graph=False)
     assert torch.equal(dec.generate(ids, 6, graph=False), a)  # state reset between requests
-    with pytest.raises(ValueError, match="padded"):
-        dec.prefill(ids, 2, attention_mask=torch.tensor([[0, 1, 1, 1]]), graph=False)
+    with pytest.raises(ValueError, match="padded batch takes input_ids"):
+        dec.prefill(ids, 2, attention_mask=torch.tensor([[0, 1, 1, 1]]), graph=False,
+                    inputs_embeds=net.model.embed_tokens(ids).detach())
     with pytest.raises(ValueError, match="at least one"):
         dec.prefill(ids[:, :0], 2, graph=False)
 
@@ -89,6 +90,40 @@ def test_batched_prefill_leaves_the_state_of_the_step():
             for i, buf in getattr(s, name).items():
                 assert rel_err(buf, getattr(s2, name)[i]) < 1e-5, (T, name, i)
         assert torch.equal(fused.generate(ids, 4, graph=False), step.generate(ids, 4, graph=False))
+
+
+@pytest.mark.parametrize("T,pad", [(2, 1), (5, 2), (6, 3), (8, 4)])
+def test_padded_batch_prefill(T, pad):
+    """A left-padded batch (runtime.py:440-460): the prompt runs through transformers' forward with the mask and its
+    cache is copied into the static buffers. Row 0 (no padding) must leave exactly the caches and conv ring of the
+    same prompt prefilled alone through the step -- keys transposed, conv state rows at their ring positions, for
+    prompts shorter than the conv length and at every ring offset -- and generate the same tokens; both rows' first
+    tokens are the argmax of the masked forward (EOS blocked). A mask of all ones takes the ordinary path."""
+    net = tiny_lfm2(seed=21, conv_bias=True)
+    lin = TorchLinears(decode_weights(net))
+    assert net.config.conv_L_cache == 3
+    g = torch.Generator().manual_seed(T * 10 + pad)
+    ids = torch.randint(3, net.config.vocab_size, (2, T), generator=g)
+    mask = torch.ones(2, T, dtype=torch.long)
+    mask[1, :pad] = 0
+    dec = StaticDecoder(net, bucket=16, keep_logits=True, linears=lin)
+    first, st = dec.prefill(ids, 4, attention_mask=mask, graph=False)
+    with torch.no_grad():
+        want = net(input_ids=ids, attention_mask=mask, use_cache=False).logits.float()[:, -1]
+    assert rel_err(dec.last_prefill_logits, want) < 1e-5
+    want[:, dec.eos] = float("-inf")
+    assert torch.equal(first, want.argmax(-1)) and st.ctr.tolist() == [T, 1]
+    alone = StaticDecoder(net, bucket=16, linears=lin)
+    first0, s0 = alone.prefill(ids[:1], 4, graph=False)
+    assert torch.equal(first[:1], first0)
+    for name in ("k", "v", "conv"):
+        for i, buf in getattr(st, name).items():
+            row0 = buf[:, :1] if name == "conv" else buf[:1]
+            assert rel_err(row0, getattr(s0, name)[i]) < 1e-5, (name, i)
+    out = dec.generate(ids, 4, attention_mask=mask, graph=False)
+    assert torch.equal(out[:1], alone.generate(ids[:1], 4, graph=False))
+    full = torch.ones(2, T, dtype=torch.long)
+    assert torch.equal(dec.generate(ids, 3, attention_mask=full, graph=False), dec.generate(ids, 3, graph=False))
 
 
 @pytest.mark.parametrize("fused", [False, True])
