@@ -1117,6 +1117,51 @@ def mfma_rate(iters=20000):
     return res
 
 
+def fq_overhead(reps=10):
+    """The one-launch per-token W8A8 form (lfm2q_gemm_i8_fq with LFM2Q_GEMM_FQ=1) against its parts: quant_rows alone,
+    the GEMM alone, the pair, and the one launch, at 512-10240 rows and N = 8 (one output tile: the time is the
+    quantizing prologue, the wait for every chunk and the leaving count, beside a GEMM that is a few microseconds)
+    and a full N; 20 calls per graph on one weight copy. Also the one launch with the steal bound at 0 (every waiting
+    workgroup quantizes the chunks still open itself)."""
+    from lfm2opt import _capi
+    from lfm2opt.kernels import int8_ext
+
+    E = int8_ext()
+    out = []
+    for M, K, N in ((64, 2048, 8), (512, 2048, 8), (512, 2048, 3072), (512, 8192, 2048), (4096, 8192, 8),
+                    (4096, 8192, 2048), (10240, 4304, 1152)):
+        g = torch.Generator(device="cuda").manual_seed(M + K + N)
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        W = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+        sw = torch.rand(N, device="cuda", generator=g) * 1e-3
+        q = torch.empty(M, K, device="cuda", dtype=torch.int8)
+        s = torch.empty(M, device="cuda")
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        R = 20
+
+        def t(fn):
+            gr = capture(lambda: [fn() for _ in range(R)])
+            ms, _ = time_graph(gr, reps, W8A8_WARMUP, W8A8_WARM_MS)
+            del gr
+            return round(ms * 1e3 / R, 2)
+
+        r = {"M": M, "K": K, "N": N, "us_quant": t(lambda: E.quant_rows(x, q, s)),
+             "us_gemm": t(lambda: E.gemm_i8(q, s, W, sw, None, y, False))}
+        r["us_pair"] = t(lambda: E.gemm_i8_fq(x, q, s, W, sw, None, y, False))  # the entry point's default
+        try:
+            _capi.set_tuning("LFM2Q_GEMM_FQ", 1)
+            r["us_one_launch"] = t(lambda: E.gemm_i8_fq(x, q, s, W, sw, None, y, False))
+            _capi.set_tuning("LFM2Q_GEMM_FQ_WAIT_US", 0)
+            r["us_one_launch_steal_all"] = t(lambda: E.gemm_i8_fq(x, q, s, W, sw, None, y, False))
+        finally:
+            _capi.set_tuning("LFM2Q_GEMM_FQ", None)
+            _capi.set_tuning("LFM2Q_GEMM_FQ_WAIT_US", None)
+        r["one_launch_minus_gemm_us"] = round(r["us_one_launch"] - r["us_gemm"], 2)
+        log(f"fq overhead {M}x{K}x{N}: {r}")
+        out.append(r)
+    return out
+
+
 def fold_ceiling(iters=2000):
     """The grouped-64 fold's cost against the matrix work it folds (lib/liblfm2q_calib.so fold_overlap): per round of
     a 64 x 64 wavefront block, 8 v_mfma_i32_32x32x32_i8 alone, the fold's 64 conversions + 64 FMAs (+ 64 integer
@@ -1181,6 +1226,8 @@ def main():
     ap.add_argument("--wfmt", default="int8", choices=("int8", "int4"), help="decode weights for --eager-kind")
     ap.add_argument("--mfma-rate", action="store_true", help="only the sustained int8 matrix-core rate calibration")
     ap.add_argument("--bw-roof", action="store_true", help="only the bare-read bandwidth roof")
+    ap.add_argument("--fq-overhead", action="store_true",
+                    help="only the one-launch per-token W8A8 form against quant_rows, the GEMM and the pair")
     ap.add_argument("--fold-ceiling", action="store_true",
                     help="only the grouped fold's MFMA / vector-work overlap calibration")
     ap.add_argument("--dispatch-sweep", action="store_true",
@@ -1209,6 +1256,9 @@ def main():
         return
     if args.fold_ceiling:
         print(json.dumps({"fold_ceiling": fold_ceiling()}))
+        return
+    if args.fq_overhead:
+        print(json.dumps({"fq_overhead": fq_overhead()}))
         return
     if args.dispatch_sweep:
         print(json.dumps({"dispatch_sweep": dispatch_sweep(max(5, args.steps // 20))}))
