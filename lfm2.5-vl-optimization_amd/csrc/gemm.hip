@@ -313,7 +313,7 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int grp = KSP == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 8);  // K group of this wavefront
-    const int wave = (tid >> 6) & 3;                                        // wavefront within its group
+    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);         // wavefront within its group
     const int wm = wave >> 1, wn = wave & 1;
     uint8_t(*sX)[BM * BK] = reinterpret_cast<uint8_t(*)[BM * BK]>(smem + grp * RING);
     uint8_t(*sW)[BN * BK] = reinterpret_cast<uint8_t(*)[BN * BK]>(smem + grp * RING + NSTG * BM * BK);
@@ -392,12 +392,13 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         else
 #pragma unroll
             for (int j = 0; j < IX; ++j) {
-                const uint32_t vo = k0 + cx[j] < K ? ox[j] + k0 : 0xfffffff0u;
+                // grouped scales need K % 64 == 0, so each of a stage's chunks is inside its row there
+                const uint32_t vo = GRP || k0 + cx[j] < K ? ox[j] + k0 : 0xfffffff0u;
                 lds_dma16(rx, vo, lds_addr(sX[buf] + 1024 * (4 * j + wave)));
             }
 #pragma unroll
         for (int j = 0; j < IW; ++j) {
-            const uint32_t vo = k0 + cw[j] < K ? ow[j] + k0 : 0xfffffff0u;
+            const uint32_t vo = GRP || k0 + cw[j] < K ? ow[j] + k0 : 0xfffffff0u;
             lds_dma16(rw, vo, lds_addr(sW[buf] + 1024 * (4 * j + wave)));
         }
         if (GRP)  // scales sxT[kt, m0 + 64 wave + lane] (rows past the tile are loaded and not used)
@@ -501,13 +502,93 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         if (p < KT) issue(p);
     if constexpr (GRP && KSP == 1) {
         // the grouped fold is VALU-bound: the stage loop is unrolled by the ring depth so that each copy's slot is a
-        // constant and no per-stage address arithmetic remains beside the fold (same loads, order and results)
+        // constant and no per-stage address arithmetic remains beside the fold (same loads, order and results).
+        // With two or more tiles per wavefront the tiles form two halves and the fold is software-pipelined against
+        // the matrix cores: stage kt runs half 0's MFMAs beside the fold of half 1's stage kt - 1 sums, then half 1's
+        // MFMAs beside the fold of half 0's stage kt sums, each MFMA followed by its share of the fold so that the
+        // SIMD runs both at once. Every accumulator is still folded once per stage, in stage order (half 1's last
+        // stage after the loop; its stage -1 fold adds 0 x 0 to the zero accumulators), so the results are the
+        // unpipelined ones bit for bit. No extra accumulators: half 1's stage kt - 1 sums are read before its stage
+        // kt MFMAs overwrite them.
+        constexpr bool PIPE = TN * TM >= 2;
+        constexpr int NT = TN * TM / 2;  // tiles per half
+        constexpr int VPM = 16;          // a tile's fold (16 conversions + 16 FMAs) per its two MFMAs
+        auto in_half = [](int h, int i, int j) { return (TN >= 2 ? i < TN / 2 : j < TM / 2) == (h == 0); };
+        float sc_prev[TM];
+#pragma unroll
+        for (int j = 0; j < TM; ++j) sc_prev[j] = 0.f;
+        auto mfma_half = [&](int h, const v4i (&wf)[2][TN], const v4i (&xf)[2][TM]) {
+            const v16i zero = {};
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+                        if (in_half(h, i, j))
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[kk][i], xf[kk][j], kk == 0 ? zero : acc[i][j],
+                                                                             0, 0, 0);
+        };
+        auto fold_half = [&](int h, const float (&sc)[TM]) {
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+                    if (in_half(h, i, j))
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            facc[GRP ? i : 0][GRP ? j : 0][e] =
+                                __builtin_fmaf((float)acc[i][j][e], sc[j], facc[GRP ? i : 0][GRP ? j : 0][e]);
+        };
+        // MFMA, then VPM fold instructions, 2 NT times: the pattern the scheduler keeps for one half's MFMAs and the
+        // other half's fold
+        auto interleave = [&]() {
+#pragma unroll
+            for (int r = 0; r < 2 * NT; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+            }
+        };
         auto step = [&](int kt, auto slot_c) {
             constexpr int SLOT = decltype(slot_c)::value;
             wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
             asm volatile("s_barrier" ::: "memory");
             if (kt + NSTG - 1 < KT) issue_in(kt + NSTG - 1, (SLOT + NSTG - 1) % NSTG);
-            compute_in(SLOT);
+            if constexpr (!PIPE) {
+                compute_in(SLOT);
+            } else {
+                const uint8_t *x_s = sX[SLOT], *w_s = sW[SLOT];
+                v4i wf[2][TN], xf[2][TM];
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                    for (int i = 0; i < TN; ++i) wf[kk][i] = *reinterpret_cast<const v4i *>(w_s + fw[kk][i]);
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) xf[kk][j] = *reinterpret_cast<const v4i *>(x_s + fx[kk][j]);
+                }
+                float sc[TM];
+#pragma unroll
+                for (int j = 0; j < TM; ++j) sc[j] = sS[SLOT][wm * WMt + 32 * j + lr];
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_half(0, wf, xf);
+                fold_half(1, sc_prev);
+                interleave();
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_half(1, wf, xf);
+                fold_half(0, sc);
+                interleave();
+                __builtin_amdgcn_sched_barrier(0);
+                // the folds stay in their stage: sunk into a later one, they would keep that stage's int32 sums
+                // alive beside the next stage's (registers the kernel does not have)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(facc[GRP ? i : 0][GRP ? j : 0][e]));
+#pragma unroll
+                for (int j = 0; j < TM; ++j) sc_prev[j] = sc[j];
+            }
         };
         static_assert(NSTG == 3, "grouped ring depth");
         int kt = 0;
@@ -518,6 +599,7 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         }
         if (kt < KT) step(kt, std::integral_constant<int, 0>{});
         if (kt + 1 < KT) step(kt + 1, std::integral_constant<int, 1>{});
+        if constexpr (PIPE) fold_half(1, sc_prev);  // half 1's last stage
     } else
     for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
         // stage kt has landed once at most the loads of the (up to NSTG - 2) stages issued after it are outstanding
