@@ -103,6 +103,24 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     }
 }
 
+// f(kt + S, integral_constant<S>) for S = S0 .. N - 1: a loop body copied once per ring slot, so that each copy's
+// slot is a compile-time constant
+template <int S, int N, class F>
+__device__ __forceinline__ void slot_steps(int kt, F &f) {
+    if constexpr (S < N) {
+        f(kt + S, std::integral_constant<int, S>{});
+        slot_steps<S + 1, N>(kt, f);
+    }
+}
+// the same for the stages below KT only (a ring's last, partial round)
+template <int S, int N, class F>
+__device__ __forceinline__ void slot_steps_below(int kt, int KT, F &f) {
+    if constexpr (S < N) {
+        if (kt + S < KT) f(kt + S, std::integral_constant<int, S>{});
+        slot_steps_below<S + 1, N>(kt, KT, f);
+    }
+}
+
 // Epilogue of one wavefront block: tokens mb .. mb + 32 TM - 1 x weight rows nb .. nb + 32 TN - 1. Per tile (i, j)
 // and run q the lane holds 4 consecutive output columns n .. n + 3 of token row m.
 template <int TM, int TN, int OUT, typename ACC>
@@ -590,15 +608,9 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
                 for (int j = 0; j < TM; ++j) sc_prev[j] = sc[j];
             }
         };
-        static_assert(NSTG == 3, "grouped ring depth");
         int kt = 0;
-        for (; kt + 3 <= KT; kt += 3) {
-            step(kt, std::integral_constant<int, 0>{});
-            step(kt + 1, std::integral_constant<int, 1>{});
-            step(kt + 2, std::integral_constant<int, 2>{});
-        }
-        if (kt < KT) step(kt, std::integral_constant<int, 0>{});
-        if (kt + 1 < KT) step(kt + 1, std::integral_constant<int, 1>{});
+        for (; kt + NSTG <= KT; kt += NSTG) slot_steps<0, NSTG>(kt, step);
+        slot_steps_below<0, NSTG - 1>(kt, KT, step);
         if constexpr (PIPE) fold_half(1, sc_prev);  // half 1's last stage
     } else
     for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
@@ -1673,10 +1685,17 @@ void launch_gemm_grouped(const int8_t *A, const int8_t *B, const float *sxT, con
                          void *Y, float *YsT, int M, int N, int K, hipStream_t st) {
     const TileCfg t = pick_tile(M, N, K, out_q8(OUT) ? TILES_Q8 : TILES_GROUPED);
     const int sh = knob_int(KNOB_GEMM_SWZ, 2);
+    // a 4-stage ring (three stages in flight; 68 KiB for 128 x 128, still two workgroups a CU): equal to the
+    // 3-stage ring where two workgroups share each CU, 24 % faster where the tiles leave one or none (512 x 8192 x
+    // 2048); 6 stages (one workgroup a CU) were 50 % slower on the large shapes. LFM2Q_GEMM_STAGES = 3 keeps 3.
+    const bool three = knob_int(KNOB_GEMM_STAGES, 0) == 3;
     const dim3 grid(((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn));
 #define LFM2Q_GEMM(BM_, BN_)                                                                                        \
     if (t.bm == BM_ && t.bn == BN_) {                                                                                \
-        gemm_i8_kernel<BM_, BN_, OUT, true><<<grid, GT, 0, st>>>(A, B, sxT, sw, bias, Y, M, N, K, sh, YsT);          \
+        if (three)                                                                                                   \
+            gemm_i8_kernel<BM_, BN_, OUT, true, 3><<<grid, GT, 0, st>>>(A, B, sxT, sw, bias, Y, M, N, K, sh, YsT);   \
+        else                                                                                                         \
+            gemm_i8_kernel<BM_, BN_, OUT, true, 4><<<grid, GT, 0, st>>>(A, B, sxT, sw, bias, Y, M, N, K, sh, YsT);   \
         return;                                                                                                      \
     }
     LFM2Q_GEMM(128, 128)

@@ -39,7 +39,7 @@ enum Knob {
     KNOB_GEMM_SWZ,      // XCD band traversal group (log2 of M-tiles per group)
     KNOB_GEMM_BIGP,     // 256 x 256 tiles: 0 = one workgroup per tile instead of the persistent kernel
     KNOB_GEMM_RING,     // 256 x 256 one-workgroup-per-tile ring shape (1282, 644, 645)
-    KNOB_GEMM_STAGES,   // LDS ring depth (3, 6; 2 for the persistent kernels)
+    KNOB_GEMM_STAGES,   // LDS ring depth (3, 6; 2 for the persistent kernels; 3 for the grouped kernel, default 4)
     KNOB_GEMM_SPLITK,   // per-token W8A8 with a workspace: K slices over workgroups (1 = none, 2..8)
     KNOB_CHAIN_WAIT_MS, // GEMV chain: bound of each dependency wait in milliseconds (default 20; 0: at once)
     KNOB_QUANT_WG,      // quant_rows / quant_groups: 1 a workgroup per row, 0 a wavefront per row

@@ -55,12 +55,28 @@ def test_gemm_grouped_vs_oracle(E, M, K, N, bias, gelu):
     assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
 
 
+@pytest.mark.parametrize("stages", ["default", "3"])
 @pytest.mark.parametrize("tile", ["128x128", "128x64", "64x128", "64x64"])
-def test_gemm_grouped_every_tile(E, tile, tune):
+def test_gemm_grouped_every_tile(E, tile, stages, tune):
+    """Each tile on the default 4-stage LDS ring and on the 3-stage one (LFM2Q_GEMM_STAGES = 3)."""
     bm, bn = tile.split("x")
     tune("LFM2Q_GEMM_BM", bm)
     tune("LFM2Q_GEMM_BN", bn)
+    if stages != "default":
+        tune("LFM2Q_GEMM_STAGES", stages)
     xq, sxT, wq, sw, b = operands(5, 200, 576, 264, True)
+    y = run_grouped(E, xq, sxT, wq, sw, b, False)
+    assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
+
+
+@pytest.mark.parametrize("stages", ["default", "3"])
+@pytest.mark.parametrize("K", [64, 128, 192, 448, 704])
+def test_gemm_grouped_ring_rounds(E, K, stages, tune):
+    """K of 1-3 groups (fewer stages than the ring has slots) and of 7 and 11 groups (every partial last round of
+    both ring depths), bit-exact against the oracle."""
+    if stages != "default":
+        tune("LFM2Q_GEMM_STAGES", stages)
+    xq, sxT, wq, sw, b = operands(K + 3, 150, K, 200, True)
     y = run_grouped(E, xq, sxT, wq, sw, b, False)
     assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
 
