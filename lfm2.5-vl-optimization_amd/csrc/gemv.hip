@@ -213,8 +213,11 @@ __global__ __launch_bounds__(256) void gemv_b1p_kernel(const WT *__restrict__ W,
 // rows). CPL > 0: K = 64 PER CPL, all of a wavefront's weight and activation loads are issued before the first
 // dot. CPL == 0: any K % PER == 0, chunks streamed 8 per lane at a time. Per row, the arithmetic is that of the
 // persistent kernel (same chunk order, same PairDot, same fold_sum lane pairing), so either kernel gives the same
-// bits.
-template <typename WT, int R, int CPL, int EPI, bool NORM = false>
+// bits. XS (CPL > 0, not NORM): the workgroup's four wavefronts load the activation row once between them into LDS
+// and each lane reads its chunks' vectors from there (the same values, so the same bits), instead of every
+// wavefront fetching the whole row through L2 -- with one row per wavefront at K = 8192 that is 16 KiB of
+// activations beside 8 KiB of weights per wavefront.
+template <typename WT, int R, int CPL, int EPI, bool NORM = false, bool XS = false>
 __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, const float *__restrict__ scale,
                                                       const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
                                                       int N, int K, int S,
@@ -223,9 +226,12 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, 
     constexpr int PER = D::PER, XL = D::XL;
     constexpr int NROW = EPI == EPI_SWIGLU ? 2 * R : R;
     static_assert(!NORM || CPL > 0, "the normalizing form needs K = 64 PER CPL");
+    static_assert(!XS || (CPL > 0 && !NORM), "the shared-activation form needs K = 64 PER CPL");
     const int lane = threadIdx.x & 63;
     const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * R);
-    if (n0 >= N) return;  // no block-level synchronization in this kernel
+    // XS: every wavefront takes part in the workgroup's activation load and barrier; a wavefront past the last row
+    // reads row N - 1 (the row pointers clamp) and stores nothing
+    if (!XS && n0 >= N) return;  // no block-level synchronization in this kernel
     const char *rp[NROW];
 #pragma unroll
     for (int i = 0; i < NROW; ++i) {
@@ -242,7 +248,31 @@ __global__ __launch_bounds__(256) void gemv_b1_kernel(const WT *__restrict__ W, 
 #pragma unroll
     for (int i = 0; i < NROW; ++i) acc[i] = 0.f;
 
-    if constexpr (CPL > 0) {
+    if constexpr (CPL > 0 && XS) {
+        // the row is NV vectors of 8 bf16; lane l's chunk l + 64 u multiplies vectors XL (l + 64 u) + q
+        constexpr int NV = 64 * CPL * XL, VPT = (NV + 255) / 256;
+        __shared__ v4i xs[NV];
+        v4i w[CPL][NROW], xv[VPT], xr[CPL][XL];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j)
+            if (NV % 256 == 0 || (int)threadIdx.x + 256 * j < NV) xv[j] = ld16(x + (size_t)(threadIdx.x + 256 * j) * 8);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+#pragma unroll
+            for (int i = 0; i < NROW; ++i) w[u][i] = ld_nt16(rp[i] + (size_t)(lane + 64 * u) * 16);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j)
+            if (NV % 256 == 0 || (int)threadIdx.x + 256 * j < NV) xs[threadIdx.x + 256 * j] = xv[j];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+#pragma unroll
+            for (int q = 0; q < XL; ++q) xr[u][q] = xs[XL * (lane + 64 * u) + q];
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+#pragma unroll
+            for (int i = 0; i < NROW; ++i) acc[i] = D::dot(w[u][i], xr[u], acc[i]);
+    } else if constexpr (CPL > 0) {
         v4i w[CPL][NROW], xr[CPL][XL];
         XLoadB1<PER, XL, CPL, NORM> xl;
         xl.issue(x, normw, lane);
@@ -625,7 +655,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 // MI355X) once every wavefront gets at least 64 rows (the 65536-row lm_head is 2.2 us faster one-shot), one-shot
 // kernel below that with R output rows per wavefront:
 // R = 2 from 6144 weight rows (half the wavefronts, each with twice the loads in flight and one reduction for both
-// rows), else 1; the LFM2Q_GEMV_R knob (1, 2 or 4) overrides it where the registers allow. Both need
+// rows) and for the residual GEMVs of K <= 2048, else 1; the LFM2Q_GEMV_R knob (1, 2 or 4) overrides it where the
+// registers allow, LFM2Q_GEMV_XS (0 / 1) the activation staging. Both need
 // K = 64 PER CPL with CPL in {1, 2, 4, 8}; other K take the one-shot kernel's generic loop, where `rows` (1, 2, 4)
 // sets the output rows per wavefront. Per-row arithmetic is the same in all of them.
 template <typename WT, int EPI, bool NORM = false>
@@ -643,21 +674,33 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
     // large GEMVs four rows per wavefront share that work (MI355X runtime decode step 0.708 -> 0.702 ms; four rows
     // for the plain GEMVs too measured 0.3245 -> 0.3387 ms on the GEMV-only step, so only here)
     if (NORM && r1 == 2) r1 = 4;
+    // the activation row staged in LDS once per workgroup (XS) where a wavefront reads at most two weight rows,
+    // i.e. as many activation bytes as weight bytes or more; with it the K = 2048 residual GEMVs take two rows per
+    // wavefront (MI355X, per launch in a graph: o/out_proj 3.96 -> 3.79 us, in_proj 4.54 -> 4.45, w2 5.31 -> 5.10;
+    // w1|w3 + SwiGLU, four weight rows per wavefront, 7.15 -> 7.26 with it, so not there)
+    const int xs_forced = knob_int(KNOB_GEMV_XS, -1);
+    if (!NORM && xs_forced < 0 && EPI == EPI_RESIDUAL && cpl > 0 && cpl <= 2) r1 = 2;
     if (const KnobVal f = knob(KNOB_GEMV_R); f.n) r1 = f.v[0];
+    const bool xs = !NORM && (xs_forced >= 0 ? xs_forced == 1 : (EPI == EPI_SWIGLU ? 2 * r1 : r1) <= 2);
     auto grid = [&](int R) { return dim3((N + 4 * R - 1) / (4 * R)); };
     const dim3 gridp(std::min((N + 3) / 4, blocks_p));
+#define LFM2Q_B1R(R_, C_)                                                                                      \
+    do {                                                                                                       \
+        if (xs)                                                                                                \
+            gemv_b1_kernel<WT, R_, C_, EPI, false, !NORM><<<grid(R_), 256, 0, st>>>(W, scale, x, y, N, K, S);  \
+        else                                                                                                   \
+            gemv_b1_kernel<WT, R_, C_, EPI, NORM><<<grid(R_), 256, 0, st>>>(W, scale, x, y, N, K, S, nw, eps); \
+    } while (0)
 #define LFM2Q_B1(C_)                                                                                        \
     do {                                                                                                    \
         if (persistent)                                                                                     \
             gemv_b1p_kernel<WT, C_, EPI, NORM><<<gridp, 256, 0, st>>>(W, scale, x, y, N, K, S, nw, eps);    \
         else if (r1 == 4 && C_ <= 2)                                                                        \
-            gemv_b1_kernel<WT, C_ <= 2 ? 4 : 1, C_, EPI, NORM><<<grid(4), 256, 0, st>>>(W, scale, x, y, N, K, \
-                                                                                       S, nw, eps);         \
+            LFM2Q_B1R(C_ <= 2 ? 4 : 1, C_);                                                                 \
         else if (r1 == 2 && C_ <= 4)                                                                        \
-            gemv_b1_kernel<WT, C_ <= 4 ? 2 : 1, C_, EPI, NORM><<<grid(2), 256, 0, st>>>(W, scale, x, y, N, K, \
-                                                                                       S, nw, eps);         \
+            LFM2Q_B1R(C_ <= 4 ? 2 : 1, C_);                                                                 \
         else                                                                                                \
-            gemv_b1_kernel<WT, 1, C_, EPI, NORM><<<grid(1), 256, 0, st>>>(W, scale, x, y, N, K, S, nw, eps); \
+            LFM2Q_B1R(1, C_);                                                                               \
     } while (0)
     switch (cpl) {
         case 1: LFM2Q_B1(1); break;
@@ -676,6 +719,7 @@ void launch_b1(const WT *W, const float *scale, const uint16_t *x, uint16_t *y, 
         }
     }
 #undef LFM2Q_B1
+#undef LFM2Q_B1R
 }
 
 // Batch 2 on the VALU kernel when a row is at most 128 chunks (K <= 2048 int8, 1024 bf16), R as for batch 1

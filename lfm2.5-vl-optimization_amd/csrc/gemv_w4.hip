@@ -229,7 +229,11 @@ __global__ __launch_bounds__(256) void gemv_w4_b1_kernel(const uint8_t *__restri
 // chunks' activations in registers (no LDS, no barrier) with the persistent kernel's arithmetic, so each row's bits
 // are the same as gemv_w4_b1_kernel's. Used below 32768 weight rows (measured: the decode step's w1|w3 6.5 -> 5.5
 // us, in_proj 4.1 -> 3.8 us; the 65536-row lm_head stays faster persistent).
-template <int FMT, int CPL, int EPI, int R>
+// XS: the workgroup repacks the activation row once between its four wavefronts -- thread t converts chunks t,
+// t + 256, ... with the same arithmetic into LDS (pair vector j of chunk c at xpv[j][c], its activation sum at
+// xsv[c]) -- and every lane reads its chunks' pairs from there, instead of every wavefront loading the whole row
+// and repacking it (same values, so the same bits).
+template <int FMT, int CPL, int EPI, int R, bool XS = false>
 __global__ __launch_bounds__(256) void gemv_w4_b1o_kernel(const uint8_t *__restrict__ Wq, const void *__restrict__ S,
                                                           const int32_t *__restrict__ Z, const uint16_t *__restrict__ x,
                                                           uint16_t *__restrict__ y, int N, int K, int group, int Sr) {
@@ -237,21 +241,28 @@ __global__ __launch_bounds__(256) void gemv_w4_b1o_kernel(const uint8_t *__restr
     const NibbleMasks nm;
     constexpr int NROW = EPI == EPI_SWIGLU ? 2 : 1;
     constexpr int V = NROW * R;
+    constexpr int NC = 64 * CPL, CPT = XS ? (NC + 255) / 256 : CPL;  // chunks of a row; chunks loaded per thread
     const int lane = threadIdx.x & 63;
     const int n0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * R);
-    if (n0 >= N) return;  // no block-level synchronization in this kernel
+    // XS: every wavefront takes part in the workgroup's activation repack and barrier; one past the last row reads
+    // row N - 1's scales (clamped) through an empty weight range and stores nothing
+    if (!XS && n0 >= N) return;  // no block-level synchronization in this kernel
     const int G = K / group;
     int gl[CPL];
 #pragma unroll
     for (int u = 0; u < CPL; ++u) gl[u] = min(32 * (lane + 64 * u) / group, G - 1);
     const uint32_t rowb = (uint32_t)K / 2;
-    // activations first (cache hits), then every row's weights, scales and zero points
+    // activations first (cache hits), then every row's weights, scales and zero points; the activations of chunk c
+    // are bytes 64 c .. 64 c + 63 of x (chunks past K read zeros through the range)
     const rsrc_t xr = make_rsrc(x, (uint32_t)K * 2u);
-    v4i xd[CPL][4];
+    v4i xd[CPT][4];
 #pragma unroll
-    for (int u = 0; u < CPL; ++u)
+    for (int u = 0; u < CPT; ++u) {
+        const int c = XS ? (int)threadIdx.x + 256 * u : lane + 64 * u;
+        if (!XS || NC % 256 == 0 || c < NC)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xd[u][j] = buf_ld16(xr, (uint32_t)(lane + 64 * u) * 64u + 16u * j);
+            for (int j = 0; j < 4; ++j) xd[u][j] = buf_ld16(xr, (uint32_t)c * 64u + 16u * j);
+    }
     v4i w[R][NROW][CPL];
     uint32_t sr[R][NROW][CPL], zr[R][NROW][CPL];
 #pragma unroll
@@ -272,19 +283,50 @@ __global__ __launch_bounds__(256) void gemv_w4_b1o_kernel(const uint8_t *__restr
     const uint32_t h0 = EPI == EPI_RESIDUAL ? y[ns] : 0u;
     uint32_t xp[CPL][16];
     float xs[CPL];
-#pragma unroll
-    for (int u = 0; u < CPL; ++u) {
+    // chunk pairs (x[p], x[p + 4]) of each 8-value vector and the chunk's activation sum
+    auto repack = [&](const v4i(&d)[4], uint32_t(&pp)[16], float &sum) {
         float t4[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
-            for (int p = 0; p < 4; ++p) xp[u][4 * j + p] = xpair(xd[u][j], p);
+            for (int p = 0; p < 4; ++p) pp[4 * j + p] = xpair(d[j], p);
             float t = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) t += bf2f_lo((uint32_t)xd[u][j][e]) + bf2f_hi((uint32_t)xd[u][j][e]);
+            for (int e = 0; e < 4; ++e) t += bf2f_lo((uint32_t)d[j][e]) + bf2f_hi((uint32_t)d[j][e]);
             t4[j] = t;
         }
-        xs[u] = ((t4[0] + t4[1]) + t4[2]) + t4[3];
+        sum = ((t4[0] + t4[1]) + t4[2]) + t4[3];
+    };
+    if constexpr (XS) {
+        __shared__ v4i xpv[4][NC];
+        __shared__ float xsv[NC];
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+            const int c = (int)threadIdx.x + 256 * u;
+            if (NC % 256 == 0 || c < NC) {
+                uint32_t pp[16];
+                float sum;
+                repack(xd[u], pp, sum);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    xpv[j][c] = v4i{(int)pp[4 * j], (int)pp[4 * j + 1], (int)pp[4 * j + 2], (int)pp[4 * j + 3]};
+                xsv[c] = sum;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const v4i v = xpv[j][lane + 64 * u];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) xp[u][4 * j + p] = (uint32_t)v[p];
+            }
+            xs[u] = xsv[lane + 64 * u];
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) repack(xd[u], xp[u], xs[u]);
     }
     float part[V];
 #pragma unroll
@@ -535,12 +577,28 @@ void launch_w4_b1(const uint8_t *W, const void *S, const int32_t *Z, const uint1
     if (const KnobVal f = knob(KNOB_W4_ONESHOT); f.n) oneshot = f.v[0] != 0;
     if (oneshot && C <= 256) {
         const dim3 go((N + 7) / 8);
+        // the activation repack shared by the workgroup for w1|w3 + SwiGLU and the residual GEMVs of K <= 2048
+        // (LFM2Q_GEMV_XS = 0 / 1 forces it off / on). Measured on MI355X: each decode kind is faster with it in a
+        // graph of that kind alone (w1|w3 5.41 -> 5.17 us, o/out_proj 3.83 -> 3.71, w2 4.62 -> 4.50, qkv 3.79 ->
+        // 3.71), but in the 65-kernel decode step it on qkv / in_proj or on w2 lengthened the step by ~2.5 us while
+        // shortening the kernels (a kernel trace shows the time moving into the gaps between kernels; not
+        // understood), and on w1|w3 or o/out_proj alone it is neutral to -0.4 us
+        const int xs_forced = knob_int(KNOB_GEMV_XS, -1);
+        const bool xs = xs_forced >= 0 ? xs_forced == 1 : EPI == EPI_SWIGLU || (EPI == EPI_RESIDUAL && C <= 64);
+#define LFM2Q_W4O(C_)                                                                                 \
+    do {                                                                                              \
+        if (xs)                                                                                       \
+            gemv_w4_b1o_kernel<FMT, C_, EPI, 2, true><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N); \
+        else                                                                                          \
+            gemv_w4_b1o_kernel<FMT, C_, EPI, 2><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);   \
+    } while (0)
         if (C <= 64)
-            gemv_w4_b1o_kernel<FMT, 1, EPI, 2><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
+            LFM2Q_W4O(1);
         else if (C <= 128)
-            gemv_w4_b1o_kernel<FMT, 2, EPI, 2><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
+            LFM2Q_W4O(2);
         else
-            gemv_w4_b1o_kernel<FMT, 4, EPI, 2><<<go, 256, 0, st>>>(W, S, Z, x, y, N, K, group, N);
+            LFM2Q_W4O(4);
+#undef LFM2Q_W4O
         return;
     }
     if (C <= 64)

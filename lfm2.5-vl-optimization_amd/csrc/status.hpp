@@ -45,6 +45,7 @@ enum Knob {
     KNOB_QUANT_WG,      // quant_rows / quant_groups: 1 a workgroup per row, 0 a wavefront per row
     KNOB_GEMM_FQ,       // gemm_i8_fq: 1 = the one-launch kernel (quantizing prologue); default 0, quant_rows + GEMM
     KNOB_GEMM_FQ_WAIT_US, // gemm_i8_fq prologue: microseconds before a waiting workgroup quantizes open chunks itself
+    KNOB_GEMV_XS,       // batch-1 one-shot GEMV: 1 the activation row staged in LDS per workgroup, 0 per wavefront
     KNOB_COUNT
 };
 struct KnobVal {

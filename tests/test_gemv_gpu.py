@@ -187,6 +187,46 @@ def test_gemv_persistent_matches_one_shot(E, tune, wt, N, K):
                                                           host_bits(x)), what=f"persistent gemv {wt} [{N}x{K}]")
 
 
+@pytest.mark.parametrize("wt,N,K", [("int8", 2048, 8192), ("int8", 2050, 2048), ("int8", 3074, 2048),
+                                    ("int8", 1030, 8192), ("int8", 102, 1024), ("int8", 38, 4096),
+                                    ("bf16", 2054, 2048), ("bf16", 70, 512)])
+@pytest.mark.parametrize("rows", ["1", "2", None])
+def test_gemv_shared_activations_match_per_wavefront(E, tune, wt, N, K, rows):
+    """Batch 1, one-shot kernel: the form whose workgroup stages the activation row in LDS (LFM2Q_GEMV_XS=1) gives
+    the bits of the form where every wavefront loads it (=0), plain, SwiGLU and residual, at 1 / 2 / the automatic
+    rows per wavefront. N not a multiple of the workgroup's rows: the last workgroup's wavefronts past the end take
+    part in the shared load and store nothing."""
+    g = torch.Generator(device="cuda").manual_seed(7 * N + K)
+    if wt == "int8":
+        W = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+        scale = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    else:
+        W = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        scale = None
+    x = torch.randn(1, K, device="cuda", generator=g).to(torch.bfloat16)
+    h0 = (torch.randn(1, N, device="cuda", generator=g) * 4).to(torch.bfloat16)
+    S = N // 2
+    W2, s2 = W[:2 * S].contiguous(), None if scale is None else scale[:2 * S].contiguous()
+    tune("LFM2Q_GEMV_PERSIST", 0)
+    if rows:
+        tune("LFM2Q_GEMV_R", rows)
+    res = {}
+    for mode in ("1", "0"):
+        tune("LFM2Q_GEMV_XS", mode)
+        y = torch.full((1, N), float("nan"), device="cuda", dtype=torch.bfloat16)
+        E.gemv(W, scale, x, y)
+        a = torch.full((1, S), float("nan"), device="cuda", dtype=torch.bfloat16)
+        E.gemv_epi(0, W2, s2, x, a)
+        h = h0.clone()
+        E.gemv_residual(W, scale, x, h)
+        res[mode] = (y, a, h)
+    for u, v in zip(res["1"], res["0"]):
+        assert torch.equal(u.view(torch.int16), v.view(torch.int16))
+    Wn = W.cpu().numpy() if wt == "int8" else host_bits(W)
+    assert_close_bf16(host_bits(res["1"][0]), oracle.gemv(Wn, None if scale is None else scale.cpu().numpy(),
+                                                          host_bits(x)), what=f"shared-x gemv {wt} [{N}x{K}]")
+
+
 @pytest.mark.parametrize("N,K", DECODE_SHAPES)
 @pytest.mark.parametrize("B", [1, 4, 16])
 def test_gemv_w8_decode_shapes(E, N, K, B):

@@ -298,3 +298,27 @@ def test_one_shot_matches_persistent(E, tune, fmt, N, K, group):
         res[mode] = (runs(0), runs(1, n=2 * (N // 2)), runs(2, h0))
     for a, b in zip(res["1"], res["0"]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("N,K,group", [(2048, 2048, 128), (3074, 2048, 128), (1030, 8192, 128), (130, 4096, 128),
+                                       (77, 1024, 64), (38, 3072, 128)])
+def test_one_shot_shared_repack_matches_per_wavefront(E, tune, fmt, N, K, group):
+    """Batch 1, one-shot kernel: the form whose workgroup repacks the activation row once into LDS
+    (LFM2Q_GEMV_XS=1) gives the bits of the form where every wavefront repacks it (=0), plain, SwiGLU and residual,
+    in both weight formats; N not a multiple of the workgroup's 8 rows (wavefronts past the end take part in the
+    repack and store nothing) and K below a wavefront's 2048 CPL weights (chunks past K are zero)."""
+    h0 = oracle.f2bf(np.random.default_rng(N + 1).standard_normal((1, N)).astype(np.float32) * 4)
+    if fmt == 0:
+        Wp, S, x = gen_ref(N + K + 2, 1, N, K, group)
+        runs = lambda epi, h=None, n=N: run_ref(E, Wp[:n], S[:n], x, epi, h)  # noqa: E731
+    else:
+        Wq, S, Z, x = gen_zp(N + K + 3, 1, N, K, group)
+        runs = lambda epi, h=None, n=N: run_zp(E, Wq[:n], S[:n], Z[:n], x, epi, h)  # noqa: E731
+    tune("LFM2Q_W4_ONESHOT", 1)
+    res = {}
+    for mode in ("1", "0"):
+        tune("LFM2Q_GEMV_XS", mode)
+        res[mode] = (runs(0), runs(1, n=2 * (N // 2)), runs(2, h0))
+    for a, b in zip(res["1"], res["0"]):
+        assert np.array_equal(a, b)
