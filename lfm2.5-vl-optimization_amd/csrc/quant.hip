@@ -107,20 +107,12 @@ __global__ __launch_bounds__(256) void quant_kernel(const uint16_t *__restrict__
 // take the wavefronts' maxima through LDS (a maximum does not depend on the order it is taken in); a grouped scale
 // covers 8 consecutive vectors, i.e. 8 consecutive lanes of one wavefront, as in quant_kernel. Each value is quantized
 // by the same quant8 with the same scale and reciprocal, so the bytes and scales equal quant_kernel's.
+// Quantize one row held by a workgroup's 256 threads (thread t: vectors c 256 + t, c < CH; threads past the row hold
+// zeros) into qr and its scale(s), as quant_store does for a row held by one wavefront.
 template <int CH, bool GROUPED>
-__global__ __launch_bounds__(256) void quant_row_wg_kernel(const uint16_t *__restrict__ x, int8_t *__restrict__ q,
-                                                           float *__restrict__ s, int rows, int K) {
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int row = blockIdx.x;
-    const uint16_t *xr = x + (size_t)row * K;
-    int8_t *qr = q + (size_t)row * K;
-    const int C = K / 8;
-    v4i v[CH];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int i = c * 256 + t;
-        v[c] = i < C ? ld_nt16(xr + (size_t)i * 8) : v4i{0, 0, 0, 0};
-    }
+__device__ __forceinline__ void quant_store_wg(const v4i (&v)[CH], int C, int8_t *__restrict__ qr,
+                                               float *__restrict__ s, int row, int rows, int t) {
+    const int lane = t & 63, wave = t >> 6;
     float sc_row = 0.f, rc_row = 0.f;
     if (!GROUPED) {
         __shared__ float wmax[4];
@@ -153,6 +145,22 @@ __global__ __launch_bounds__(256) void quant_row_wg_kernel(const uint16_t *__res
             *reinterpret_cast<int2 *>(qr + (size_t)i * 8) = make_int2(lo, hi);
         }
     }
+}
+
+template <int CH, bool GROUPED>
+__global__ __launch_bounds__(256) void quant_row_wg_kernel(const uint16_t *__restrict__ x, int8_t *__restrict__ q,
+                                                           float *__restrict__ s, int rows, int K) {
+    const int t = threadIdx.x;
+    const int row = blockIdx.x;
+    const uint16_t *xr = x + (size_t)row * K;
+    const int C = K / 8;
+    v4i v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 256 + t;
+        v[c] = i < C ? ld_nt16(xr + (size_t)i * 8) : v4i{0, 0, 0, 0};
+    }
+    quant_store_wg<CH, GROUPED>(v, C, q + (size_t)row * K, s, row, rows, t);
 }
 
 // Per-row scales only, s = max(amax, 1e-8) / 127 -- the s of quant_rows (a maximum does not depend on the order it
@@ -325,6 +333,43 @@ __global__ __launch_bounds__(256) void silu_mul_q_kernel(const uint16_t *__restr
     quant_store<CH, GROUPED>(xv, C, q + (size_t)row * I, s, row, rows, lane);
 }
 
+// silu_mul_q with a workgroup per row (long rows: I = 8192 holds 128 values per lane on one wavefront, 171 VGPRs,
+// two wavefronts per SIMD, each running its loads, ~30 VALU per value of SiLU and quantization, and its stores in
+// turn): thread t holds the vectors c 256 + t (c < CH), every load issued before the first SiLU, then
+// quant_store_wg. Each value is the same expression as silu_mul_q_kernel's and the row / group maxima do not depend
+// on the order they are taken in, so the bytes, scales and bf16 x are the same.
+template <int CH, bool GROUPED>
+__global__ __launch_bounds__(256) void silu_mul_q_wg_kernel(const uint16_t *__restrict__ g, int8_t *__restrict__ q,
+                                                            float *__restrict__ s, uint16_t *__restrict__ xo,
+                                                            int rows, int I) {
+    const int t = threadIdx.x;
+    const int row = blockIdx.x;
+    const int C = I / 8;
+    const uint16_t *gr = g + (size_t)row * 2 * I;
+    v4i av[CH], uv[CH], xv[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 256 + t;
+        if (i < C) {
+            av[c] = ld_nt16(gr + (size_t)i * 8);
+            uv[c] = ld_nt16(gr + I + (size_t)i * 8);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 256 + t;
+        xv[c] = v4i{0, 0, 0, 0};
+        if (i < C) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xv[c][j] = (int)pack_bf16x2(rbf(silu_f32(bf2f_lo((uint32_t)av[c][j]))) * bf2f_lo((uint32_t)uv[c][j]),
+                                      rbf(silu_f32(bf2f_hi((uint32_t)av[c][j]))) * bf2f_hi((uint32_t)uv[c][j]));
+            if (xo) *reinterpret_cast<v4i *>(xo + (size_t)row * I + (size_t)i * 8) = xv[c];
+        }
+    }
+    quant_store_wg<CH, GROUPED>(xv, C, q + (size_t)row * I, s, row, rows, t);
+}
+
 // ------------------------------------------------------------------------------------------------ dispatch
 // CH = vectors of 8 per lane holding a row of `len` values: len <= 512 CH <= 8192
 #define LFM2Q_CH_SWITCH(len, CALL)                                                                                  \
@@ -467,6 +512,25 @@ extern "C" int lfm2q_silu_mul_q(const lfm2q_bf16 *g, int8_t *q, float *s, lfm2q_
                   "silu_mul_q: g, x must be 16-byte and q 8-byte aligned");
     const dim3 grid((rows + 3) / 4);
     const hipStream_t st = (hipStream_t)stream;
+    // a workgroup per row from I = 2048 (MI355X, per call over rotating inputs, wavefront -> workgroup form: 4096 x
+    // 8192 54.7 -> 41.3 us, grouped 46.9 -> 43.6; 2048 x 8192 29.3 -> 25.8; 512 x 8192 22.5 -> 10.1; 10240 x 4304
+    // 57.5 -> 52.9; 4096 x 2048 13.0 -> 12.4, grouped 14.1 -> 12.7); the LFM2Q_QUANT_WG knob forces either form
+    const int fwg = knob_int(KNOB_QUANT_WG, -1);
+    if (fwg >= 0 ? fwg != 0 : I >= 2048) {
+#define LFM2Q_W(CH_)                                                                                                 \
+    if (grouped)                                                                                                     \
+        silu_mul_q_wg_kernel<CH_, true><<<rows, 256, 0, st>>>(g, q, s, x, rows, I);                                  \
+    else                                                                                                             \
+        silu_mul_q_wg_kernel<CH_, false><<<rows, 256, 0, st>>>(g, q, s, x, rows, I)
+        switch ((I / 8 + 255) / 256) {
+            case 1: LFM2Q_W(1); break;
+            case 2: LFM2Q_W(2); break;
+            case 3: LFM2Q_W(3); break;
+            default: LFM2Q_W(4); break;
+        }
+#undef LFM2Q_W
+        return launch_status("silu_mul_q");
+    }
 #define LFM2Q_P(CH_)                                                                                                 \
     if (grouped)                                                                                                     \
         silu_mul_q_kernel<CH_, true><<<grid, 256, 0, st>>>(g, q, s, x, rows, I);                                     \

@@ -165,6 +165,24 @@ def test_silu_mul_q(E, D, rows, I, grouped):
     assert_close_bf16(host_bits(a), oracle.silu_mul(host_bits(g)), what=f"silu_mul_q x {rows}x{I}")
 
 
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("rows,I", [(257, 8192), (5, 8128), (33, 4352), (9, 2048), (70, 1152), (3, 64)])
+def test_silu_mul_q_workgroup_form_matches_wavefront_form(E, tune, rows, I, grouped):
+    """silu_mul_q with a workgroup per row (LFM2Q_QUANT_WG=1, the default from 4096 columns) and with a wavefront per
+    row (=0) give the same int8 rows, scales and bf16 x, per row and per 64-column group, on rows that do not fill
+    the workgroup's last vector set."""
+    g = dev_bf16(rand_bf16(rows + I, (rows, 2 * I), 2.0))
+    out = {}
+    for wg in (1, 0):
+        tune("LFM2Q_QUANT_WG", wg)
+        x = torch.empty(rows, I, device="cuda", dtype=torch.bfloat16)
+        q, s = qs_buffers(rows, I, grouped)
+        E.silu_mul_q(g, q, s, x=x)
+        out[wg] = (q, s, x)
+    for a, b in zip(out[1], out[0]):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))  # bit patterns
+
+
 def test_silu_mul_q_non_grouped_length(E, D):
     """A length that is not a multiple of 64 (4304, the vision MLP width) is accepted per row, and rejected grouped."""
     rows, I = 6, 4304
