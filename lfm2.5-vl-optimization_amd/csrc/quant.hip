@@ -254,6 +254,61 @@ __global__ __launch_bounds__(256) void add_rmsnorm_q_kernel(uint16_t *__restrict
     quant_store<CH, GROUPED>(xv, C, q + (size_t)row * H, s, row, rows, lane);
 }
 
+// add_rmsnorm_q for rows of at most 64 values (the per-head q / k norms of head_dim 64): eight rows per wavefront,
+// lane 8 r + j holding vector j (j < C) of row r, where one wavefront per row would leave 56 of its 64 lanes idle.
+// The sum of squares is folded by the steps of wave_sum that stay within 8 lanes (DPP xor 1, xor 2, half mirror);
+// with one wavefront per row wave_sum's remaining steps add only the zeros of the lanes past the row, so each row
+// gets add_rmsnorm_q_kernel's bits. The row maximum is taken over the row's 8 lanes (order-free), and with H = 64 a
+// row is one 64-column group, so per-row and grouped scales are the same value in the same slot s[row].
+__global__ __launch_bounds__(256) void add_rmsnorm_q_short_kernel(uint16_t *__restrict__ h,
+                                                                  const uint16_t *__restrict__ y,
+                                                                  const uint16_t *__restrict__ w,
+                                                                  int8_t *__restrict__ q, float *__restrict__ s,
+                                                                  uint16_t *__restrict__ xo, int rows, int H,
+                                                                  float eps) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+    const int j = lane & 7, C = H / 8;
+    const bool act = row < rows && j < C;  // every lane takes part in the lane exchanges below
+    const size_t o = (size_t)row * H + (size_t)j * 8;
+    v4i hv = {0, 0, 0, 0}, yv = {0, 0, 0, 0}, wv = {0, 0, 0, 0};
+    if (act) {
+        hv = ld16(h + o);
+        if (y) yv = ld16(y + o);
+        wv = ld16(w + (size_t)j * 8);
+    }
+    if (act && y) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            hv[k] = (int)pack_bf16x2(bf2f_lo((uint32_t)hv[k]) + bf2f_lo((uint32_t)yv[k]),
+                                     bf2f_hi((uint32_t)hv[k]) + bf2f_hi((uint32_t)yv[k]));
+        *reinterpret_cast<v4i *>(h + o) = hv;
+    }
+    float ss = sumsq8(hv, 0.f);
+    ss += dpp<DPP_XOR1>(ss);
+    ss += dpp<DPP_XOR2>(ss);
+    ss += dpp<DPP_HALF_MIRROR>(ss);
+    const float rs = rms_scale(ss, H, eps);
+    v4i xv = {0, 0, 0, 0};
+    if (act) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xv[k] = (int)rms_apply2((uint32_t)wv[k], (uint32_t)hv[k], rs);
+        if (xo) *reinterpret_cast<v4i *>(xo + o) = xv;
+    }
+    float m = absmax8(xv, 0.f);
+    m = fmaxf(m, dpp<DPP_XOR1>(m));
+    m = fmaxf(m, dpp<DPP_XOR2>(m));
+    m = fmaxf(m, dpp<DPP_HALF_MIRROR>(m));
+    const float sc = scale_of(m), rc = 1.f / sc;
+    if (act) {
+        int lo, hi;
+        quant8(xv, sc, rc, lo, hi);
+        *reinterpret_cast<int2 *>(q + o) = make_int2(lo, hi);
+        if (j == 0) s[row] = sc;
+    }
+}
+
 template <int CH, bool GROUPED>
 __global__ __launch_bounds__(256) void add_layernorm_q_kernel(uint16_t *__restrict__ h,
                                                               const uint16_t *__restrict__ y,
@@ -474,6 +529,10 @@ extern "C" int lfm2q_add_rmsnorm_q(lfm2q_bf16 *h, const lfm2q_bf16 *y, const lfm
                   LFM2Q_ERR_ALIGN, "add_rmsnorm_q: h, y, w, x must be 16-byte and q 8-byte aligned");
     const dim3 grid((rows + 3) / 4);
     const hipStream_t st = (hipStream_t)stream;
+    if (H <= 64 && knob_int(KNOB_QUANT_WG, -1) != 0) {  // short rows: eight per wavefront (knob 0: one per wavefront)
+        add_rmsnorm_q_short_kernel<<<(rows + 31) / 32, 256, 0, st>>>(h, y, w, q, s, x, rows, H, eps);
+        return launch_status("add_rmsnorm_q");
+    }
 #define LFM2Q_P(CH_)                                                                                                 \
     if (grouped)                                                                                                     \
         add_rmsnorm_q_kernel<CH_, true><<<grid, 256, 0, st>>>(h, y, w, q, s, x, rows, H, eps);                       \
