@@ -140,14 +140,17 @@ def test_tuning_knobs_set_get_reset():
 
 
 def test_every_documented_knob_exists():
-    """Each knob name the header lists is accepted by lfm2q_get_tuning."""
+    """The header lists exactly the knobs the library defines (status.cpp's name table), and each is accepted by
+    lfm2q_get_tuning."""
     from lfm2opt import _capi
 
     text = HEADER.read_text()
-    listed = re.search(r"Knob names: (.*?)\.\n", text, flags=re.S).group(1)
+    listed = re.search(r"Knob names:\s*(.*?)\.\n", text, flags=re.S).group(1)
     names = []
-    for prefix, body in re.findall(r"(LFM2Q_\w+?)_\{([^}]*)\}", listed):
+    for prefix, body in re.findall(r"(LFM2Q_[A-Z0-9]+?)_\{([^}]*)\}", listed):
         names += [f"{prefix}_{n.strip()}" for n in body.split(",")]
-    assert len(names) >= 17
+    src = (HEADER.parent.parent / "lfm2.5-vl-optimization_amd" / "csrc" / "status.cpp").read_text()
+    table = re.search(r"kKnobNames\[KNOB_COUNT\] = \{(.*?)\};", src, flags=re.S).group(1)
+    assert sorted(names) == sorted(re.findall(r'"(LFM2Q_\w+)"', table))
     for n in names:
         _capi.get_tuning(n)
