@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import oracle
+import rounding_cases
 from conftest import GOLDEN
 from gpu_util import dev, dev_bf16, host_bits, ulp_dist
 
@@ -285,6 +286,26 @@ def test_gemm_every_tile_config(E, bm, bn, stages, ksplit, tune):
         y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
         E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), dev_bf16(b), y, False)
         assert int(ulp_dist(host_bits(y), oracle.gemm_i8_epilogue(acc, sx, sw, b)).max()) == 0, f"bf16 K={K}"
+
+
+@pytest.mark.parametrize("tile,persistent", [pytest.param(None, None, id="auto")]
+                         + [pytest.param(t, p, id=f"{t[0]}x{t[1]}-bigp{p}") for t, p in
+                            [(t, "0") for t in TILES] + [(t, "1") for t in ((256, 256), (256, 128), (128, 128), (128, 64))]])
+def test_gemm_epilogue_rounding_points(E, tile, persistent, tune):
+    """Operands whose bf16 outputs depend on each rounding point of the per-token epilogue (tests/rounding_cases.py,
+    expected bits derived by hand: fl(fl(fl(acc sx) sw) + b), no contraction), on every tile, one tile per
+    workgroup and persistent."""
+    if tile:
+        tune("LFM2Q_GEMM_BM", str(tile[0]))
+        tune("LFM2Q_GEMM_BN", str(tile[1]))
+        tune("LFM2Q_GEMM_BIGP", persistent)
+    xq, sx, wq, sw, b, expect = rounding_cases.per_token_epilogue_case()
+    y = torch.empty(*xq.shape[:1], wq.shape[0], device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(dev(xq), dev(sx), dev(wq), dev(sw), dev_bf16(b), y, False)
+    y = host_bits(y)
+    for (m, n), bits in expect.items():
+        assert int(y[m, n]) == bits, (m, n, hex(int(y[m, n])))
+    assert np.array_equal(y, oracle.gemm_i8(xq, sx, wq, sw, b))
 
 
 @pytest.mark.parametrize("bm,bn", [(256, 256), (256, 128), (128, 128), (128, 64)])

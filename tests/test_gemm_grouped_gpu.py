@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle
+import rounding_cases
 from gpu_util import dev, dev_bf16, host_bits, ulp_dist
 
 pytestmark = pytest.mark.gpu
@@ -67,6 +68,22 @@ def test_gemm_grouped_every_tile(E, tile, stages, tune):
     xq, sxT, wq, sw, b = operands(5, 200, 576, 264, True)
     y = run_grouped(E, xq, sxT, wq, sw, b, False)
     assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
+
+
+@pytest.mark.parametrize("tile", [None, "128x128", "128x64", "64x128", "64x64"])
+def test_gemm_grouped_rounding_points(E, tile, tune):
+    """Operands whose bf16 outputs depend on each rounding point of the fold and the epilogue (tests/rounding_cases.py,
+    expected bits derived by hand: an fma per group in group order into an fp32 accumulator, then fl(fl(facc sw) +
+    b)), on every grouped tile, the pipelined fold of the tiles with several 32 x 32 blocks per wavefront included."""
+    if tile:
+        bm, bn = tile.split("x")
+        tune("LFM2Q_GEMM_BM", bm)
+        tune("LFM2Q_GEMM_BN", bn)
+    xq, sxT, wq, sw, b, expect = rounding_cases.grouped_fold_case()
+    y = host_bits(run_grouped(E, xq, sxT, wq, sw, b, False))
+    for (m, n), bits in expect.items():
+        assert int(y[m, n]) == bits, (m, n, hex(int(y[m, n])))
+    assert np.array_equal(y, oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
 
 
 @pytest.mark.parametrize("stages", ["default", "3"])

@@ -16,6 +16,7 @@ import torch
 import torch.nn.functional as F
 
 import oracle
+import rounding_cases
 
 RNG = np.random.default_rng(1234)
 
@@ -239,6 +240,43 @@ def test_gemm_i8_grouped_close_to_fp64():
     e_ours = np.linalg.norm(oracle.bf2f(y) - r) / np.linalg.norm(r)
     e_round = np.linalg.norm(oracle.bf2f(bf16_bits(torch.from_numpy(r).float())) - r) / np.linalg.norm(r)
     assert e_ours <= 1.05 * e_round + 1e-6
+
+
+def test_gemm_i8_grouped_rounding_points():
+    """The grouped fold's operation sequence on constructed operands whose expected bits are derived by hand
+    (tests/rounding_cases.py): fma per group in group order in an fp32 accumulator, then fl(fl(facc sw) + b). The
+    slips each case is built to catch are evaluated here too, with separately rounded fp32 numpy arithmetic, to show
+    that they give other bits."""
+    xq, sxT, wq, sw, b, expect = rounding_cases.grouped_fold_case()
+    y = oracle.gemm_i8_grouped(xq, sxT, wq, sw, b)
+    for (m, n), bits in expect.items():
+        assert int(y[m, n]) == bits, (m, n, hex(int(y[m, n])))
+    f = np.float32
+    part = [f(int(xq[0, 64 * g])) for g in range(3)]
+    unfused = f(0)
+    for g in range(3):  # product rounded before the add
+        unfused = f(f(part[g] * sxT[g, 0]) + unfused)
+    backwards = f(0)
+    for g in (2, 1, 0):  # fma emulated exactly in fp64: every product here has at most 26 significant bits
+        backwards = f(np.float64(part[g]) * np.float64(sxT[g, 0]) + np.float64(backwards))
+    assert unfused == 0 and backwards == 0 and expect[0, 0] != 0
+    wide = sum(np.float64(int(xq[1, 64 * g])) * np.float64(sxT[g, 1]) for g in range(3))
+    assert wide == 2.0 ** -24 and expect[1, 0] == 0
+    fused = np.float64(f(1 + 2.0 ** -23)) * np.float64(sw[1]) - 1.0  # fma(facc, sw, b): one rounding
+    assert int(bf16_bits(torch.tensor([fused], dtype=torch.float32))[0]) == 0x3380 and expect[2, 1] == 0
+
+
+def test_gemm_i8_epilogue_rounding_points():
+    """Per-token epilogue on constructed operands (tests/rounding_cases.py): y = bf16(fl(fl(fl(acc sx) sw) + b)),
+    with the expected bits derived by hand; fl(sx sw) first, or an fma of the last two operations, gives other bits
+    (shown with separately rounded fp32 numpy arithmetic)."""
+    xq, sx, wq, sw, b, expect = rounding_cases.per_token_epilogue_case()
+    y = oracle.gemm_i8(xq, sx, wq, sw, b)
+    for (m, n), bits in expect.items():
+        assert int(y[m, n]) == bits, (m, n, hex(int(y[m, n])))
+    f = np.float32
+    assert f(f(f(3) * f(sx[0] * sw[0])) - f(3)) == f(3 * 2.0 ** -22)  # the other association: 0x3540
+    assert np.float64(sx[1]) * np.float64(sw[1]) - 1.0 == 2.0 ** -24 - 2.0 ** -47  # what an fma would keep
 
 
 # ------------------------------------------------------------------------------------------------ GEMVs
