@@ -570,7 +570,11 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         auto step = [&](int kt, auto slot_c) {
             constexpr int SLOT = decltype(slot_c)::value;
             wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
-            asm volatile("s_barrier" ::: "memory");
+            // every LDS read of the previous stage completes before the barrier: the loads issued right after it
+            // refill that stage's slot, and a direct-to-LDS write is not ordered after an LDS read issued earlier.
+            // (With one 32 x 32 block per wavefront the compiler sinks a stage's fold, and the wait for its scale
+            // read, below the next barrier; under load the refill then overtook the read.)
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (kt + NSTG - 1 < KT) issue_in(kt + NSTG - 1, (SLOT + NSTG - 1) % NSTG);
             if constexpr (!PIPE) {
                 compute_in(SLOT);

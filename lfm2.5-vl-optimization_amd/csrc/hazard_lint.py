@@ -14,10 +14,17 @@ it, so two gfx9 hazards on the asm's scalar operands are left to the source:
 The compiler does honour both for its own instructions (a buffer load from the builtin after v_readfirstlane gets an
 `s_nop 3` in front of it on gfx950), so every violation found here is in inline asm.
 
+A third rule covers the LDS rings those loads fill: in a kernel with direct-to-LDS loads, no LDS read may still be
+outstanding at an s_barrier (an s_waitcnt lgkmcnt(0) between them on every path). After the barrier another
+wavefront may refill the slot the read targets, and the asynchronous LDS write of a direct-to-LDS load is not
+ordered after an LDS read issued before it. The barriers are inline asm too (a bare s_barrier, so that the loads in
+flight are not drained), and the compiler moves a read's consumers, and with them its wait, across them.
+
 This tool extracts the gfx950 code object from the library, disassembles it (llvm-objdump), builds each kernel's
 control-flow graph (branch targets and fall-through edges) and, for every vector memory instruction, walks back
 along every path counting wait states (one per instruction, N + 1 for s_nop N) until the hazard's window is
-covered. It prints each violation and exits 1 if there is any.
+covered, and for every s_barrier walks back to an LDS-count wait or an LDS read. It prints each violation and exits
+1 if there is any.
 
 Usage: python3 hazard_lint.py path/to/liblfm2q.so   (or a .o / .co / a disassembly text file)
 """
@@ -170,6 +177,44 @@ def check_function(insts):
     return found
 
 
+def _clears_lgkm(mn, ops):
+    return mn == "s_waitcnt" and (re.search(r"lgkmcnt\(0\)", ops) is not None or ops.strip() == "0")
+
+
+def check_barriers(insts):
+    """LDS reads that may still be outstanding at an s_barrier, in a function with direct-to-LDS loads: (barrier
+    addr, read text, read addr). After the barrier another wavefront may refill the slot the read targets, and a
+    direct-to-LDS write is not ordered after an LDS read issued before it; only an s_waitcnt lgkmcnt(0) between the
+    read and the barrier (on every path) makes the read complete first."""
+    if not any(mn.startswith(VMEM_PREFIX) and re.search(r"\blds\b", ops) for _, mn, ops, _ in insts):
+        return []
+    idx = {a: i for i, (a, _, _, _) in enumerate(insts)}
+    preds = [[] for _ in insts]
+    for i, (a, mn, ops, tgt) in enumerate(insts):
+        if tgt is not None and tgt in idx:
+            preds[idx[tgt]].append(i)
+        if mn not in ("s_branch", "s_endpgm", "s_setpc_b64") and i + 1 < len(insts):
+            preds[i + 1].append(i)
+    found = []
+    for i, (a, mn, _, _) in enumerate(insts):
+        if mn != "s_barrier":
+            continue
+        stack, seen = list(preds[i]), set()
+        while stack:
+            j = stack.pop()
+            if j in seen:
+                continue
+            seen.add(j)
+            _, mnj, opsj, _ = insts[j]
+            if _clears_lgkm(mnj, opsj):
+                continue
+            if mnj.startswith("ds_read"):
+                found.append((a, f"{mnj} {opsj}", insts[j][0]))
+                break
+            stack.extend(preds[j])
+    return found
+
+
 def disassemble(path):
     if path.endswith((".s", ".txt", ".dis")):
         with open(path) as f:
@@ -208,6 +253,8 @@ def lint(path):
         nvmem += sum(1 for _, mn, _, _ in insts if mn.startswith(VMEM_PREFIX))
         for v in check_function(insts):
             viol.append((name,) + v)
+        for b, rd, ra in check_barriers(insts):
+            viol.append((name, b, "s_barrier", "LDS read outstanding at a barrier", f"{rd} at 0x{ra:x}", 0))
     return viol, len(funcs), nvmem
 
 

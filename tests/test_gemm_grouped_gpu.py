@@ -98,6 +98,39 @@ def test_gemm_grouped_ring_rounds(E, K, stages, tune):
     assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
 
 
+@pytest.mark.parametrize("stages", ["4", "3"])
+def test_gemm_grouped_64x64_full_occupancy(E, stages, tune):
+    """The 64 x 64 grouped kernel (one 32 x 32 block per wavefront, whose fold the compiler sinks below the next
+    stage's barrier) at 4096 x 2048 x 16384: 16384 workgroups, 4-5 resident per CU, LDS busy. Before its stage
+    barrier waited for the LDS reads, a stage's scale read could be overtaken by the refill of its slot (seen once, at
+    the 3-stage ring); every call must equal the 128 x 128 kernel bit for bit, and sampled rows the oracle."""
+    M, K, N = 4096, 2048, 16384
+    g = torch.Generator(device="cuda").manual_seed(41)
+    wq = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+    sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    xq = torch.empty(M, K, device="cuda", dtype=torch.int8)
+    sxT = torch.empty(K // 64, M, device="cuda")
+    E.quant_rows(x, xq, sxT)
+    tune("LFM2Q_GEMM_BM", "128")
+    tune("LFM2Q_GEMM_BN", "128")
+    ref = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(xq, sxT, wq, sw, None, ref, False)
+    tune("LFM2Q_GEMM_BM", "64")
+    tune("LFM2Q_GEMM_BN", "64")
+    tune("LFM2Q_GEMM_STAGES", stages)
+    y = torch.empty_like(ref)
+    for call in range(4):
+        y.fill_(3.0)
+        E.gemm_i8(xq, sxT, wq, sw, None, y, False)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"call {call}"
+    rows = np.array([0, 1, 63, 64, 2047, 4095])
+    o = oracle.gemm_i8_grouped(xq[rows].cpu().numpy(), sxT[:, rows].cpu().numpy(), wq.cpu().numpy(),
+                               sw.cpu().numpy())
+    assert np.array_equal(host_bits(y[rows]), o)
+
+
 @pytest.mark.skip(reason="a persistent grouped-64 kernel (two groups per 128-byte stage, scale ring in LDS) faulted "
                          "the GPU on this case, its first run with more tiles than workgroups (128 x 64 tiles, "
                          "1100 x 320 x 2056). Cause since found on the CPU: an inline-asm direct-to-LDS load read a "
