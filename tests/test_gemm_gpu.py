@@ -263,6 +263,61 @@ def test_gemm_vision_shapes(E, M, K, N, gelu):
 TILES = [(256, 256), (128, 256), (256, 128), (128, 128), (128, 64), (64, 128), (64, 64)]
 
 
+_PERS = [(256, 256), (256, 128), (128, 128), (128, 64)]
+EVERY_CONFIG = ([dict(BM=bm, BN=bn, STAGES=3, KSPLIT=1, BIGP=0) for bm, bn in TILES]
+                + [dict(BM=bm, BN=bn, STAGES=6, KSPLIT=1, BIGP=0) for bm, bn in TILES if bm + bn <= 384]
+                + [dict(BM=bm, BN=bn, STAGES=3, KSPLIT=2, BIGP=0) for bm, bn in TILES if bm + bn <= 384]
+                + [dict(BM=bm, BN=bn, STAGES=3, KSPLIT=4, BIGP=0) for bm, bn in TILES if bm + bn <= 192]
+                + [dict(BM=bm, BN=bn, BIGP=1, SPLITK=1) for bm, bn in _PERS]
+                + [dict(BM=bm, BN=bn, BIGP=1, SPLITK=sk) for bm, bn in _PERS[1:] for sk in (2, 4)]
+                + [dict(BM=256, BN=256, BIGP=0, RING=r) for r in (1282, 644, 645)])
+
+
+@pytest.mark.parametrize("M,K,N,bias,gelu", [(M, K, N, False, False) for M, K, N in PREFILL]
+                         + [(M, K, N, True, g) for M, K, N, g in VISION])
+def test_gemm_every_configuration_full_shapes(E, M, K, N, bias, gelu, tune):
+    """Every forced per-token configuration (tile, ring depth, in-workgroup K split, persistent or one workgroup per
+    tile, K split across workgroups, the 256 x 256 ring forms) at the full prefill / vision shapes, on quantized
+    ~N(0,1) activations with 0.1 % outliers at 20 sigma, two calls each: bit-identical to the automatic choice, which
+    equals hipBLASLt's exact int32 product (torch._int_mm) followed by the epilogue as separate fp32 torch ops (0 ulp;
+    with GELU the same check runs without it, and the GELU outputs are compared across configurations); and the
+    int32-output kernel of every tile equals torch._int_mm."""
+    g = torch.Generator(device="cuda").manual_seed(M + K + N)
+    wq = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+    sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 1e-3
+    b = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16) if bias else None
+    x = torch.randn(M, K, device="cuda", generator=g)
+    x[torch.rand(M, K, device="cuda", generator=g) < 1e-3] = 20.0
+    xq = torch.empty(M, K, device="cuda", dtype=torch.int8)
+    sx = torch.empty(M, device="cuda")
+    E.quant_rows(x.to(torch.bfloat16), xq, sx)
+    acc = torch._int_mm(xq, wq.t())
+    r = (acc.float() * sx[:, None]) * sw[None, :]
+    if bias:
+        r = r + b.float()[None, :]
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    E.gemm_i8(xq, sx, wq, sw, b, y, False)
+    assert torch.equal(y.view(torch.int16), r.to(torch.bfloat16).view(torch.int16)), "auto vs int32 + epilogue"
+    base = torch.empty_like(y)
+    E.gemm_i8(xq, sx, wq, sw, b, base, gelu)
+    for cfg in EVERY_CONFIG:
+        for k, v in cfg.items():
+            tune("LFM2Q_GEMM_" + k, str(v))
+        for call in range(2):
+            y.fill_(3.0)
+            E.gemm_i8(xq, sx, wq, sw, b, y, gelu)
+            assert torch.equal(y.view(torch.int16), base.view(torch.int16)), (cfg, call)
+        for k in ("BM", "BN", "STAGES", "KSPLIT", "BIGP", "SPLITK", "RING"):
+            tune("LFM2Q_GEMM_" + k, None)
+    c = torch.empty(M, N, device="cuda", dtype=torch.int32)
+    for bm, bn in TILES:
+        tune("LFM2Q_GEMM_BM", str(bm))
+        tune("LFM2Q_GEMM_BN", str(bn))
+        c.fill_(7)
+        E.gemm_i8_i32(xq, wq, c)
+        assert torch.equal(c, acc), (bm, bn)
+
+
 @pytest.mark.parametrize("bm,bn,stages,ksplit", [(bm, bn, 3, 1) for bm, bn in TILES]
                          + [(bm, bn, 6, 1) for bm, bn in TILES if bm + bn <= 384]
                          + [(bm, bn, 3, 2) for bm, bn in TILES if bm + bn <= 384]
