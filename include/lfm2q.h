@@ -48,7 +48,7 @@ const char *lfm2q_version(void);
  * bits between configurations where a kernel's summation order depends on them (the GEMV launch shapes); the W8A8
  * int32 paths are exact whatever the configuration. Knob names:
  * LFM2Q_GEMV_{WPC, PERSIST, R, VALU, MFMA, CHUNK, XS}, LFM2Q_W4_{WPC, ONESHOT, MFMA, B1_MFMA},
- * LFM2Q_GEMM_{BM, BN, KSPLIT, SWZ, BIGP, RING, STAGES, SPLITK, FQ, FQ_WAIT_US}, LFM2Q_CHAIN_{WAIT_MS},
+ * LFM2Q_GEMM_{BM, BN, KSPLIT, SWZ, BIGP, RING, STAGES, SPLITK, FQ, FQ_WAIT_US, GSEQ}, LFM2Q_CHAIN_{WAIT_MS},
  * LFM2Q_QUANT_{WG}.
  * Replaces the reference's implementation switches: set_gemv_impl() (kernels/lfm2_decode.cu:662-663, bound at
  * kernels/lfm2_decode.cpp:166) and the LFM2_INT8_BM tile override (kernels/int8_gemm.cu:691). */

@@ -299,12 +299,14 @@ __device__ __forceinline__ void epilogue(const ACC (&acc)[TN][TM], const float *
 // 64 * 127^2 < 2^24. The group's scales for the tile's rows travel with the operands (one 4-byte direct load per
 // wavefront per stage into a 1 KiB LDS slot) and are read after the stage's barrier. YsT: OUT_Q8 scales.
 // Occupancy hint: two wavefronts per SIMD, except where the 6-stage ring of a large tile (or the bf16 staging ring of
-// a 128-row tile) leaves room for one workgroup
-template <int BM, int BN, int NSTG, bool XBF = false>
-constexpr int gemm_waves_per_eu() { return (NSTG == 6 && BM + BN > 192) || (XBF && BM == 128) ? 1 : 2; }
+// a 128-row tile) leaves room for one workgroup, and three for the grouped kernel's tile-sequential fold (SEQ)
+template <int BM, int BN, int NSTG, bool XBF = false, bool SEQ = false>
+constexpr int gemm_waves_per_eu() {
+    return SEQ ? 3 : (NSTG == 6 && BM + BN > 192) || (XBF && BM == 128) ? 1 : 2;
+}
 
-template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES, int KSP = 1, bool XBF = false>
-__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu<BM, BN, NSTG, XBF>()))) void gemm_i8_kernel(
+template <int BM, int BN, int OUT, bool GRP = false, int NSTG = STAGES, int KSP = 1, bool XBF = false, bool SEQ = false>
+__global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu<BM, BN, NSTG, XBF, SEQ>()))) void gemm_i8_kernel(
     const int8_t *__restrict__ X, const int8_t *__restrict__ W, const float *__restrict__ sx,
     const float *__restrict__ sw, const uint16_t *__restrict__ bias, void *__restrict__ Y, int M, int N, int K,
     int sh, float *__restrict__ YsT = nullptr) {
@@ -324,6 +326,9 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
     // loads (bf16, 128-byte rows) beside the weights, and each wavefront quantizes the rows it loaded itself
     // (quant8, the quantizers' own code) into the int8 slot the direct int8 loads would have filled.
     static_assert(!XBF || (!GRP && KSP == 1 && NSTG == 3 && BM <= 128), "bf16 activations: per-token, 3-stage ring");
+    // SEQ: the grouped fold tile by tile through two int32 accumulator buffers (instead of every tile's), so that the
+    // 128 x 128 kernel fits three wavefronts per SIMD; with a 3-stage ring three workgroups share a CU's LDS
+    static_assert(!SEQ || (GRP && KSP == 1 && (TN * TM) % 2 == 0), "tile-sequential fold: grouped, even tile count");
     constexpr int IXB = XBF ? BM / 32 : 1;  // bf16 activation loads per wavefront per stage (8 rows x 128 bytes)
     constexpr int XBS = XBF ? NSTG * BM * 2 * BK : 0;  // bf16 staging ring
     constexpr int RING = NSTG * (BM + BN) * BK;
@@ -567,6 +572,22 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
                 __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
             }
         };
+        // SEQ: tile t (i = t / TM, j = t % TM) accumulates its stage sum in buffer t % 2, and the previous tile's sum
+        // (the previous stage's last tile for t = 0) is folded from the other buffer right after; the last tile's
+        // fold therefore runs beside the next stage's first MFMAs, and each accumulator is still folded once per
+        // stage in stage order (the stage -1 fold adds 0 x 0), bit-identical to the other forms
+        constexpr int NTS = TN * TM;
+        v16i ab[2] = {};
+        float sc_last = 0.f;
+        auto fold_buf = [&](int t, int buf, float sc) {
+            const int i = t / TM, j = t % TM;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                facc[GRP ? i : 0][GRP ? j : 0][e] = __builtin_fmaf((float)ab[buf][e], sc, facc[GRP ? i : 0][GRP ? j : 0][e]);
+            // pinned here: sunk past the next tile's MFMAs, the fold would keep more than two tiles' sums alive
+#pragma unroll
+            for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(facc[GRP ? i : 0][GRP ? j : 0][e]));
+        };
         auto step = [&](int kt, auto slot_c) {
             constexpr int SLOT = decltype(slot_c)::value;
             wait_stages<IX + IW + IS>(min(NSTG - 2, KT - 1 - kt));
@@ -576,7 +597,34 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
             // read, below the next barrier; under load the refill then overtook the read.)
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (kt + NSTG - 1 < KT) issue_in(kt + NSTG - 1, (SLOT + NSTG - 1) % NSTG);
-            if constexpr (!PIPE) {
+            if constexpr (SEQ) {
+                const uint8_t *x_s = sX[SLOT], *w_s = sW[SLOT];
+                v4i wf[2][TN], xf[2][TM];
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                    for (int i = 0; i < TN; ++i) wf[kk][i] = *reinterpret_cast<const v4i *>(w_s + fw[kk][i]);
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) xf[kk][j] = *reinterpret_cast<const v4i *>(x_s + fx[kk][j]);
+                }
+                float sc[TM];
+#pragma unroll
+                for (int j = 0; j < TM; ++j) sc[j] = sS[SLOT][wm * WMt + 32 * j + lr];
+                __builtin_amdgcn_sched_barrier(0);
+                const v16i zero = {};
+#pragma unroll
+                for (int t = 0; t < NTS; ++t) {
+                    const int i = t / TM, j = t % TM, buf = t & 1;
+                    ab[buf] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[0][i], xf[0][j], zero, 0, 0, 0);
+                    ab[buf] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[1][i], xf[1][j], ab[buf], 0, 0, 0);
+                    if (t == 0)
+                        fold_buf(NTS - 1, 1, sc_last);  // the previous stage's last tile
+                    else
+                        fold_buf(t - 1, buf ^ 1, sc[(t - 1) % TM]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                sc_last = sc[(NTS - 1) % TM];
+            } else if constexpr (!PIPE) {
                 compute_in(SLOT);
             } else {
                 const uint8_t *x_s = sX[SLOT], *w_s = sW[SLOT];
@@ -615,7 +663,10 @@ __global__ __launch_bounds__(GT * KSP) __attribute__((amdgpu_waves_per_eu(gemm_w
         int kt = 0;
         for (; kt + NSTG <= KT; kt += NSTG) slot_steps<0, NSTG>(kt, step);
         slot_steps_below<0, NSTG - 1>(kt, KT, step);
-        if constexpr (PIPE) fold_half(1, sc_prev);  // half 1's last stage
+        if constexpr (SEQ)
+            fold_buf(NTS - 1, 1, sc_last);  // the last stage's last tile
+        else if constexpr (PIPE)
+            fold_half(1, sc_prev);  // half 1's last stage
     } else
     for (int kt = 0; kt < (KSP == 1 ? KT : KTg); ++kt) {
         // stage kt has landed once at most the loads of the (up to NSTG - 2) stages issued after it are outstanding
@@ -1701,6 +1752,17 @@ void launch_gemm_grouped(const int8_t *A, const int8_t *B, const float *sxT, con
         else                                                                                                         \
             gemm_i8_kernel<BM_, BN_, OUT, true, 4><<<grid, GT, 0, st>>>(A, B, sxT, sw, bias, Y, M, N, K, sh, YsT);   \
         return;                                                                                                      \
+    }
+    // 128 x 128 tiles, more than two a CU: the tile-sequential fold (158 VGPRs: three wavefronts a SIMD) on a 3-stage
+    // ring (51 KiB: three workgroups a CU), against two of each for the pipelined fold. Measured on MI355X: 5-7 %
+    // faster from 720 tiles (4096 x 2048 x 16384 240.3 -> 224.0 us, the vision shapes 5-7 %), neutral to 3 % slower
+    // at 256-512 tiles, where every tile is resident at two a CU. LFM2Q_GEMM_GSEQ = 0 / 1 forces it off / on
+    // (LFM2Q_GEMM_STAGES = 3 alone keeps the pipelined fold on its 3-stage ring).
+    const int gseq = knob_int(KNOB_GEMM_GSEQ, -1);
+    if (t.bm == 128 && t.bn == 128 && (gseq >= 0 ? gseq == 1 : !three && (long)grid.x > 2L * device_cus())) {
+        gemm_i8_kernel<128, 128, OUT, true, 3, 1, false, true><<<grid, GT, 0, st>>>(A, B, sxT, sw, bias, Y, M, N, K, sh,
+                                                                                   YsT);
+        return;
     }
     LFM2Q_GEMM(128, 128)
     LFM2Q_GEMM(64, 128)

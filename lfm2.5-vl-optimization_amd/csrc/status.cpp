@@ -45,7 +45,7 @@ const char *const kKnobNames[KNOB_COUNT] = {
     "LFM2Q_GEMV_CHUNK", "LFM2Q_W4_WPC",      "LFM2Q_W4_ONESHOT", "LFM2Q_W4_MFMA",    "LFM2Q_W4_B1_MFMA",
     "LFM2Q_GEMM_BM",   "LFM2Q_GEMM_BN",      "LFM2Q_GEMM_KSPLIT", "LFM2Q_GEMM_SWZ",   "LFM2Q_GEMM_BIGP",
     "LFM2Q_GEMM_RING", "LFM2Q_GEMM_STAGES", "LFM2Q_GEMM_SPLITK", "LFM2Q_CHAIN_WAIT_MS",
-    "LFM2Q_QUANT_WG", "LFM2Q_GEMM_FQ", "LFM2Q_GEMM_FQ_WAIT_US", "LFM2Q_GEMV_XS",
+    "LFM2Q_QUANT_WG", "LFM2Q_GEMM_FQ", "LFM2Q_GEMM_FQ_WAIT_US", "LFM2Q_GEMV_XS", "LFM2Q_GEMM_GSEQ",
 };
 
 // A knob word: bits 0-3 the count n, value i (signed, |v| < 16384) in bits 4 + 15 i .. 18 + 15 i.

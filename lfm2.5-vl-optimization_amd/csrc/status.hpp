@@ -46,6 +46,7 @@ enum Knob {
     KNOB_GEMM_FQ,       // gemm_i8_fq: 1 = the one-launch kernel (quantizing prologue); default 0, quant_rows + GEMM
     KNOB_GEMM_FQ_WAIT_US, // gemm_i8_fq prologue: microseconds before a waiting workgroup quantizes open chunks itself
     KNOB_GEMV_XS,       // batch-1 one-shot GEMV: 1 the activation row staged in LDS per workgroup, 0 per wavefront
+    KNOB_GEMM_GSEQ,     // grouped 128 x 128 W8A8: 1 tile-sequential fold (three workgroups a CU), 0 pipelined fold
     KNOB_COUNT
 };
 struct KnobVal {

@@ -57,15 +57,24 @@ def test_gemm_grouped_vs_oracle(E, M, K, N, bias, gelu):
     assert u <= (1 if gelu else 0), f"{u} bf16 ulp"
 
 
-@pytest.mark.parametrize("stages", ["default", "3"])
-@pytest.mark.parametrize("tile", ["128x128", "128x64", "64x128", "64x64"])
+def force_form(tune, stages):
+    """stages: "default" (the automatic form), "3" (the 3-stage ring, pipelined fold), "pipe" / "seq" (the 128 x 128
+    kernel's pipelined / tile-sequential fold, LFM2Q_GEMM_GSEQ = 0 / 1)."""
+    if stages == "3":
+        tune("LFM2Q_GEMM_STAGES", "3")
+    elif stages in ("pipe", "seq"):
+        tune("LFM2Q_GEMM_GSEQ", "1" if stages == "seq" else "0")
+
+
+@pytest.mark.parametrize("tile,stages", [(t, st) for t in ("128x128", "128x64", "64x128", "64x64")
+                                         for st in ("default", "3")] + [("128x128", "seq")])
 def test_gemm_grouped_every_tile(E, tile, stages, tune):
-    """Each tile on the default 4-stage LDS ring and on the 3-stage one (LFM2Q_GEMM_STAGES = 3)."""
+    """Each tile on the default 4-stage LDS ring and on the 3-stage one (LFM2Q_GEMM_STAGES = 3), and the 128 x 128
+    kernel's tile-sequential fold (LFM2Q_GEMM_GSEQ = 1)."""
     bm, bn = tile.split("x")
     tune("LFM2Q_GEMM_BM", bm)
     tune("LFM2Q_GEMM_BN", bn)
-    if stages != "default":
-        tune("LFM2Q_GEMM_STAGES", stages)
+    force_form(tune, stages)
     xq, sxT, wq, sw, b = operands(5, 200, 576, 264, True)
     y = run_grouped(E, xq, sxT, wq, sw, b, False)
     assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
@@ -87,13 +96,16 @@ def test_gemm_grouped_rounding_points(E, tile, tune):
     assert np.array_equal(y, oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
 
 
-@pytest.mark.parametrize("stages", ["default", "3"])
+@pytest.mark.parametrize("stages", ["default", "3", "seq"])
 @pytest.mark.parametrize("K", [64, 128, 192, 448, 704])
 def test_gemm_grouped_ring_rounds(E, K, stages, tune):
     """K of 1-3 groups (fewer stages than the ring has slots) and of 7 and 11 groups (every partial last round of
-    both ring depths), bit-exact against the oracle."""
-    if stages != "default":
-        tune("LFM2Q_GEMM_STAGES", stages)
+    both ring depths; "seq": the 128 x 128 tile-sequential fold, whose first fold is the stage -1 one and whose last
+    tile is folded after the loop), bit-exact against the oracle."""
+    if stages == "seq":
+        tune("LFM2Q_GEMM_BM", "128")
+        tune("LFM2Q_GEMM_BN", "128")
+    force_form(tune, stages)
     xq, sxT, wq, sw, b = operands(K + 3, 150, K, 200, True)
     y = run_grouped(E, xq, sxT, wq, sw, b, False)
     assert np.array_equal(host_bits(y), oracle.gemm_i8_grouped(xq, sxT, wq, sw, b))
@@ -106,7 +118,8 @@ GROUPED_FULL = ([(M, K, N, False, False) for M in (512, 2048, 4096) for K, N in 
 
 @pytest.mark.parametrize("M,K,N,bias,gelu", GROUPED_FULL)
 def test_gemm_grouped_every_configuration_full_shapes(E, M, K, N, bias, gelu, tune):
-    """Every grouped tile on both ring depths at the full prefill / vision shapes whose K is a multiple of 64, on
+    """Every grouped tile on both ring depths (and the 128 x 128 kernel's pipelined and tile-sequential folds, each
+    forced) at the full prefill / vision shapes whose K is a multiple of 64, on
     grouped-quantized ~N(0,1) activations with 0.1 % outliers at 20 sigma, two calls each: bit-identical to the
     automatic choice, whose sampled rows equal the oracle's fold (<= 1 ulp with GELU)."""
     g = torch.Generator(device="cuda").manual_seed(M + K + N + 5)
@@ -139,8 +152,10 @@ def test_gemm_grouped_every_configuration_full_shapes(E, M, K, N, bias, gelu, tu
         bm, bn = tile.split("x")
         tune("LFM2Q_GEMM_BM", bm)
         tune("LFM2Q_GEMM_BN", bn)
-        for stages in ("4", "3"):
-            tune("LFM2Q_GEMM_STAGES", stages)
+        for stages in ("default", "3") + (("pipe", "seq") if tile == "128x128" else ()):
+            tune("LFM2Q_GEMM_STAGES", None)
+            tune("LFM2Q_GEMM_GSEQ", None)
+            force_form(tune, stages)
             for call in range(2):
                 y.fill_(3.0)
                 E.gemm_i8(xq, sxT, wq, sw, b, y, gelu)
@@ -236,9 +251,16 @@ def test_gemm_grouped_full_shape_error_rule(E, M, K, N):
     assert np.array_equal(host_bits(y[rows]), ref)
 
 
+@pytest.mark.parametrize("form", ["default", "seq"])
 @pytest.mark.parametrize("M,K,N,bias,gelu", [(300, 1152, 1152, True, False), (65, 2048, 3072, False, True),
                                              (17, 256, 192, True, True), (129, 4352, 4352, False, False)])
-def test_gemm_i8_q_equals_gemm_then_quant_groups(E, M, K, N, bias, gelu):
+def test_gemm_i8_q_equals_gemm_then_quant_groups(E, M, K, N, bias, gelu, form, tune):
+    """The INT8-output form (its row maxima, scales and bytes) against gemm_i8 + grouped quant_rows, on the automatic
+    kernel and on the 128 x 128 tile-sequential fold."""
+    if form == "seq":
+        tune("LFM2Q_GEMM_BM", "128")
+        tune("LFM2Q_GEMM_BN", "128")
+        tune("LFM2Q_GEMM_GSEQ", "1")
     xq, sxT, wq, sw, b = operands(M * 3 + N, M, K, N, bias)
     y = run_grouped(E, xq, sxT, wq, sw, b, gelu)
     rq = torch.empty(M, N, device="cuda", dtype=torch.int8)
